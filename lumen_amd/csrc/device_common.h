@@ -1,0 +1,75 @@
+// Device helpers shared by the built-in kernels and the generated loop kernels: storage types, exact
+// conversions and wavefront reductions for gfx950 (wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nhipk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// 16-bit floats are stored as their bit patterns.
+struct bf16_t {
+    uint16_t bits;
+};
+struct f16_t {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// float32 -> bfloat16, round to nearest even; NaN stays a quiet NaN of its sign. A float32 value is the
+// exact value here, so this is the reference's one correct rounding (lumen/tensor/dtype.rs:215-239).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+    _Float16 h = __builtin_bit_cast(_Float16, b);
+    return float(h);
+}
+
+// float32 -> float16 by the hardware conversion (v_cvt_f16_f32: round to nearest even, overflow to inf).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    _Float16 h = _Float16(f);
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+template <typename T>
+struct Storage;
+template <>
+struct Storage<float> {
+    __device__ static float load(const float *p) { return *p; }
+    __device__ static void store(float *p, float v) { *p = v; }
+};
+
+__device__ __forceinline__ float load_as_f32(const float *p) { return *p; }
+__device__ __forceinline__ float load_as_f32(const bf16_t *p) { return bf16_to_f32(p->bits); }
+__device__ __forceinline__ float load_as_f32(const f16_t *p) { return f16_to_f32(p->bits); }
+__device__ __forceinline__ void store_f32_as(float *p, float v) { *p = v; }
+__device__ __forceinline__ void store_f32_as(bf16_t *p, float v) { p->bits = f32_to_bf16(v); }
+__device__ __forceinline__ void store_f32_as(f16_t *p, float v) { p->bits = f32_to_f16(v); }
+
+// Sum over the 64 lanes of a wavefront (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Maximum over the 64 lanes of a wavefront, NaN-propagating as the reference's fmax.
+__device__ __forceinline__ float nan_max(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace nhipk

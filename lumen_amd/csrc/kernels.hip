@@ -1,0 +1,215 @@
+// Built-in kernels of libnhip and their C entry points: nhip_gemm (dot_general), the flash attention
+// forward and backward, and the fill used by plans (a kernel, not hipMemsetAsync, so a captured plan
+// replays it correctly).
+#include <cstring>
+
+#include "attention.h"
+#include "gemm.h"
+#include "nhip_internal.h"
+
+using namespace nhipk;
+
+namespace nhip {
+namespace {
+
+struct TileConfig {
+    int bm, bn, bk, wm, wn;
+};
+
+// Candidates for bf16/f16 GEMMs, largest first (lumen/codegen/dot_general/cuda/mod.rs:430-633 keeps a
+// similar list for SM80; these are sized for 160 KiB of LDS and wave64).
+constexpr TileConfig kConfigs[] = {
+    {256, 256, 64, 2, 2},
+    {256, 128, 64, 2, 2},
+    {128, 128, 64, 2, 2},
+    {128, 64, 64, 2, 2},
+    {64, 64, 64, 2, 2},
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+GemmShape shape_of(const nhip_gemm_desc *d) {
+    GemmShape s;
+    std::memset(&s, 0, sizeof(s));
+    s.m = d->m;
+    s.n = d->n;
+    s.k = d->k;
+    s.nbatch = d->nbatch;
+    for (int i = 0; i < 3; ++i) {
+        s.batch[i] = d->batch[i];
+        s.a_batch[i] = d->a_batch[i];
+        s.b_batch[i] = d->b_batch[i];
+        s.d_batch[i] = d->d_batch[i];
+    }
+    s.a_m = d->a_m;
+    s.a_k = d->a_k;
+    s.b_k = d->b_k;
+    s.b_n = d->b_n;
+    s.d_m = d->d_m;
+    s.d_n = d->d_n;
+    return s;
+}
+
+int64_t batch_count(const nhip_gemm_desc *d) {
+    int64_t z = 1;
+    for (int i = 0; i < d->nbatch; ++i) z *= d->batch[i];
+    return z;
+}
+
+// The default tile for a shape: the largest whose tile count fills the 256 CUs at least once.
+int default_config(const nhip_gemm_desc *d) {
+    int64_t z = batch_count(d);
+    for (int c = 0; c < kNumConfigs; ++c) {
+        int64_t tiles = ((d->m + kConfigs[c].bm - 1) / kConfigs[c].bm) * ((d->n + kConfigs[c].bn - 1) / kConfigs[c].bn) * z;
+        if (tiles >= 256) return c;
+    }
+    return kNumConfigs - 1;
+}
+
+template <typename TD>
+int launch_exact(hipStream_t st, GemmShape s, const nhip_gemm_desc *d, const void *a, const void *b, void *out) {
+    s.tiles_m = int((s.m + 63) / 64);
+    s.tiles_n = int((s.n + 63) / 64);
+    dim3 grid(s.tiles_m * s.tiles_n, unsigned(batch_count(d)));
+    StoreEpilogue<TD> epi{static_cast<TD *>(out)};
+    if (d->a_dtype == NHIP_F32)
+        hipLaunchKernelGGL((gemm_exact<float, float, StoreEpilogue<TD>>), grid, dim3(256), 0, st,
+                           s, static_cast<const float *>(a), static_cast<const float *>(b), epi);
+    else if (d->a_dtype == NHIP_BF16)
+        hipLaunchKernelGGL((gemm_exact<bf16_t, bf16_t, StoreEpilogue<TD>>), grid, dim3(256), 0, st,
+                           s, static_cast<const bf16_t *>(a), static_cast<const bf16_t *>(b), epi);
+    else
+        hipLaunchKernelGGL((gemm_exact<f16_t, f16_t, StoreEpilogue<TD>>), grid, dim3(256), 0, st,
+                           s, static_cast<const f16_t *>(a), static_cast<const f16_t *>(b), epi);
+    return check(hipGetLastError(), "gemm_exact launch");
+}
+
+template <bool F16, int BM, int BN, int BK, int WM, int WN, typename TD>
+int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out) {
+    s.tiles_m = int((s.m + BM - 1) / BM);
+    s.tiles_n = int((s.n + BN - 1) / BN);
+    constexpr int lds = gemm_mfma_lds_bytes<BM, BN, BK>();
+    auto kern = gemm_mfma<F16, BM, BN, BK, WM, WN, StoreEpilogue<TD>>;
+    static bool attr = false;
+    if (!attr) {
+        if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                  "hipFuncSetAttribute"))
+            return 1;
+        attr = true;
+    }
+    dim3 grid(s.tiles_m * s.tiles_n, unsigned(z));
+    hipLaunchKernelGGL(kern, grid, dim3(WM * WN * 64), lds, st, s, static_cast<const uint16_t *>(a),
+                       static_cast<const uint16_t *>(b), StoreEpilogue<TD>{static_cast<TD *>(out)});
+    return check(hipGetLastError(), "gemm_mfma launch");
+}
+
+template <bool F16, typename TD>
+int launch_mfma(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out) {
+    switch (cfg) {
+        case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 2, TD>(st, s, z, a, b, out);
+        case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, TD>(st, s, z, a, b, out);
+        case 2: return launch_mfma_cfg<F16, 128, 128, 64, 2, 2, TD>(st, s, z, a, b, out);
+        case 3: return launch_mfma_cfg<F16, 128, 64, 64, 2, 2, TD>(st, s, z, a, b, out);
+        default: return launch_mfma_cfg<F16, 64, 64, 64, 2, 2, TD>(st, s, z, a, b, out);
+    }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Whether the MFMA kernel reads these operands: k-contiguous rows starting on 16-byte boundaries.
+bool mfma_ready(const nhip_gemm_desc *d, const void *a, const void *b) {
+    if (d->a_dtype != d->b_dtype || d->a_dtype == NHIP_F32) return false;
+    if (d->a_k != 1 || d->b_k != 1 || d->k % 8 || d->a_m % 8 || d->b_n % 8) return false;
+    if (!aligned16(a) || !aligned16(b)) return false;
+    for (int i = 0; i < d->nbatch; ++i)
+        if (d->a_batch[i] % 8 || d->b_batch[i] % 8) return false;
+    return true;
+}
+
+}  // namespace
+
+int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *b, void *out) {
+    if (d->nbatch < 0 || d->nbatch > 3) return fail("nhip_gemm: at most 3 batch axes");
+    if ((d->a_dtype == NHIP_F32) != (d->b_dtype == NHIP_F32))
+        return fail("nhip_gemm: operands must both be float32 or both 16-bit");
+    GemmShape s = shape_of(d);
+    int64_t z = batch_count(d);
+    if (d->m == 0 || d->n == 0 || z == 0) return 0;
+    if (z > 65535) return fail("nhip_gemm: more than 65535 batches");
+    if (d->k > 0 && mfma_ready(d, a, b)) {  // k == 0 folds nothing: the exact kernel writes zeros
+        int cfg = d->config < 0 ? default_config(d) : d->config;
+        if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
+        bool f16 = d->a_dtype == NHIP_F16;
+        switch (d->d_dtype) {
+            case NHIP_F32:
+                return f16 ? launch_mfma<true, float>(st, cfg, s, z, a, b, out) : launch_mfma<false, float>(st, cfg, s, z, a, b, out);
+            case NHIP_BF16:
+                return f16 ? launch_mfma<true, bf16_t>(st, cfg, s, z, a, b, out) : launch_mfma<false, bf16_t>(st, cfg, s, z, a, b, out);
+            default:
+                return f16 ? launch_mfma<true, f16_t>(st, cfg, s, z, a, b, out) : launch_mfma<false, f16_t>(st, cfg, s, z, a, b, out);
+        }
+    }
+    switch (d->d_dtype) {
+        case NHIP_F32: return launch_exact<float>(st, s, d, a, b, out);
+        case NHIP_BF16: return launch_exact<bf16_t>(st, s, d, a, b, out);
+        default: return launch_exact<f16_t>(st, s, d, a, b, out);
+    }
+}
+
+__global__ void fill_kernel(unsigned char *dst, size_t n, unsigned char v) {
+    size_t i = (size_t(blockIdx.x) * blockDim.x + threadIdx.x) * 16;
+    size_t stride = size_t(gridDim.x) * blockDim.x * 16;
+    uint32_t w = v * 0x01010101u;
+    for (; i < n; i += stride) {
+        if (i + 16 <= n && (reinterpret_cast<uintptr_t>(dst + i) & 15) == 0) {
+            *reinterpret_cast<uint4 *>(dst + i) = make_uint4(w, w, w, w);
+        } else {
+            for (size_t j = i; j < n && j < i + 16; ++j) dst[j] = v;
+        }
+    }
+}
+
+int fill_on(hipStream_t st, void *dst, size_t bytes, unsigned char value) {
+    if (!bytes) return 0;
+    size_t blocks = (bytes + 256 * 16 - 1) / (256 * 16);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, static_cast<unsigned char *>(dst), bytes,
+                       value);
+    return check(hipGetLastError(), "fill launch");
+}
+
+}  // namespace nhip
+
+using namespace nhip;
+
+extern "C" {
+
+int nhip_gemm(const nhip_gemm_desc *desc, const void *a, const void *b, void *d) {
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    return gemm_on(s, desc, a, b, d);
+}
+
+int nhip_gemm_config_count(int *count) {
+    *count = kNumConfigs;
+    return 0;
+}
+
+int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, void *o, float *lse) {
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    return flash_fwd_on(s, desc, q, k, v, o, lse);
+}
+
+int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
+                   const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace) {
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    return flash_bwd_on(s, desc, q, k, v, o, d_o, lse, dq, dk, dv, workspace);
+}
+
+int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes) {
+    *bytes = flash_bwd_workspace_bytes(desc);
+    return 0;
+}
+
+}  // extern "C"
