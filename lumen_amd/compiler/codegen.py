@@ -1,0 +1,825 @@
+"""HIP source for fused loop kernels (the hip counterpart of ``lumen/codegen/elementwise/cuda/mod.rs``,
+``codegen/row/triton.rs``, ``codegen/reduction/triton.rs`` and the emitter ``codegen/emitter/cuda.rs``).
+
+Every value of a kernel is evaluated at an index derived from the kernel's iteration index by walking its
+producers (layout ops are index maps, never copies). Each primitive's result is rounded to its dtype exactly
+where the reference rounds it: 16-bit floats are computed in float32 and rounded to nearest even after every
+op (for + - * / and sqrt that is the one correct rounding of the reference's float64 result), float32 in
+float32, float64 in float64; no FMA contraction (the generated code is compiled with -ffp-contract=off).
+
+Kernels:
+  * loop: flat iteration over the output elements, V consecutive elements a thread, 16-byte vector loads and
+    stores for operands read at the iteration's own flat index, grid-stride over the whole tensor;
+  * row: one workgroup (or one wavefront) a row of a row space R x C; each reduction over the row is a
+    stage (wavefront shuffles, then LDS across wavefronts), its result a per-row scalar later stages read;
+    element values a later stage needs again stay in registers (the row's work is unrolled);
+  * reduce: any other reduction: threads over the outputs, workgroups over chunks of the reduced range,
+    float32 partial sums added atomically into a zero-filled output.
+"""
+
+from __future__ import annotations
+
+import math
+import struct
+
+from lumen_amd import dtypes as D
+from lumen_amd.graph.ir import Graph, TensorType
+
+
+class Unfusable(Exception):
+    """A fused group the generator cannot express (the plan then splits it)."""
+
+    def __init__(self, var, msg):
+        super().__init__(msg)
+        self.var = var
+
+
+HEADER = r"""
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+#define DEV __device__ __forceinline__
+DEV float lb_bf16(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+DEV uint16_t sb_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+DEV float r_bf16(float f) { return lb_bf16(sb_bf16(f)); }
+DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
+DEV float r_f16(float f) { return lb_f16(sb_f16(f)); }
+DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
+DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
+DEV float fmin_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
+DEV double dmin_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmin(a, b); }
+template <typename T> DEV T sat_cast(double x, double lo, double hi) {
+  if (x != x) return T(0);
+  if (x <= lo) return T(lo);
+  if (x >= hi) return T(hi);
+  return T(x);
+}
+DEV float wsum(float v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
+DEV double wsum(double v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
+DEV float wmax(float v) { for (int o = 32; o > 0; o >>= 1) v = fmax_n(v, __shfl_xor(v, o, 64)); return v; }
+DEV double wmax(double v) { for (int o = 32; o > 0; o >>= 1) v = dmax_n(v, __shfl_xor(v, o, 64)); return v; }
+template <int N> struct alignas(N * 2) u16v { uint16_t e[N]; };
+template <int N> struct alignas(N * 4) f32v { float e[N]; };
+template <int N> struct alignas(N * 4) u32v { uint32_t e[N]; };
+template <int N> struct alignas(N * 8) u64v { uint64_t e[N]; };
+"""
+
+# Storage C type of each dtype in memory.
+STORE_T = {
+    "bool": "uint8_t", "uint8": "uint8_t", "uint16": "uint16_t", "uint32": "uint32_t", "uint64": "uint64_t",
+    "int8": "int8_t", "int16": "int16_t", "int32": "int32_t", "int64": "int64_t",
+    "float16": "uint16_t", "bfloat16": "uint16_t", "float32": "float", "float64": "double",
+}
+# Compute C type of each dtype.
+COMP_T = {
+    "bool": "int", "uint8": "uint32_t", "uint16": "uint32_t", "uint32": "uint32_t", "uint64": "uint64_t",
+    "int8": "int32_t", "int16": "int32_t", "int32": "int32_t", "int64": "int64_t",
+    "float16": "float", "bfloat16": "float", "float32": "float", "float64": "double",
+}
+VEC_T = {2: "u16v", 4: "f32v", 8: "u64v"}
+
+
+def _lit(value, dtype):
+    """A C literal of ``value`` rounded to ``dtype`` (in its compute type)."""
+    if D.is_float(dtype):
+        v = float(value)
+        if dtype in ("bfloat16", "float16", "float32"):
+            import numpy as np
+
+            if dtype == "bfloat16":
+                v = float(D.bf16_to_f32(D.bf16_bits(np.array([v], np.float64)))[0])
+            elif dtype == "float16":
+                from lumen_amd.dtypes import _round_to_odd_f32
+
+                v = float(np.float16(_round_to_odd_f32(np.array([v]))[0]))
+            else:
+                v = float(np.float32(v))
+            if math.isnan(v):
+                return "__builtin_nanf(\"\")"
+            if math.isinf(v):
+                return "__builtin_inff()" if v > 0 else "(-__builtin_inff())"
+            return f"{v.hex()}f" if v != 0 or math.copysign(1, v) > 0 else "(-0.0f)"
+        if math.isnan(v):
+            return "__builtin_nan(\"\")"
+        if math.isinf(v):
+            return "__builtin_inf()" if v > 0 else "(-__builtin_inf())"
+        return v.hex()
+    if dtype == "bool":
+        return "1" if value else "0"
+    return f"(({COMP_T[dtype]})({int(value)}LL))"
+
+
+def _contig(shape):
+    st, s = [], 1
+    for n in reversed(shape):
+        st.append(s)
+        s *= n
+    return tuple(reversed(st))
+
+
+class View:
+    """Where a kernel operand lives: element offset and strides from its buffer's base pointer."""
+
+    def __init__(self, dtype, shape, offset=0, strides=None):
+        self.dtype, self.shape, self.offset = dtype, tuple(shape), offset
+        self.strides = tuple(strides) if strides is not None else _contig(shape)
+
+    def contiguous(self):
+        return self.strides == _contig(self.shape) or math.prod(self.shape) <= 1
+
+
+class Emitter:
+    """Evaluates graph values of one kernel at index expressions, writing C statements."""
+
+    def __init__(self, graph: Graph, nodes, inputs: dict, rows=None):
+        self.graph = graph
+        self.prod = {n.output: n for n in nodes}
+        self.inputs = inputs          # var -> (arg index, View)
+        self.lines: list[str] = []
+        self.memo: dict = {}
+        self.count = 0
+        self.rows = rows
+        self.row_scalars: dict = {}   # reduction var -> C name of its per-row value
+        self.flat_loads: dict = {}    # (arg, fbase) -> element names (vectorized loads)
+        self.vec = 1
+
+    def tmp(self, prefix="t"):
+        self.count += 1
+        return f"{prefix}{self.count}"
+
+    def emit(self, line):
+        self.lines.append(line)
+
+    # ---- indices
+    def multi(self, idx, shape):
+        """``idx`` as one expression per dimension of ``shape``."""
+        kind = idx[0]
+        if kind == "multi":
+            return list(idx[1])
+        f = self.flat(idx, shape)
+        if not shape:
+            return []
+        out = []
+        st = _contig(shape)
+        for d, n in enumerate(shape):
+            if n == 1:
+                out.append("0")
+            elif d == 0:
+                out.append(f"(({f}) / {st[0]}LL)")
+            else:
+                out.append(f"((({f}) / {st[d]}LL) % {n}LL)")
+        return out
+
+    def flat(self, idx, shape):
+        kind = idx[0]
+        if kind == "flat":
+            return idx[1]
+        if kind == "rc":
+            return f"({idx[1]} * {self.rows[1]}LL + {idx[2]})"
+        if kind == "r":
+            return idx[1]
+        st = _contig(shape)
+        terms = [f"({e}) * {s}LL" for e, s in zip(idx[1], st) if s and e != "0"]
+        return "(" + (" + ".join(terms) if terms else "0") + ")"
+
+    # ---- values
+    def value(self, var, idx):
+        ty = self.graph.types[var]
+        key = (var, self._key(idx, ty.shape))
+        if key in self.memo:
+            return self.memo[key]
+        name = self._compute(var, idx, ty)
+        self.memo[key] = name
+        return name
+
+    def _key(self, idx, shape):
+        if idx[0] in ("rc", "r", "flat"):
+            return idx
+        return ("multi", tuple(idx[1]))
+
+    def load(self, var, idx, ty):
+        arg, view = self.inputs[var]
+        ct = COMP_T[ty.dtype]
+        if idx[0] in ("flat", "rc") and view.contiguous() and view.offset % max(1, self.vec) == 0 and self.vec > 1:
+            f = self.flat(idx, ty.shape)
+            base, lane = self._split_vec(idx)
+            if base is not None:
+                names = self.flat_loads.setdefault((arg, base), [None] * self.vec)
+                if names[lane] is None:
+                    names[lane] = self.tmp("v")
+                raw = names[lane]
+                return self._widen(raw, ty.dtype)
+            del f
+        if idx[0] in ("flat", "rc", "r") and view.contiguous():
+            addr = self.flat(idx, ty.shape)
+        else:
+            m = self.multi(idx, ty.shape)
+            terms = [f"({e}) * {s}LL" for e, s in zip(m, view.strides) if s and e != "0"]
+            addr = "(" + (" + ".join(terms) if terms else "0") + ")"
+        n = self.tmp()
+        self.emit(f"const {ct} {n} = {self._widen(f'in{arg}[{addr}]', ty.dtype)};")
+        return n
+
+    def _split_vec(self, idx):
+        """``(base, lane)`` if ``idx`` is ``base + lane`` of the current vector, else (None, None)."""
+        if idx[0] == "flat" and isinstance(idx, tuple) and len(idx) == 4:
+            return idx[2], idx[3]
+        if idx[0] == "rc" and len(idx) == 5:
+            return f"({idx[1]} * {self.rows[1]}LL + {idx[3]})", idx[4]
+        return None, None
+
+    @staticmethod
+    def _widen(raw, dtype):
+        if dtype == "bfloat16":
+            return f"lb_bf16({raw})"
+        if dtype == "float16":
+            return f"lb_f16({raw})"
+        return f"(({COMP_T[dtype]})({raw}))"
+
+    def round(self, expr, dtype):
+        if dtype == "bfloat16":
+            return f"r_bf16({expr})"
+        if dtype == "float16":
+            return f"r_f16({expr})"
+        if dtype == "float32":
+            return f"((float)({expr}))"
+        if dtype == "float64":
+            return f"((double)({expr}))"
+        if dtype == "bool":
+            return f"(({expr}) != 0)"
+        return f"(({COMP_T[dtype]})({STORE_T[dtype]})({expr}))"
+
+    def _compute(self, var, idx, ty):
+        if var in self.inputs:
+            return self.load(var, idx, ty)
+        n = self.prod.get(var)
+        if n is None:
+            raise Unfusable(var, f"value %{var} is neither computed in the kernel nor an input")
+        p = n.prim
+        dt = ty.dtype
+        ct = COMP_T[dt]
+        out = self.tmp()
+        ins = [self.graph.types[v] for v in n.inputs]
+
+        def same(k=0):
+            return self.value(n.inputs[k], idx)
+
+        if p in ("add", "sub", "mul", "div", "max", "eq", "lt"):
+            a, b = same(0), same(1)
+            src = ins[0].dtype
+            if p in ("eq", "lt"):
+                op = "==" if p == "eq" else "<"
+                self.emit(f"const int {out} = ({a} {op} {b});")
+            elif p == "max":
+                if D.is_float(src):
+                    fn = "dmax_n" if src == "float64" else "fmax_n"
+                    self.emit(f"const {ct} {out} = {fn}({a}, {b});")
+                else:
+                    self.emit(f"const {ct} {out} = ({a} > {b} ? {a} : {b});")
+            else:
+                op = {"add": "+", "sub": "-", "mul": "*", "div": "/"}[p]
+                if D.is_float(dt):
+                    self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
+                elif p == "div":
+                    self.emit(f"const {ct} {out} = ({b} == 0 ? ({ct})-1 : {self.round(f'{a} / {b}', dt)});")
+                else:
+                    self.emit(f"const {ct} {out} = {self.round(f'(int64_t){a} {op} (int64_t){b}', dt)};")
+            return out
+        if p == "neg":
+            a = same()
+            self.emit(f"const {ct} {out} = {self.round(f'-{a}', dt) if not D.is_float(dt) else f'-{a}'};")
+            return out
+        if p in ("exp", "log", "sqrt", "tanh", "logistic", "sin", "cos", "tan", "asin", "acos", "atan", "sinh",
+                 "cosh", "asinh", "acosh", "atanh", "floor", "ceil", "round", "log1p", "expm1", "exp2", "log2",
+                 "rsqrt", "cbrt", "abs"):
+            a = same()
+            if not D.is_float(dt):
+                if p == "abs":
+                    self.emit(f"const {ct} {out} = {self.round(f'({a} < 0 ? -(int64_t){a} : (int64_t){a})', dt)};")
+                    return out
+                raise Unfusable(var, f"{p} of {dt}")
+            f32 = dt != "float64"
+            fn = {
+                "exp": "exp", "log": "log", "sqrt": "sqrt", "tanh": "tanh", "sin": "sin", "cos": "cos", "tan": "tan",
+                "asin": "asin", "acos": "acos", "atan": "atan", "sinh": "sinh", "cosh": "cosh", "asinh": "asinh",
+                "acosh": "acosh", "atanh": "atanh", "floor": "floor", "ceil": "ceil", "round": "rint",
+                "log1p": "log1p", "expm1": "expm1", "exp2": "exp2", "log2": "log2", "cbrt": "cbrt", "abs": "fabs",
+            }.get(p)
+            s = "f" if f32 else ""
+            one = "1.0f" if f32 else "1.0"
+            if p == "logistic":
+                expr = f"{one} / ({one} + exp{s}(-{a}))"
+            elif p == "rsqrt":
+                expr = f"{one} / sqrt{s}({a})"
+            else:
+                expr = f"{fn}{s}({a})"
+            self.emit(f"const {ct} {out} = {self.round(expr, dt)};")
+            return out
+        if p == "sign":
+            a = same()
+            if D.is_float(dt):
+                self.emit(f"const {ct} {out} = ({a} == 0 || {a} != {a}) ? {a} : ({a} > 0 ? ({ct})1 : ({ct})-1);")
+            else:
+                self.emit(f"const {ct} {out} = ({a} > 0) - ({a} < 0);")
+            return out
+        if p == "is_finite":
+            a = same()
+            self.emit(f"const int {out} = isfinite({a}) ? 1 : 0;")
+            return out
+        if p == "not":
+            a = same()
+            self.emit(f"const {ct} {out} = {('!' + a) if dt == 'bool' else self.round('~' + a, dt)};")
+            return out
+        if p in ("min", "pow", "rem", "and", "or", "xor"):
+            a, b = same(0), same(1)
+            if p == "min":
+                if D.is_float(dt):
+                    self.emit(f"const {ct} {out} = {'dmin_n' if dt == 'float64' else 'fmin_n'}({a}, {b});")
+                else:
+                    self.emit(f"const {ct} {out} = ({a} < {b} ? {a} : {b});")
+            elif p == "pow":
+                s = "" if dt == "float64" else "f"
+                self.emit(f"const {ct} {out} = {self.round(f'pow{s}({a}, ({ct}){b})', dt)};")
+            elif p == "rem":
+                if D.is_float(dt):
+                    s = "" if dt == "float64" else "f"
+                    self.emit(f"const {ct} {out} = {self.round(f'fmod{s}({a}, {b})', dt)};")
+                else:
+                    self.emit(f"const {ct} {out} = ({b} == 0 ? {a} : {a} % {b});")
+            else:
+                op = {"and": "&", "or": "|", "xor": "^"}[p]
+                self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
+            return out
+        if p == "cast":
+            a = same()
+            src = ins[0].dtype
+            if D.is_float(dt) and D.is_float(src):
+                expr = self.round(a, dt) if dt != "float64" else f"(double){a}"
+                if src == "float64" and dt in ("bfloat16", "float16"):
+                    raise Unfusable(var, "float64 to a 16-bit float needs round to odd")
+            elif D.is_float(dt):
+                expr = self.round(f"(float)({a})", dt) if dt != "float64" else f"(double)({a})"
+            elif dt == "bool":
+                expr = f"(({a}) != 0)"
+            elif D.is_float(src):
+                info = _int_range(dt)
+                expr = f"sat_cast<{COMP_T[dt]}>((double)({a}), {info[0]!r}, {info[1]!r})"
+            else:
+                expr = self.round(a, dt)
+            self.emit(f"const {ct} {out} = {expr};")
+            return out
+        if p == "select":
+            c = same(0)
+            a, b = same(1), same(2)
+            self.emit(f"const {ct} {out} = ({c}) ? {a} : {b};")
+            return out
+        if p == "full":
+            return _lit(n.params["fill_value"], dt)
+        if p == "iota":
+            m = self.multi(idx, ty.shape)
+            self.emit(f"const {ct} {out} = ({ct})({m[n.params['dimension']]});")
+            return out
+        if p in ("host_wait", "device_wait"):
+            return same()
+        if p == "reshape":
+            src = ins[0]
+            if idx[0] in ("flat", "rc") or (idx[0] == "r" and src.numel() == self.rows[0]):
+                return self.value(n.inputs[0], idx)
+            return self.value(n.inputs[0], ("flat", self.flat(idx, ty.shape)))
+        if p == "broadcast_in_dim":
+            src = ins[0]
+            dims = n.params["broadcast_dimensions"]
+            if idx[0] in ("rc",) and self._row_broadcast(src, ty, dims):
+                return self.value(n.inputs[0], ("r", idx[1]))
+            m = self.multi(idx, ty.shape)
+            sm = [("0" if src.shape[i] == 1 else m[d]) for i, d in enumerate(dims)]
+            return self.value(n.inputs[0], ("multi", tuple(sm)))
+        if p == "transpose":
+            m = self.multi(idx, ty.shape)
+            perm = n.params["permutation"]
+            sm = [None] * len(perm)
+            for i, d in enumerate(perm):
+                sm[d] = m[i]
+            return self.value(n.inputs[0], ("multi", tuple(sm)))
+        if p == "slice":
+            m = self.multi(idx, ty.shape)
+            st = n.params["start_indices"]
+            return self.value(n.inputs[0], ("multi", tuple(f"({e} + {s}LL)" if s else e for e, s in zip(m, st))))
+        if p == "swap_pairs":
+            m = self.multi(idx, ty.shape)
+            m[-1] = f"(({m[-1]}) ^ 1LL)"
+            return self.value(n.inputs[0], ("multi", tuple(m)))
+        if p == "concatenate":
+            d = n.params["dimension"]
+            m = self.multi(idx, ty.shape)
+            self.emit(f"{ct} {out};")
+            start = 0
+            for k, v in enumerate(n.inputs):
+                size = ins[k].shape[d]
+                cond = f"if (({m[d]}) < {start + size}LL)" if k < len(n.inputs) - 1 else ""
+                self.emit(("else " if k else "") + cond + " {")
+                saved = self.memo
+                self.memo = dict(saved)
+                sm = list(m)
+                sm[d] = f"(({m[d]}) - {start}LL)" if start else m[d]
+                val = self.value(v, ("multi", tuple(sm)))
+                self.memo = saved
+                self.emit(f"  {out} = {val};")
+                self.emit("}")
+                start += size
+            return out
+        if p == "gather":
+            axis = n.params["axis"]
+            x, ix = ins
+            m = self.multi(idx, ty.shape)
+            r = len(ix.shape)
+            iv = self.value(n.inputs[1], ("multi", tuple(m[axis : axis + r])))
+            k = self.tmp()
+            hi = max(x.shape[axis] - 1, 0)
+            self.emit(f"const int64_t {k} = min(max((int64_t){iv}, 0LL), {hi}LL);")
+            sm = m[:axis] + [k] + m[axis + r :]
+            return self.value(n.inputs[0], ("multi", tuple(sm)))
+        if p == "take_along_axis":
+            axis = n.params["axis"]
+            x = ins[0]
+            m = self.multi(idx, ty.shape)
+            iv = self.value(n.inputs[1], ("multi", tuple(m)))
+            k = self.tmp()
+            self.emit(f"const int64_t {k} = min(max((int64_t){iv}, 0LL), {max(x.shape[axis] - 1, 0)}LL);")
+            sm = list(m)
+            sm[axis] = k
+            return self.value(n.inputs[0], ("multi", tuple(sm)))
+        if p == "dynamic_slice":
+            x = ins[0]
+            m = self.multi(idx, ty.shape)
+            sm = []
+            for d in range(len(x.shape)):
+                s = self.value(n.inputs[1 + d], ("multi", ()))
+                hi = x.shape[d] - ty.shape[d]
+                k = self.tmp()
+                self.emit(f"const int64_t {k} = min(max((int64_t){s}, 0LL), {hi}LL);")
+                sm.append(f"({m[d]} + {k})")
+            return self.value(n.inputs[0], ("multi", tuple(sm)))
+        if p in ("reduce_sum", "reduce_max"):
+            if var in self.row_scalars:
+                return self.row_scalars[var]
+            raise Unfusable(var, f"{p} %{var} read outside its row")
+        raise Unfusable(var, f"{p} has no loop-kernel lowering")
+
+    def _row_broadcast(self, src, out, dims):
+        """Whether broadcasting ``src`` (numel R) to ``out`` (the R x C row space) repeats each row value over
+        the row's C elements."""
+        if self.rows is None or src.numel() != self.rows[0] or out.numel() != self.rows[0] * self.rows[1]:
+            return False
+        # the source's non-1 dims must be the leading output dims, equal in size, covering R
+        lead = 1
+        for i, d in enumerate(dims):
+            if src.shape[i] == 1:
+                continue
+            if d != i or out.shape[d] != src.shape[i]:
+                return False
+            lead *= src.shape[i]
+        k = 0
+        while k < len(out.shape) and math.prod(out.shape[:k]) < self.rows[0]:
+            k += 1
+        return lead == self.rows[0] and math.prod(out.shape[:k]) == self.rows[0]
+
+
+def _int_range(dt):
+    import numpy as np
+
+    if dt == "bool":
+        return (0.0, 1.0)
+    info = np.iinfo(D.storage(dt))
+    return (float(info.min), float(info.max))
+
+
+def _store(expr_name, dtype):
+    if dtype == "bfloat16":
+        return f"sb_bf16({expr_name})"
+    if dtype == "float16":
+        return f"sb_f16({expr_name})"
+    return f"({STORE_T[dtype]})({expr_name})"
+
+
+def _vec_width(numel, elem_bytes):
+    for v in (8, 4, 2):
+        if numel % v == 0 and v * elem_bytes <= 16 and v * elem_bytes in (4, 8, 16) or (v * elem_bytes == 2 and False):
+            return v
+    return 1
+
+
+class LoopKernel:
+    """A fused loop kernel of a plan step: its source, name and launch shape."""
+
+    def __init__(self, graph, step, name, views: dict, out_views: dict):
+        self.graph, self.step, self.name = graph, step, name
+        self.views, self.out_views = views, out_views
+        self.args = []  # ("in"|"out", var)
+        self.extra_fill = []
+
+    def source(self):
+        st = self.step
+        if st.kind == "row":
+            return self._row()
+        if st.kind == "reduce":
+            return self._reduce()
+        return self._loop()
+
+    def _params(self):
+        ps = []
+        self.args = []
+        for k, v in enumerate(self.step.inputs):
+            ps.append(f"const {STORE_T[self.graph.types[v].dtype]}* __restrict__ in{k}")
+            self.args.append(("in", v))
+        for k, v in enumerate(self.step.outputs):
+            ps.append(f"{STORE_T[self.graph.types[v].dtype]}* __restrict__ out{k}")
+            self.args.append(("out", v))
+        return ", ".join(ps)
+
+    def _emitter(self, rows=None):
+        ins = {v: (k, self.views[v]) for k, v in enumerate(self.step.inputs)}
+        return Emitter(self.graph, self.step.nodes, ins, rows)
+
+    # ---- elementwise
+    def _loop(self):
+        g, st = self.graph, self.step
+        root = st.outputs[0]
+        shape = g.types[root].shape
+        numel = g.types[root].numel()
+        for v in st.outputs:
+            if g.types[v].numel() != numel:
+                raise Unfusable(v, "loop kernel outputs of different sizes")
+        esz = max(D.size_of(g.types[v].dtype) for v in st.outputs)
+        esz_min = min(D.size_of(g.types[v].dtype) for v in st.outputs)
+        V = 1
+        for cand in (8, 4, 2):
+            if numel % cand == 0 and cand * esz <= 16 and cand * esz_min >= 4:
+                V = cand
+                break
+        em = self._emitter()
+        em.vec = V
+        per_v = []
+        for lane in range(V):
+            idx = ("flat", f"(base + {lane})", "base", lane) if V > 1 else ("flat", "base")
+            names = [em.value(v, idx) for v in st.outputs]
+            per_v.append(names)
+        body = em.lines
+        pro = self._vec_prologue(em, V)
+        stores = []
+        for k, v in enumerate(st.outputs):
+            dt = g.types[v].dtype
+            if V > 1 and self.out_views[v].contiguous():
+                stores.append(self._vec_store(f"out{k}", "base", [per_v[l][k] for l in range(V)], dt, V))
+            else:
+                view = self.out_views[v]
+                for lane in range(V):
+                    addr = self._out_addr(view, g.types[v].shape, f"(base + {lane})")
+                    stores.append(f"out{k}[{addr}] = {_store(per_v[lane][k], dt)};")
+        threads = 256
+        blocks = max(1, min(-(-numel // (threads * V)), 8192))
+        self.grid, self.block, self.lds = (blocks, 1, 1), (threads, 1, 1), 0
+        src = [
+            f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{',
+            f"  for (int64_t base = ((int64_t)blockIdx.x * {threads} + threadIdx.x) * {V}; base < {numel}LL; "
+            f"base += (int64_t)gridDim.x * {threads * V}) {{",
+        ]
+        src += ["    " + l for l in pro + body + stores]
+        src += ["  }", "}"]
+        del shape
+        return "\n".join(src)
+
+    def _out_addr(self, view, shape, flat):
+        if view.contiguous():
+            return flat
+        st = _contig(shape)
+        terms = []
+        for d, n in enumerate(shape):
+            if n == 1 or view.strides[d] == 0:
+                continue
+            e = f"(({flat}) / {st[d]}LL)" if d == 0 else f"((({flat}) / {st[d]}LL) % {n}LL)"
+            terms.append(f"{e} * {view.strides[d]}LL")
+        return "(" + (" + ".join(terms) if terms else "0") + ")"
+
+    def _vec_prologue(self, em, V):
+        lines = []
+        for (arg, base), names in em.flat_loads.items():
+            dt = self.graph.types[self.step.inputs[arg]].dtype
+            esz = D.size_of(dt)
+            vt = {2: "u16v", 4: "u32v", 8: "u64v"}.get(esz)
+            if vt is None or V * esz not in (4, 8, 16) or esz == 1:
+                for lane, nm in enumerate(names):
+                    if nm is not None:
+                        lines.append(f"const {STORE_T[dt]} {nm} = in{arg}[{base} + {lane}];")
+                continue
+            tmp = em.tmp("V")
+            lines.append(f"const {vt}<{V}> {tmp} = *reinterpret_cast<const {vt}<{V}>*>(in{arg} + {base});")
+            ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
+            for lane, nm in enumerate(names):
+                if nm is not None:
+                    lines.append(f"const {STORE_T[dt]} {nm} = __builtin_bit_cast({STORE_T[dt]}, ({ct}){tmp}.e[{lane}]);")
+        return lines
+
+    def _vec_store(self, ptr, base, names, dt, V):
+        esz = D.size_of(dt)
+        vt = {2: "u16v", 4: "u32v", 8: "u64v"}.get(esz)
+        if vt is None or V * esz not in (4, 8, 16):
+            return " ".join(f"{ptr}[{base} + {l}] = {_store(n, dt)};" for l, n in enumerate(names))
+        ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
+        t = f"S{abs(hash((ptr, base))) % 100000}"
+        parts = [f"{{ {vt}<{V}> {t};"]
+        for l, n in enumerate(names):
+            parts.append(f"{t}.e[{l}] = __builtin_bit_cast({ct}, ({STORE_T[dt]}){_store(n, dt)});")
+        parts.append(f"*reinterpret_cast<{vt}<{V}>*>({ptr} + {base}) = {t}; }}")
+        return " ".join(parts)
+
+    # ---- row kernels
+    def _row(self):
+        g, st = self.graph, self.step
+        R, C = st.rows
+        reds = [n for n in st.nodes if n.prim in ("reduce_sum", "reduce_max")]
+        outs_elem = [v for v in st.outputs if g.types[v].numel() == R * C and R * C != R]
+        outs_row = [v for v in st.outputs if v not in outs_elem]
+        dts = [g.types[v].dtype for v in st.outputs] + [g.types[v].dtype for v in st.inputs]
+        esz = max([D.size_of(d) for d in dts] + [2])
+        V = 1
+        for cand in (8, 4, 2):
+            if C % cand == 0 and cand * esz <= 16 and C // cand >= 64:
+                V = cand
+                break
+        chunks = -(-C // V)
+        if chunks <= 64:
+            T, rows_per_block = 64, 4
+        else:
+            T = min(1024, -(-chunks // 64) * 64)
+            rows_per_block = 1
+        J = -(-chunks // T)
+        exact = C % (T * V) == 0
+        em = self._emitter(rows=(R, C))
+        em.vec = V if exact else 1
+        body = []
+        red_identity = {"reduce_sum": "0", "reduce_max": "-INFINITY"}
+        for red in reds:
+            acc_dt = g.types[red.output].dtype
+            act = COMP_T[acc_dt]
+            accn = em.tmp("acc")
+            em.emit(f"{act} {accn} = {red_identity[red.prim] if act != 'double' else red_identity[red.prim]};")
+            for j in range(J):
+                for lane in range(V):
+                    cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
+                    cidx = f"c{j}_{lane}"
+                    if cidx not in _declared(em):
+                        em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
+                        _declared(em).add(cidx)
+                    idx = ("rc", "r", cidx, f"(({j} * {T} + tid) * {V})", lane)
+                    val = em.value(red.inputs[0], idx)
+                    guard = "" if exact else f"if ({cexpr} < {C}LL) "
+                    if red.prim == "reduce_sum":
+                        em.emit(f"{guard}{accn} = {em.round(f'{accn} + {val}', acc_dt)};")
+                    else:
+                        fn = "dmax_n" if act == "double" else "fmax_n"
+                        em.emit(f"{guard}{accn} = {fn}({accn}, {val});")
+            total = em.tmp("red")
+            op = "wsum" if red.prim == "reduce_sum" else "wmax"
+            em.emit(f"{act} {total} = {op}({accn});")
+            if rows_per_block == 1 and T > 64:
+                nw = T // 64
+                comb = "+" if red.prim == "reduce_sum" else "max"
+                em.emit(f"if (lane == 0) red_lds[wave] = (double){total};")
+                em.emit("__syncthreads();")
+                em.emit(f"{total} = ({act})red_lds[0];")
+                for w in range(1, nw):
+                    if comb == "+":
+                        em.emit(f"{total} = {total} + ({act})red_lds[{w}];")
+                    else:
+                        fn = "dmax_n" if act == "double" else "fmax_n"
+                        em.emit(f"{total} = {fn}({total}, ({act})red_lds[{w}]);")
+                em.emit("__syncthreads();")
+            em.row_scalars[red.output] = total
+        # element outputs
+        stores = []
+        for j in range(J):
+            lanes = []
+            for lane in range(V):
+                cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
+                cidx = f"c{j}_{lane}"
+                if cidx not in _declared(em):
+                    em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
+                    _declared(em).add(cidx)
+                idx = ("rc", "r", cidx, f"(({j} * {T} + tid) * {V})", lane)
+                lanes.append([em.value(v, idx) for v in outs_elem])
+            for k, v in enumerate(outs_elem):
+                oi = st.outputs.index(v)
+                dt = g.types[v].dtype
+                base = f"(r * {C}LL + ({j} * {T} + tid) * {V})"
+                if V > 1 and self.out_views[v].contiguous():
+                    s = self._vec_store(f"out{oi}", base, [lanes[l][k] for l in range(V)], dt, V)
+                else:
+                    s = " ".join(
+                        f"out{oi}[{self._out_addr(self.out_views[v], g.types[v].shape, f'({base} + {l})')}] = "
+                        f"{_store(lanes[l][k], dt)};"
+                        for l in range(V)
+                    )
+                if not exact:
+                    s = f"if ((({j} * {T} + tid) * {V}) < {C}LL) {{ {s} }}"
+                stores.append(s)
+        for v in outs_row:
+            oi = st.outputs.index(v)
+            val = em.value(v, ("r", "r"))
+            dt = g.types[v].dtype
+            addr = self._out_addr(self.out_views[v], g.types[v].shape, "r")
+            stores.append(f"if (tid == 0) out{oi}[{addr}] = {_store(val, dt)};")
+        body = em.lines
+        pro = self._vec_prologue(em, V)
+        threads = T * rows_per_block
+        self.grid, self.block = (-(-R // rows_per_block), 1, 1), (threads, 1, 1)
+        self.lds = 0
+        src = [f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{']
+        if rows_per_block > 1:
+            src += [
+                "  const int tid = threadIdx.x & 63; const int lane = tid; const int wave = threadIdx.x >> 6;",
+                f"  const int64_t r = (int64_t)blockIdx.x * {rows_per_block} + wave;",
+                f"  if (r >= {R}LL) return;",
+            ]
+        else:
+            src += [
+                "  const int tid = threadIdx.x; const int lane = tid & 63; const int wave = tid >> 6;",
+                "  const int64_t r = blockIdx.x;",
+                "  __shared__ double red_lds[16];",
+            ]
+        src += ["  (void)lane; (void)wave;"]
+        # vector loads need the c indices declared before them: emit prologue after index decls
+        decl = [l for l in body if l.startswith("const int64_t c") and "(( " not in l]
+        rest = [l for l in body if l not in decl]
+        src += ["  " + l for l in decl + pro + rest + stores]
+        src += ["}"]
+        return "\n".join(src)
+
+    # ---- general reductions
+    def _reduce(self):
+        g, st = self.graph, self.step
+        red = [n for n in st.nodes if n.prim in ("reduce_sum", "reduce_max")]
+        if len(red) != 1 or red[0].output != st.outputs[0] or len(st.outputs) != 1:
+            raise Unfusable(st.outputs[0], "a reduce step computes one reduction")
+        red = red[0]
+        x = g.types[red.inputs[0]]
+        axes = tuple(red.params["axes"])
+        kept = [d for d in range(len(x.shape)) if d not in axes]
+        oshape = tuple(x.shape[d] for d in kept)
+        rshape = tuple(x.shape[d] for d in axes)
+        O, Q = math.prod(oshape), math.prod(rshape)
+        out_dt = g.types[red.output].dtype
+        atomic = red.prim == "reduce_sum" and out_dt == "float32" and Q >= 64
+        chunk = max(1, min(Q, 64)) if atomic else Q
+        nchunks = -(-Q // chunk)
+        em = self._emitter()
+        om = em.multi(("flat", "o"), oshape)
+        qm = em.multi(("flat", "q"), rshape)
+        xm = [None] * len(x.shape)
+        for i, d in enumerate(kept):
+            xm[d] = om[i]
+        for i, d in enumerate(axes):
+            xm[d] = qm[i]
+        em.lines = []
+        val = em.value(red.inputs[0], ("multi", tuple(xm)))
+        body = em.lines
+        act = COMP_T[out_dt]
+        if red.prim == "reduce_sum":
+            upd = f"acc = {em.round(f'acc + {val}', out_dt)};"
+            init = "0"
+        else:
+            fn = "dmax_n" if act == "double" else "fmax_n"
+            upd = f"acc = {fn}(acc, {val});" if D.is_float(out_dt) else f"acc = acc > {val} ? acc : {val};"
+            init = "-INFINITY" if D.is_float(out_dt) else str(_int_range(out_dt)[0]).split(".")[0] + "LL"
+        self.atomic = atomic
+        threads = 256
+        self.grid, self.block, self.lds = (-(-O // threads), nchunks, 1), (threads, 1, 1), 0
+        addr = self._out_addr(self.out_views[red.output], oshape, "o")
+        store = f"atomicAdd(&out0[{addr}], acc);" if atomic else f"out0[{addr}] = {_store('acc', out_dt)};"
+        src = [
+            f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{',
+            f"  const int64_t o = (int64_t)blockIdx.x * {threads} + threadIdx.x;",
+            f"  if (o >= {O}LL) return;",
+            f"  const int64_t q0 = (int64_t)blockIdx.y * {chunk}LL;",
+            f"  const int64_t q1 = min(q0 + {chunk}LL, {Q}LL);",
+            f"  {act} acc = {init};",
+            "  for (int64_t q = q0; q < q1; ++q) {",
+        ]
+        src += ["    " + l for l in body]
+        src += ["    " + upd, "  }", "  " + store, "}"]
+        return "\n".join(src)
+
+
+def _declared(em):
+    if not hasattr(em, "_decl"):
+        em._decl = set()
+    return em._decl
+
+
+_ = (struct, TensorType, VEC_T)

@@ -1,0 +1,261 @@
+"""Loop fusion: groups a graph's nodes into the steps of a plan (``lumen/graph_compiler/passes/fusion/mod.rs``,
+``passes/diamonds.rs``, ``passes/alone.rs``).
+
+Nodes are visited in reverse topological order. A dot, a flash-attention fusion or a scatter-add is a step
+of its own (a built-in kernel). Every other node is fusible: it joins the loop kernel of its consumers when
+all of them are in one kernel, so its value never reaches memory. A value with consumers in several kernels
+is computed once (it gets a kernel, or becomes an extra output of the kernel it is in) unless it is index
+math alone (``full``, ``iota``, layout ops of a kernel input), which each kernel recomputes.
+
+A loop kernel with reductions is a row kernel: every reduction sums (or maxes) the trailing axes of one row
+space ``R x C`` (a normalization diamond: softmax, layer norm, RMS norm, cross entropy's log-sum-exp), its
+results flowing back to the rows only through size-1 reshapes and broadcasts of the trailing axes. Any
+other reduction is a reduce step of its own.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from lumen_amd.graph.ir import ELEMENTWISE, Graph
+
+LAYOUT = {"reshape", "broadcast_in_dim", "transpose", "slice", "concatenate", "swap_pairs"}
+VIEWABLE = {"reshape", "broadcast_in_dim", "transpose", "slice"}
+INDEX_ONLY = {"full", "iota"}
+FUSIBLE = ELEMENTWISE | LAYOUT | INDEX_ONLY | {"gather", "take_along_axis", "reduce_sum", "reduce_max",
+                                               "dynamic_slice", "host_wait", "device_wait"}
+# Built-in kernels: each node is a step of its own.
+OWN_STEP = {"dot_general", "flash_attention", "flash_attention_backward", "scatter_add", "cumsum",
+            "random_bits", "linear_cross_entropy", "dynamic_update_slice", "fusion_output"}
+
+
+@dataclass
+class Step:
+    """One launch (or view) of the plan."""
+
+    kind: str                       # "loop", "row", "reduce", "dot", "flash_fwd", "flash_bwd", "scatter_add", "copy"
+    nodes: list = field(default_factory=list)    # graph nodes computed, topological order
+    outputs: list = field(default_factory=list)  # values this step writes to memory
+    inputs: list = field(default_factory=list)   # values it reads from memory
+    rows: tuple | None = None       # (R, C) of a row kernel
+    name: str = ""
+
+    def label(self):
+        return " → ".join(n.prim for n in self.nodes[:6]) + (" → …" if len(self.nodes) > 6 else "")
+
+
+def _row_space(graph, n):
+    """``(R, C)`` of a reduction over trailing axes, or None."""
+    x = graph.types[n.inputs[0]]
+    axes = tuple(n.params["axes"])
+    r = len(x.shape)
+    if not axes or axes != tuple(range(r - len(axes), r)):
+        return None
+    c = math.prod(x.shape[r - len(axes):])
+    return (math.prod(x.shape[: r - len(axes)]), c)
+
+
+def fuse(graph: Graph, fuse_loops=True) -> list:
+    """The steps computing ``graph``'s outputs, in an order respecting dependencies."""
+    users = graph.users()
+    prod = graph.producers()
+    order = {n.output: i for i, n in enumerate(graph.nodes)}
+    for i, v in enumerate(graph.inputs):
+        order[v] = -1 - i
+    is_input = set(graph.inputs)
+    must = set(graph.outputs)
+    views = set()
+    # Operands of built-in steps live in memory; a layout op there is a strided view when it can be one.
+    for n in graph.nodes:
+        if n.prim in OWN_STEP:
+            for u in n.inputs:
+                while u in prod and prod[u].prim in VIEWABLE and u not in graph.outputs:
+                    views.add(u)
+                    u = prod[u].inputs[0]
+                must.add(u)
+    for v in views:
+        must.add(prod[v].inputs[0])
+    kernel_of: dict[int, int] = {}
+    members: list[set] = []
+    kinds: list[str] = []
+    rows: list = []
+    roots: list[list] = []
+
+    def cheap(v):
+        n = prod.get(v)
+        if n is None:
+            return True
+        if n.prim in INDEX_ONLY:
+            return True
+        if n.prim in ("reshape", "broadcast_in_dim", "transpose", "slice"):
+            return all(cheap(u) for u in n.inputs)
+        return False
+
+    def depends(v, target, memo):
+        """Whether ``v`` transitively depends on ``target`` (pruned by topological order)."""
+        if v == target:
+            return True
+        if order.get(v, -1) <= order.get(target, -1):
+            return False
+        if v in memo:
+            return memo[v]
+        n = prod.get(v)
+        r = n is not None and any(depends(u, target, memo) for u in n.inputs)
+        memo[v] = r
+        return r
+
+    for n in reversed(graph.nodes):
+        v = n.output
+        if v in kernel_of:
+            continue
+        if cheap(v) and v not in must and v not in views:
+            continue
+        if v in views and v not in must:
+            k = len(members)
+            members.append({v})
+            kinds.append("view")
+            rows.append(None)
+            roots.append([v])
+            kernel_of[v] = k
+            continue
+        if n.prim in OWN_STEP or n.prim not in FUSIBLE or not fuse_loops:
+            k = len(members)
+            members.append({v})
+            kinds.append("own")
+            rows.append(None)
+            roots.append([v])
+            kernel_of[v] = k
+            continue
+        k = len(members)
+        mem = {v}
+        members.append(mem)
+        kinds.append("loop")
+        rows.append(None)
+        roots.append([v])
+        kernel_of[v] = k
+        if n.prim in ("reduce_sum", "reduce_max"):
+            rs = _row_space(graph, n)
+            if rs is not None:
+                rows[k] = rs
+            else:
+                kinds[k] = "reduce"
+                continue
+        frontier = list(n.inputs)
+        while frontier:
+            frontier.sort(key=lambda u: -order.get(u, -1))
+            u = frontier.pop(0)
+            if u in is_input or u in mem or u in views:
+                continue
+            p = prod[u]
+            if p.prim not in FUSIBLE or p.prim in OWN_STEP:
+                continue
+            if cheap(u) and u not in must:
+                mem.add(u)
+                frontier.extend(p.inputs)
+                continue
+            if u in kernel_of:
+                continue
+            outside = {c.output for c in users.get(u, []) if c.output not in mem}
+            if p.prim in ("reduce_sum", "reduce_max"):
+                rs = _row_space(graph, p)
+                if rs is None or (rows[k] is not None and rows[k] != rs):
+                    continue
+                if not all(graph.types[r].numel() in (rs[0] * rs[1], rs[0]) for r in roots[k]):
+                    continue
+            if outside or u in must:
+                if not _fits(graph, u, roots[k], rows[k] if p.prim not in ("reduce_sum", "reduce_max") else _row_space(graph, p)):
+                    continue
+                memo = {}
+                if any(depends(m, c, memo) for c in outside for m in mem):
+                    continue
+                roots[k].append(u)
+                must.add(u)
+            mem.add(u)
+            kernel_of[u] = k
+            if p.prim in ("reduce_sum", "reduce_max"):
+                rows[k] = _row_space(graph, p)
+            frontier.extend(p.inputs)
+    steps = []
+    for k, mem in enumerate(members):
+        nodes = [m for m in graph.nodes if m.output in mem]
+        outs = list(roots[k])
+        if kinds[k] == "own":
+            node = nodes[0]
+            kind = {"dot_general": "dot", "flash_attention": "flash_fwd", "flash_attention_backward": "flash_bwd"}.get(
+                node.prim, node.prim
+            )
+            st = Step(kind, nodes, outs)
+        elif kinds[k] in ("view", "reduce"):
+            st = Step(kinds[k], nodes, outs)
+        else:
+            st = Step("row" if rows[k] is not None else "loop", nodes, outs, rows=rows[k])
+        produced = {m.output for m in nodes}
+        ins = []
+        for m in nodes:
+            for u in m.inputs:
+                if u not in produced and u not in ins:
+                    ins.append(u)
+        st.inputs = ins
+        steps.append(st)
+    for st in steps:
+        if st.kind in ("loop", "row"):
+            _pull_index_math(graph, st, prod, done_inputs=set(graph.inputs))
+    done, ordered = set(graph.inputs), []
+    pending = steps[:]
+    while pending:
+        progressed = False
+        for st in list(pending):
+            if all(u in done for u in st.inputs):
+                ordered.append(st)
+                done.update(st.outputs)
+                pending.remove(st)
+                progressed = True
+        if not progressed:
+            raise RuntimeError("fusion produced a cycle: " + ", ".join(s.label() for s in pending))
+    return ordered
+
+
+def _index_only(v, prod, done):
+    n = prod.get(v)
+    if n is None:
+        return False
+    if n.prim in INDEX_ONLY:
+        return True
+    if n.prim in ("reshape", "broadcast_in_dim", "transpose", "slice"):
+        return all(u in done or _index_only(u, prod, done) for u in n.inputs)
+    return False
+
+
+def _pull_index_math(graph, st, prod, done_inputs):
+    materialized = set()
+    for s in st.inputs:
+        materialized.add(s)
+    changed = True
+    while changed:
+        changed = False
+        produced = {m.output for m in st.nodes}
+        for u in list(st.inputs):
+            n = prod.get(u)
+            if n is not None and u not in produced and (n.prim in INDEX_ONLY) and u not in st.outputs:
+                st.nodes.append(n)
+                changed = True
+        if changed:
+            st.nodes.sort(key=lambda m: m.output)
+            produced = {m.output for m in st.nodes}
+            st.inputs = []
+            for m in st.nodes:
+                for u in m.inputs:
+                    if u not in produced and u not in st.inputs:
+                        st.inputs.append(u)
+
+
+def _fits(graph, u, roots, rs):
+    """Whether value ``u`` can be an extra output of a kernel with ``roots`` (and row space ``rs``)."""
+    nu = graph.types[u].numel()
+    base = graph.types[roots[0]].numel()
+    if rs is None:
+        return nu == base
+    return nu in (rs[0] * rs[1], rs[0])
+
+

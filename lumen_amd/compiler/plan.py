@@ -1,0 +1,392 @@
+"""The static plan of a graph on one hip device (``lumen/plan``).
+
+``Plan(graph, device)`` runs the hip pass pipeline, groups the graph into steps (``fusion.fuse``), places
+every value a step writes in one workspace by live range at 256-byte alignment (``plan/compile.rs:49-555``,
+``ALIGNMENT`` ``plan/mod.rs:26``), lowers layout ops feeding built-in kernels to strided views, generates and
+compiles the loop kernels, and builds the native step list (``nhip_plan_*``). ``run_in(workspace, inputs)``
+then queues every step on the device's stream with no host work per step but the launch
+(``plan/run.rs:247-427``).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+import struct
+from dataclasses import dataclass
+
+from lumen_amd import dtypes as D
+from lumen_amd.compiler import attention as attn_pass
+from lumen_amd.compiler import codegen, fusion, kcache, passes
+from lumen_amd.config import config
+from lumen_amd.graph.ir import Graph
+
+ALIGNMENT = 256
+NHIP_DT = {"float32": 0, "bfloat16": 1, "float16": 2}
+
+
+@dataclass
+class Loc:
+    """Where a value lives: a base (``("ws", 0)`` the workspace, ``("in", i)`` plan input ``i``), an element
+    offset and element strides."""
+
+    base: tuple
+    offset: int
+    strides: tuple
+    dtype: str
+    shape: tuple
+
+    def contiguous(self):
+        return codegen.View(self.dtype, self.shape, self.offset, self.strides).contiguous()
+
+    def view(self):
+        return codegen.View(self.dtype, self.shape, self.offset, self.strides)
+
+
+def _contig(shape):
+    return codegen._contig(shape)
+
+
+def _view_of(prim, params, src: Loc, ty) -> Loc | None:
+    """The layout op ``prim`` of ``src`` as a strided view, or None when strides cannot express it."""
+    if prim == "transpose":
+        perm = params["permutation"]
+        return Loc(src.base, src.offset, tuple(src.strides[d] for d in perm), ty.dtype, ty.shape)
+    if prim == "broadcast_in_dim":
+        dims = params["broadcast_dimensions"]
+        st = [0] * len(ty.shape)
+        for i, d in enumerate(dims):
+            st[d] = 0 if src.shape[i] == 1 else src.strides[i]
+        return Loc(src.base, src.offset, tuple(st), ty.dtype, ty.shape)
+    if prim == "slice":
+        off = src.offset + sum(s * st for s, st in zip(params["start_indices"], src.strides))
+        return Loc(src.base, off, src.strides, ty.dtype, ty.shape)
+    if prim == "reshape":
+        if src.contiguous():
+            return Loc(src.base, src.offset, _contig(ty.shape), ty.dtype, ty.shape)
+        st = _reshape_strides(src.shape, src.strides, ty.shape)
+        return None if st is None else Loc(src.base, src.offset, st, ty.dtype, ty.shape)
+    return None
+
+
+def _reshape_strides(shape, strides, new):
+    """torch's view rule: strides for ``new`` over memory laid out as ``shape``/``strides``, or None."""
+    dims = [(n, s) for n, s in zip(shape, strides) if n != 1]
+    out = []
+    i = 0
+    for n in new:
+        if n == 1:
+            out.append(0)
+            continue
+        if i >= len(dims):
+            return None
+        size, stride = dims[i]
+        if size == n:
+            out.append(stride)
+            i += 1
+            continue
+        if size % n == 0:
+            # split a dim
+            dims[i] = (size // n, stride)
+            out.append(stride * (size // n))
+            continue
+        # merge dims while contiguous
+        acc, st = size, stride
+        j = i + 1
+        while acc < n and j < len(dims) and dims[j - 1][1] == dims[j][0] * dims[j][1]:
+            acc *= dims[j][0]
+            st = dims[j][1]
+            j += 1
+        if acc != n:
+            return None
+        out.append(st)
+        i = j
+    return tuple(out)
+
+
+def compile_graph(graph: Graph) -> Graph:
+    """The hip pipeline (``graph_compiler/pipeline.rs:162-320`` picks): frontend (cse, simplify), flash
+    attention forward and backward matching, simplify again."""
+    g = passes.frontend(graph)
+    if config.compiler.flash_attention:
+        g = attn_pass.match(g)
+        g = passes.frontend(g)
+    return g
+
+
+class Plan:
+    """A graph compiled for ``device`` (``"hip:0"``): steps, workspace layout and native step list."""
+
+    def __init__(self, graph: Graph, device="hip:0", build_kernels=True):
+        self.device = device
+        self.source_graph = graph
+        self.graph = compile_graph(graph)
+        self.steps = self._fuse()
+        self._place()
+        self.kernels = {}
+        self.sources = {}
+        self._native = None
+        self._gen_kernels()
+        if build_kernels:
+            self.build()
+
+    # ---- fusion with fallback: groups the generator rejects are split
+    def _fuse(self):
+        return fusion.fuse(self.graph, fuse_loops=config.compiler.fuse)
+
+    # ---- placement
+    def _place(self):
+        g = self.graph
+        self.loc: dict[int, Loc] = {}
+        for i, v in enumerate(g.inputs):
+            t = g.types[v]
+            self.loc[v] = Loc(("in", i), 0, _contig(t.shape), t.dtype, t.shape)
+        # views first: resolved lazily in step order; a view that strides cannot express becomes a copy
+        last_use: dict[int, int] = {}
+        base_of: dict[int, int] = {}
+        for si, st in enumerate(self.steps):
+            for u in st.inputs:
+                last_use[u] = si
+        for v in g.outputs:
+            last_use[v] = len(self.steps)
+        # a view keeps its base alive as long as it is used
+        for si in reversed(range(len(self.steps))):
+            st = self.steps[si]
+            if st.kind == "view":
+                v = st.outputs[0]
+                src = st.nodes[0].inputs[0]
+                last_use[src] = max(last_use.get(src, si), last_use.get(v, si))
+        free: list[tuple[int, int]] = []  # (offset, size)
+        top = 0
+        live: dict[int, tuple[int, int]] = {}
+
+        def take(size):
+            nonlocal top
+            size = -(-max(size, 1) // ALIGNMENT) * ALIGNMENT
+            best = None
+            for k, (off, sz) in enumerate(free):
+                if sz >= size and (best is None or sz < free[best][1]):
+                    best = k
+            if best is not None:
+                off, sz = free.pop(best)
+                if sz > size:
+                    free.append((off + size, sz - size))
+                return off, size
+            off = top
+            top += size
+            return off, size
+
+        def release(off, size):
+            free.append((off, size))
+            free.sort()
+            merged = []
+            for o, s in free:
+                if merged and merged[-1][0] + merged[-1][1] == o:
+                    merged[-1] = (merged[-1][0], merged[-1][1] + s)
+                else:
+                    merged.append((o, s))
+            free[:] = merged
+
+        converted = []
+        for si, st in enumerate(self.steps):
+            if st.kind == "view":
+                n = st.nodes[0]
+                src = self.loc[n.inputs[0]]
+                loc = _view_of(n.prim, n.params, src, g.types[n.output])
+                if loc is not None:
+                    self.loc[n.output] = loc
+                    base_of[n.output] = base_of.get(n.inputs[0], n.inputs[0])
+                    continue
+                st.kind = "loop"
+                converted.append(si)
+            for v in st.outputs:
+                t = g.types[v]
+                off, size = take(t.nbytes())
+                live[v] = (off, size)
+                self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
+            for v in list(live):
+                if last_use.get(v, -1) <= si and v not in g.outputs:
+                    off, size = live.pop(v)
+                    release(off, size)
+        self.workspace_bytes = max(top, ALIGNMENT)
+        self.workspace_alignment = ALIGNMENT
+        # graph outputs that are plan inputs (returned unchanged) are copied into the workspace
+        self.output_locs = []
+        for v in g.outputs:
+            loc = self.loc[v]
+            if loc.base[0] == "in" or not loc.contiguous():
+                t = g.types[v]
+                off = self.workspace_bytes
+                self.workspace_bytes += -(-t.nbytes() // ALIGNMENT) * ALIGNMENT
+                dst = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
+                self.steps.append(fusion.Step("copy", [], [v], [v]))
+                self._copies = getattr(self, "_copies", {})
+                self._copies[len(self.steps) - 1] = (loc, dst)
+                loc = dst
+            self.output_locs.append(loc)
+
+    # ---- kernels
+    def _gen_kernels(self):
+        g = self.graph
+        for si, st in enumerate(self.steps):
+            if st.kind not in ("loop", "row", "reduce"):
+                continue
+            views = {v: self.loc[v].view() for v in st.inputs}
+            outs = {v: self.loc[v].view() for v in st.outputs}
+            k = codegen.LoopKernel(g, st, "KNAME", views, outs)
+            body = k.source()
+            import hashlib
+
+            name = f"{st.kind}_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
+            k.name = name
+            st.name = name
+            src = codegen.HEADER + body.replace("KNAME", name)
+            self.kernels[si] = k
+            self.sources[si] = src
+
+    def build(self):
+        """Compiles every generated kernel (hipcc, cached)."""
+        keys = list(self.sources)
+        paths = kcache.compile_many([self.sources[k] for k in keys])
+        self.objects = dict(zip(keys, paths))
+
+    # ---- native
+    def _native_plan(self):
+        if self._native is not None:
+            return self._native
+        from lumen_amd import native as nv
+
+        if not hasattr(self, "objects"):
+            self.build()
+        nv.set_device(int(self.device.split(":")[1]))
+        plan = C.c_void_p()
+        nv.call("nhip_plan_create", C.byref(plan))
+        g = self.graph
+
+        def reloc(slot, loc: Loc):
+            r = nv.Reloc()
+            r.slot = slot
+            r.base = nv.NHIP_BASE_WORKSPACE if loc.base[0] == "ws" else nv.NHIP_BASE_INPUT
+            r.index = loc.base[1] if loc.base[0] == "in" else 0
+            r.offset = loc.offset * D.size_of(loc.dtype)
+            return r
+
+        for si, st in enumerate(self.steps):
+            if st.kind in ("loop", "row", "reduce"):
+                k = self.kernels[si]
+                fn = nv.module_function(self.objects[si], k.name)
+                if st.kind == "reduce" and getattr(k, "atomic", False):
+                    out = self.loc[st.outputs[0]]
+                    desc = struct.pack("<QI", g.types[st.outputs[0]].nbytes(), 0) + b"\0" * 4
+                    relocs = (nv.Reloc * 1)(reloc(0, out))
+                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), relocs, 1)
+                relocs = []
+                for j, (kind, v) in enumerate(k.args):
+                    relocs.append(reloc(8 * j, self.loc[v]))
+                args = b"\0" * (8 * len(k.args))
+                grid = (C.c_uint32 * 3)(*k.grid)
+                block = (C.c_uint32 * 3)(*k.block)
+                rr = (nv.Reloc * max(1, len(relocs)))(*relocs)
+                nv.call("nhip_plan_add_launch", plan, fn, grid, block, k.lds, args, len(args), rr, len(relocs))
+            elif st.kind == "dot":
+                desc, ops = self._gemm_desc(st.nodes[0])
+                rr = (nv.Reloc * 3)(*[reloc(i, l) for i, l in enumerate(ops)])
+                nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_GEMM, C.byref(desc), C.sizeof(desc), rr, 3)
+            elif st.kind in ("flash_fwd", "flash_bwd"):
+                kind, desc, ops = attn_pass.lower(self, st)
+                rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
+                nv.call("nhip_plan_add_builtin", plan, kind, C.byref(desc), C.sizeof(desc), rr, len(ops))
+            elif st.kind == "copy":
+                src, dst = self._copies[si]
+                desc = struct.pack("<Q", g.types[st.outputs[0]].nbytes())
+                rr = (nv.Reloc * 2)(reloc(0, dst), reloc(1, src))
+                nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
+            elif st.kind == "view":
+                continue
+            else:
+                raise NotImplementedError(f"{st.kind}: the hip backend has no kernel for it yet")
+        self._native = plan
+        return plan
+
+    def _gemm_desc(self, n):
+        """``nhip_gemm_desc`` of a dot_general node over its operands' strided locations."""
+        from lumen_amd import native as nv
+
+        g = self.graph
+        p = n.params
+        lhs, rhs = self.loc[n.inputs[0]], self.loc[n.inputs[1]]
+        out = self.loc[n.output]
+        lt, rt = g.types[n.inputs[0]], g.types[n.inputs[1]]
+        lc, rc, lb, rb = p["lhs_contracting"], p["rhs_contracting"], p["lhs_batch"], p["rhs_batch"]
+        lf = [d for d in range(len(lt.shape)) if d not in lc and d not in lb]
+        rf = [d for d in range(len(rt.shape)) if d not in rc and d not in rb]
+        if lt.dtype not in NHIP_DT or rt.dtype not in NHIP_DT or (lt.dtype == "float32") != (rt.dtype == "float32"):
+            raise NotImplementedError(f"dot_general of {lt.dtype} and {rt.dtype}: the hip backend has no kernel for it yet")
+        if lt.dtype != rt.dtype:
+            raise NotImplementedError(f"dot_general of {lt.dtype} and {rt.dtype}: the hip backend has no kernel for it yet")
+        if p["output_dtype"] not in NHIP_DT:
+            raise NotImplementedError(f"dot_general to {p['output_dtype']}: the hip backend has no kernel for it yet")
+
+        def collapse(loc, dims, what):
+            """One (size, stride) for ``dims`` of ``loc``, which must be collapsible."""
+            dims = [d for d in dims if loc.shape[d] != 1]
+            if not dims:
+                return 1, 0
+            size = loc.shape[dims[-1]]
+            stride = loc.strides[dims[-1]]
+            for a, b in zip(reversed(dims[:-1]), reversed(dims[1:])):
+                if loc.strides[a] != loc.strides[b] * loc.shape[b]:
+                    raise NotImplementedError(f"dot_general: {what} dimensions are not collapsible in memory")
+                size *= loc.shape[a]
+            return size, stride
+
+        m, a_m = collapse(lhs, lf, "lhs free")
+        k, a_k = collapse(lhs, list(lc), "lhs contracting")
+        k2, b_k = collapse(rhs, list(rc), "rhs contracting")
+        nn_, b_n = collapse(rhs, rf, "rhs free")
+        # output dims: batch, lhs free, rhs free
+        nb = len(lb)
+        od = list(range(nb))
+        o_lf = list(range(nb, nb + len(lf)))
+        o_rf = list(range(nb + len(lf), nb + len(lf) + len(rf)))
+        m2, d_m = collapse(out, o_lf, "output rows")
+        n2, d_n = collapse(out, o_rf, "output columns")
+        batches = [(lt.shape[lb[i]], lhs.strides[lb[i]], rhs.strides[rb[i]], out.strides[od[i]]) for i in range(nb)]
+        batches = [b for b in batches if b[0] != 1]
+        if len(batches) > 3:
+            raise NotImplementedError("dot_general with more than 3 batch dimensions")
+        d = nv.GemmDesc()
+        d.m, d.n, d.k = m, nn_, k
+        d.nbatch = len(batches)
+        d.a_dtype, d.b_dtype, d.d_dtype = NHIP_DT[lt.dtype], NHIP_DT[rt.dtype], NHIP_DT[p["output_dtype"]]
+        for i, (size, sa, sb, sd) in enumerate(batches):
+            d.batch[i], d.a_batch[i], d.b_batch[i], d.d_batch[i] = size, sa, sb, sd
+        d.a_m, d.a_k, d.b_k, d.b_n, d.d_m, d.d_n = a_m, a_k, b_k, b_n, d_m, d_n
+        d.config = -1
+        return d, [lhs, rhs, out]
+
+    def run_in(self, workspace_ptr: int, input_ptrs: list):
+        """Queues the plan on the stream: inputs are device pointers in graph-input order."""
+        from lumen_amd import native as nv
+
+        plan = self._native_plan()
+        arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
+        nv.call("nhip_plan_run", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs))
+
+    def __del__(self):
+        if getattr(self, "_native", None) is not None:
+            try:
+                from lumen_amd import native as nv
+
+                nv.lib().nhip_plan_destroy(self._native)
+            except Exception:
+                pass
+
+    def describe(self):
+        """One line per step: its kind, name and label (``Plan.steps()``)."""
+        return [
+            {"kind": st.kind, "name": st.name, "label": st.label(), "outputs": list(st.outputs)} for st in self.steps
+        ]
+
+
+_ = math

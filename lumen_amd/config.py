@@ -1,0 +1,47 @@
+"""``lumen_amd.config``: compiler flags the hip pipeline reads (``lumen/graph_compiler/config/mod.rs:82-133``)
+and the static region size (``lumen/allocator/config.rs:14-25``)."""
+
+from __future__ import annotations
+
+import contextlib
+import dataclasses
+
+
+@dataclasses.dataclass
+class CompilerFlags:
+    fuse: bool = True                 # loop fusion of elementwise/row work
+    flash_attention: bool = True      # match attention (forward and backward) into flash kernels
+    merge_dots: bool = True           # one dot for dots sharing an operand (QKV)
+    horizontal_fusion: bool = True    # merge small independent loop kernels into one launch
+    epilogue_fusion: bool = True      # fuse elementwise consumers into GEMM stores
+    autotune: bool = False            # time GEMM tile candidates at plan compile
+    deterministic: bool = True        # attention backward without atomics
+    _version: int = 0
+
+    def __setattr__(self, name, value):
+        object.__setattr__(self, name, value)
+        if name != "_version":
+            object.__setattr__(self, "_version", self._version + 1)
+
+    @contextlib.contextmanager
+    def patch(self, **flags):
+        old = {k: getattr(self, k) for k in flags}
+        for k, v in flags.items():
+            setattr(self, k, v)
+        try:
+            yield self
+        finally:
+            for k, v in old.items():
+                setattr(self, k, v)
+
+    def key(self):
+        return tuple((f.name, getattr(self, f.name)) for f in dataclasses.fields(self) if f.name != "_version")
+
+
+@dataclasses.dataclass
+class Config:
+    compiler: CompilerFlags = dataclasses.field(default_factory=CompilerFlags)
+    static_allocator_bytes: int = 1 << 30
+
+
+config = Config()

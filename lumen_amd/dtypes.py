@@ -114,7 +114,7 @@ def _round_to_odd_f32(x: np.ndarray) -> np.ndarray:
     x = np.asarray(x, np.float64)
     t = x.astype(np.float32)  # nearest
     back = t.astype(np.float64)
-    inexact = (back != x) & np.isfinite(x)
+    inexact = (back != x) & np.isfinite(t)
     bits_ = t.view(np.uint32).copy()
     # step toward zero if rounding went away from x, then force the low bit
     away = inexact & (np.abs(back) > np.abs(x))

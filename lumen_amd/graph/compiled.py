@@ -1,0 +1,153 @@
+"""``lumen_amd.compile`` and ``Compiled`` (``lumen/graph/tracer.py:693-1141``).
+
+A compiled function traces its Python function once per signature (tensor dtypes and shapes, module
+structure, static values; floats are runtime scalars), compiles a ``Plan`` for the device, allocates the
+plan's workspace once, and on each call passes its arguments, scalars and the modules' placed weights to the
+plan, returns views of the results in the workspace (the next call overwrites them) and writes weights the
+function assigned back into their memory.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+
+from lumen_amd import nn
+from lumen_amd.config import config
+from lumen_amd.graph.trace import trace, tree_leaves
+from lumen_amd.tensor import DeviceBuffer, Tensor, device_name, device_type, empty
+
+
+def compile(fn, device=None):
+    """``fn`` compiled for ``device`` (``"hip"``; ``"meta"`` compiles without running): see ``Compiled``."""
+    return Compiled(fn, device)
+
+
+class Compiled:
+    def __init__(self, fn, device=None):
+        functools.update_wrapper(self, fn)
+        self._fn = fn
+        self._device = None if device is None else device_name(device)
+        self._plans = {}
+        self._latest = None
+
+    def _target(self, args):
+        if self._device is not None:
+            return self._device
+        tensors = [a for a in args if isinstance(a, Tensor)]
+        data = [a for a in tensors if device_type(a.device) != "meta"]
+        return data[0].device if data else ("meta:0" if tensors else "hip:0")
+
+    def _key(self, args, target):
+        return (tuple(nn.structure(a) for a in args), target, config.compiler.key())
+
+    def _prepare(self, args):
+        target = self._target(args)
+        if device_type(target) == "cpu":
+            raise RuntimeError(
+                "device='cpu' is lumen's reference interpreter; this backend compiles for 'hip' (and 'meta')"
+            )
+        key = self._key(args, target)
+        entry = self._plans.get(key)
+        if entry is None:
+            traced = trace(self._fn, args)
+            plan, workspace = None, None
+            if device_type(target) == "hip":
+                from lumen_amd.compiler.plan import Plan
+
+                plan = Plan(traced.graph, target)
+                workspace = DeviceBuffer(int(target.split(":")[1]), plan.workspace_bytes)
+                for w in traced.weights:
+                    w._placed(target)
+            entry = (traced, plan, workspace)
+            self._plans[key] = entry
+        self._latest = key
+        return target, entry
+
+    @property
+    def plan(self):
+        return self._plans[self._latest][1]
+
+    @property
+    def graph(self):
+        return self._plans[self._latest][0].graph
+
+    def __call__(self, *args):
+        target, (traced, plan, workspace) = self._prepare(args)
+        g = traced.graph
+        ran = plan is not None and not any(isinstance(a, Tensor) and device_type(a.device) == "meta" for a in args)
+        if not ran:
+            outs = [Tensor(g.types[v].dtype, g.types[v].shape, "meta") for v in g.outputs]
+        else:
+            keep = []
+            ptrs = []
+            tensors = [a for a in args if isinstance(a, Tensor)]
+            scalars = _scalars(args)
+            for kind, k in traced.layout:
+                if kind == "arg":
+                    t = tensors[k]
+                    if device_name(t.device) != target:
+                        t = t.to(device=target)
+                    keep.append(t)
+                    ptrs.append(t.data_ptr())
+                elif kind == "scalar":
+                    t = Tensor("float64", (), "cpu", host=np.array(scalars[k], np.float64)).to(device=target)
+                    keep.append(t)
+                    ptrs.append(t.data_ptr())
+                else:
+                    t = traced.weights[k]._placed(target)
+                    keep.append(t)
+                    ptrs.append(t.data_ptr())
+            plan.run_in(workspace.ptr, ptrs)
+            outs = []
+            for v, loc in zip(g.outputs, plan.output_locs):
+                t = Tensor(loc.dtype, loc.shape, target, buffer=workspace, offset=loc.offset * _size(loc.dtype))
+                outs.append(t)
+            # weights the function assigned: written back into their memory, in stream order
+            for j, k in enumerate(traced.written):
+                traced.weights[k]._placed(target).copy_(outs[traced.n_returned + j])
+            self._keep = keep
+        for i, path, value in traced.static_writes:
+            nn.assign(args[i], path, value)
+        it = iter(outs)
+        return _rebuild(traced.out, it)
+
+
+def _size(dtype):
+    from lumen_amd import dtypes as D
+
+    return D.size_of(dtype)
+
+
+def _scalars(args):
+    out = []
+    for a in args:
+        if isinstance(a, float):
+            out.append(a)
+    # module floats follow the top-level ones in trace order
+    res = []
+    for a in args:
+        if isinstance(a, float):
+            res.append(a)
+        elif isinstance(a, (nn.Module, list, tuple)):
+            for path in nn.scalar_paths(a):
+                res.append(nn.at(a, path))
+    return res
+
+
+def _rebuild(out, it):
+    from lumen_amd.graph.tracer import TracedTensor
+
+    if isinstance(out, TracedTensor):
+        return next(it)
+    if isinstance(out, (list, tuple)):
+        return type(out)(_rebuild(v, it) for v in out)
+    if isinstance(out, dict):
+        return {k: _rebuild(v, it) for k, v in out.items()}
+    if isinstance(out, nn.Module):
+        return nn.map_tensors(out, lambda t: next(it))
+    return out
+
+
+_ = (tree_leaves, empty)

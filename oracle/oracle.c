@@ -1,0 +1,1110 @@
+/*
+ * TEST INFRASTRUCTURE: the CPU oracle the hip backend is checked against. Only tests/, the smoke check
+ * and bench.py's cpu_baseline leg load it; no product path calls it.
+ *
+ * A C restatement of lumen's reference interpreter, lumen/reference/mod.rs: every value is held widened
+ * (integers and bools as __int128, floats as double), each primitive is evaluated element by element in
+ * that precision and its result rounded once to the output dtype (`round`, mod.rs:189-209; bfloat16 and
+ * float16 through round-to-odd float32 then round to nearest even, lumen/tensor/dtype.rs:215-239).
+ * Reductions and the dot fold run in row-major input order with a rounding after every step
+ * (mod.rs:668-718, 981-993). Integer arithmetic wraps to the dtype (mod.rs:189-209), float->int casts
+ * saturate with NaN -> 0 (mod.rs:226-243).
+ *
+ * Graphs arrive in a line-oriented text format written by oracle/oracle.py (`serialize`).
+ */
+#include <ctype.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef __int128 i128;
+
+/* ---- dtypes ------------------------------------------------------------------------------------------ */
+
+enum { BOOL, U8, U16, U32, U64, I8, I16, I32, I64, F16, BF16, F32, F64, NDTYPES };
+static const char *DT_NAMES[] = {"bool", "uint8", "uint16", "uint32", "uint64", "int8", "int16",
+                                 "int32", "int64", "float16", "bfloat16", "float32", "float64"};
+static const int DT_BITS[] = {1, 8, 16, 32, 64, 8, 16, 32, 64, 16, 16, 32, 64};
+static int is_float(int d) { return d >= F16; }
+
+static char g_err[1024];
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+/* ---- rounding (lumen/tensor/dtype.rs:215-239, reference/mod.rs:189-243) ------------------------------ */
+
+static float round_to_odd(double x) {
+    float f = (float)x;
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    if (!isfinite(f) || (double)f == x || (bits & 1)) return f;
+    int outward = ((double)f < x) != (signbit(f) != 0);
+    bits = outward ? bits + 1 : bits - 1;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+static double bf16_bits_to_double(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even, overflow to infinity, subnormals kept. */
+static uint16_t f32_to_f16_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t exp = (u >> 23) & 0xffu;
+    uint32_t man = u & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u | (man >> 13) : 0));
+    int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        int shift = 14 - e;
+        uint32_t half = 1u << (shift - 1);
+        uint32_t rest = man & ((1u << shift) - 1);
+        uint32_t r = man >> shift;
+        if (rest > half || (rest == half && (r & 1))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rest = man & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (r & 1))) r++;
+    return (uint16_t)(sign | r);
+}
+static double f16_bits_to_double(uint16_t h) {
+    int sign = h >> 15, exp = (h >> 10) & 0x1f, man = h & 0x3ff;
+    double v;
+    if (exp == 0) v = ldexp((double)man, -24);
+    else if (exp == 31) v = man ? NAN : INFINITY;
+    else v = ldexp((double)(man | 0x400), exp - 25);
+    return sign ? -v : v;
+}
+
+static double round_to(double x, int d) {
+    switch (d) {
+        case F16: return f16_bits_to_double(f32_to_f16_bits(round_to_odd(x)));
+        case BF16: return bf16_bits_to_double(f32_to_bf16_bits(round_to_odd(x)));
+        case F32: return (double)(float)x;
+        default: return x;
+    }
+}
+
+static i128 wrap(i128 x, int d) {
+    switch (d) {
+        case BOOL: return x != 0;
+        case U8: return (uint8_t)x;
+        case U16: return (uint16_t)x;
+        case U32: return (uint32_t)x;
+        case U64: return (uint64_t)x;
+        case I8: return (int8_t)x;
+        case I16: return (int16_t)x;
+        case I32: return (int32_t)x;
+        default: return (int64_t)x;
+    }
+}
+
+/* Rust's saturating `f64 as int` (NaN to 0). */
+static i128 saturate(double x, int d) {
+    if (d == BOOL) return x != 0.0;
+    if (isnan(x)) return 0;
+    double lo, hi;
+    switch (d) {
+        case U8: lo = 0, hi = 255; break;
+        case U16: lo = 0, hi = 65535; break;
+        case U32: lo = 0, hi = 4294967295.0; break;
+        case U64: lo = 0, hi = 18446744073709551615.0; break;
+        case I8: lo = -128, hi = 127; break;
+        case I16: lo = -32768, hi = 32767; break;
+        case I32: lo = -2147483648.0, hi = 2147483647.0; break;
+        default: lo = -9223372036854775808.0, hi = 9223372036854775807.0; break;
+    }
+    if (x <= lo) {
+        if (d == I64) return (i128)INT64_MIN;
+        return (i128)lo;
+    }
+    if (x >= hi) {
+        if (d == U64) return (i128)UINT64_MAX;
+        if (d == I64) return (i128)INT64_MAX;
+        return (i128)hi;
+    }
+    return (i128)trunc(x);
+}
+
+/* ---- values and graphs ------------------------------------------------------------------------------- */
+
+typedef struct {
+    int is_float;
+    size_t n;
+    double *f;
+    i128 *i;
+} Values;
+
+typedef struct {
+    int dtype, rank;
+    int64_t shape[8];
+} Type;
+
+typedef struct Graph Graph;
+
+typedef struct {
+    char key[32];
+    char kind; /* 'i' ints, 'd' dtype, 'f' float, 'n' int, 'b' bool, 'g' graph */
+    int nints;
+    int64_t ints[16];
+    int dtype;
+    double fval;
+    int64_t ival;
+    Graph *body;
+} Param;
+
+typedef struct {
+    char name[40];
+    int out, nin, ins[64], nparams;
+    Param params[8];
+} Node;
+
+struct Graph {
+    int ntypes, ninputs, nnodes, noutputs;
+    Type *types;
+    int *inputs, *outputs;
+    Node *nodes;
+};
+
+static size_t numel(const Type *t) {
+    size_t n = 1;
+    for (int i = 0; i < t->rank; ++i) n *= (size_t)t->shape[i];
+    return n;
+}
+
+static Values vnew(int is_float, size_t n) {
+    Values v = {is_float, n, NULL, NULL};
+    if (is_float) v.f = (double *)calloc(n ? n : 1, sizeof(double));
+    else v.i = (i128 *)calloc(n ? n : 1, sizeof(i128));
+    return v;
+}
+static void vfree(Values *v) {
+    free(v->f);
+    free(v->i);
+    v->f = NULL;
+    v->i = NULL;
+}
+static Values vclone(const Values *a) {
+    Values v = vnew(a->is_float, a->n);
+    if (a->is_float) memcpy(v.f, a->f, a->n * sizeof(double));
+    else memcpy(v.i, a->i, a->n * sizeof(i128));
+    return v;
+}
+
+static const Param *param(const Node *n, const char *key) {
+    for (int i = 0; i < n->nparams; ++i)
+        if (!strcmp(n->params[i].key, key)) return &n->params[i];
+    return NULL;
+}
+static const Param *need(const Node *n, const char *key) {
+    const Param *p = param(n, key);
+    if (!p) {
+        fprintf(stderr, "oracle: %s needs parameter %s\n", n->name, key);
+        abort();
+    }
+    return p;
+}
+
+/* ---- parsing -------------------------------------------------------------------------------------------- */
+
+typedef struct {
+    const char *s;
+} Cursor;
+
+static int next_token(Cursor *c, char *buf, size_t cap) {
+    while (*c->s && isspace((unsigned char)*c->s)) c->s++;
+    if (!*c->s) return 0;
+    size_t n = 0;
+    while (*c->s && !isspace((unsigned char)*c->s)) {
+        if (n + 1 < cap) buf[n++] = *c->s;
+        c->s++;
+    }
+    buf[n] = 0;
+    return 1;
+}
+static long long next_int(Cursor *c) {
+    char b[64];
+    next_token(c, b, sizeof b);
+    return strtoll(b, NULL, 10);
+}
+static int dtype_of(const char *name) {
+    for (int i = 0; i < NDTYPES; ++i)
+        if (!strcmp(name, DT_NAMES[i])) return i;
+    fprintf(stderr, "oracle: unknown dtype %s\n", name);
+    abort();
+}
+
+static Graph *parse_graph(Cursor *c);
+
+static void parse_param(Cursor *c, Param *p) {
+    char tok[4096];
+    next_token(c, p->key, sizeof p->key);
+    next_token(c, tok, sizeof tok);
+    p->kind = tok[0];
+    const char *v = tok + 2;
+    switch (p->kind) {
+        case 'i': {
+            p->nints = (int)strtol(v, (char **)&v, 10);
+            if (*v == ':') v++;
+            for (int k = 0; k < p->nints; ++k) {
+                p->ints[k] = strtoll(v, (char **)&v, 10);
+                if (*v == ',') v++;
+            }
+            break;
+        }
+        case 'd': p->dtype = dtype_of(v); break;
+        case 'f': p->fval = strtod(v, NULL); break;
+        case 'n': p->ival = strtoll(v, NULL, 10); break;
+        case 'b': p->ival = atoi(v); break;
+        case 'g': p->body = parse_graph(c); break;
+    }
+}
+
+static Graph *parse_graph(Cursor *c) {
+    char tok[256];
+    Graph *g = (Graph *)calloc(1, sizeof(Graph));
+    next_token(c, tok, sizeof tok); /* "graph" */
+    next_token(c, tok, sizeof tok); /* "types" */
+    g->ntypes = (int)next_int(c);
+    g->types = (Type *)calloc(g->ntypes ? g->ntypes : 1, sizeof(Type));
+    for (int i = 0; i < g->ntypes; ++i) {
+        next_token(c, tok, sizeof tok);
+        g->types[i].dtype = dtype_of(tok);
+        g->types[i].rank = (int)next_int(c);
+        for (int d = 0; d < g->types[i].rank; ++d) g->types[i].shape[d] = next_int(c);
+    }
+    next_token(c, tok, sizeof tok); /* "inputs" */
+    g->ninputs = (int)next_int(c);
+    g->inputs = (int *)calloc(g->ninputs ? g->ninputs : 1, sizeof(int));
+    for (int i = 0; i < g->ninputs; ++i) g->inputs[i] = (int)next_int(c);
+    next_token(c, tok, sizeof tok); /* "nodes" */
+    g->nnodes = (int)next_int(c);
+    g->nodes = (Node *)calloc(g->nnodes ? g->nnodes : 1, sizeof(Node));
+    for (int i = 0; i < g->nnodes; ++i) {
+        Node *n = &g->nodes[i];
+        next_token(c, n->name, sizeof n->name);
+        n->out = (int)next_int(c);
+        n->nin = (int)next_int(c);
+        for (int k = 0; k < n->nin; ++k) n->ins[k] = (int)next_int(c);
+        n->nparams = (int)next_int(c);
+        for (int k = 0; k < n->nparams; ++k) parse_param(c, &n->params[k]);
+    }
+    next_token(c, tok, sizeof tok); /* "outputs" */
+    g->noutputs = (int)next_int(c);
+    g->outputs = (int *)calloc(g->noutputs ? g->noutputs : 1, sizeof(int));
+    for (int i = 0; i < g->noutputs; ++i) g->outputs[i] = (int)next_int(c);
+    next_token(c, tok, sizeof tok); /* "end" */
+    return g;
+}
+
+static void free_graph(Graph *g) {
+    if (!g) return;
+    for (int i = 0; i < g->nnodes; ++i)
+        for (int k = 0; k < g->nodes[i].nparams; ++k)
+            if (g->nodes[i].params[k].kind == 'g') free_graph(g->nodes[i].params[k].body);
+    free(g->types);
+    free(g->inputs);
+    free(g->outputs);
+    free(g->nodes);
+    free(g);
+}
+
+/* ---- index helpers ------------------------------------------------------------------------------------ */
+
+static void strides_of(const Type *t, int64_t *st) {
+    int64_t s = 1;
+    for (int d = t->rank - 1; d >= 0; --d) {
+        st[d] = s;
+        s *= t->shape[d];
+    }
+}
+
+/* Advances a row-major multi-index over `shape`; returns 0 when it wraps around. */
+static int step_index(int64_t *idx, const int64_t *shape, int rank) {
+    for (int d = rank - 1; d >= 0; --d) {
+        if (++idx[d] < shape[d]) return 1;
+        idx[d] = 0;
+    }
+    return 0;
+}
+
+static int contains(const int64_t *xs, int n, int64_t v) {
+    for (int i = 0; i < n; ++i)
+        if (xs[i] == v) return 1;
+    return 0;
+}
+
+static int64_t clampi(i128 k, int64_t lo, int64_t hi) { return k < lo ? lo : (k > hi ? hi : (int64_t)k); }
+
+/* ---- erf_inv, reduce_precision, nextafter (reference/mod.rs:282-420) ---------------------------------- */
+
+static double erf_inv(double x) {
+    if (fabs(x) == 1.0) return x * INFINITY;
+    double w = -log((1.0 - x) * (1.0 + x)), p;
+    if (w < 5.0) {
+        static const double c[] = {2.81022636e-08, 3.43273939e-07, -3.5233877e-06, -4.39150654e-06, 0.00021858087,
+                                   -0.00125372503, -0.00417768164, 0.246640727, 1.50140941};
+        w -= 2.5;
+        p = 0;
+        for (int i = 0; i < 9; ++i) p = c[i] + p * w;
+    } else {
+        static const double c[] = {-0.000200214257, 0.000100950558, 0.00134934322, -0.00367342844, 0.00573950773,
+                                   -0.0076224613,   0.00943887047,  1.00167406,    2.83297682};
+        w = sqrt(w) - 3.0;
+        p = 0;
+        for (int i = 0; i < 9; ++i) p = c[i] + p * w;
+    }
+    return p * x;
+}
+
+static double reduce_precision(double x, int eb, int mb) {
+    if (isnan(x)) return x;
+    uint64_t b;
+    memcpy(&b, &x, 8);
+    if (mb < 52) {
+        uint64_t last = 1ull << (52 - mb);
+        uint64_t bias = (last >> 1) - 1 + ((b & last) >> (52 - mb));
+        b = (b + bias) & ~(last - 1);
+    }
+    if (eb < 11) {
+        uint64_t rb = (1ull << (eb - 1)) - 1;
+        uint64_t e = b & 0x7FF0000000000000ull, sign = b & 0x8000000000000000ull;
+        if (e > ((1023 + rb) << 52)) b = sign | 0x7FF0000000000000ull;
+        else if (e <= ((1023 - rb) << 52)) b = sign;
+    }
+    memcpy(&x, &b, 8);
+    return x;
+}
+
+static uint64_t na_step(uint64_t bits, uint64_t sign, int up, double x, double y) {
+    if ((bits & ~sign) == 0) return (y > x ? 0 : sign) | 1;
+    if (up == ((bits & sign) == 0)) return bits + 1;
+    return bits - 1;
+}
+static double next_after(double x, double y, int d) {
+    if (isnan(x) || isnan(y)) return NAN;
+    if (x == y) return y;
+    int up = y > x;
+    if (d == F32) {
+        float f = (float)x;
+        uint32_t b;
+        memcpy(&b, &f, 4);
+        b = (uint32_t)na_step(b, 1u << 31, up, x, y);
+        memcpy(&f, &b, 4);
+        return f;
+    }
+    if (d == F16) return f16_bits_to_double((uint16_t)na_step(f32_to_f16_bits(round_to_odd(x)), 1u << 15, up, x, y));
+    if (d == BF16) return bf16_bits_to_double((uint16_t)na_step(f32_to_bf16_bits(round_to_odd(x)), 1u << 15, up, x, y));
+    uint64_t b;
+    memcpy(&b, &x, 8);
+    b = na_step(b, 1ull << 63, up, x, y);
+    memcpy(&x, &b, 8);
+    return x;
+}
+
+static double fmax_nan(double a, double b) { return (isnan(a) || isnan(b)) ? NAN : (a > b ? a : b); }
+static double fmin_nan(double a, double b) { return (isnan(a) || isnan(b)) ? NAN : (a < b ? a : b); }
+
+/* Philox4x32-10 (reference/mod.rs:1162-1188). */
+static uint32_t philox_bits(uint64_t key, uint64_t counter) {
+    uint32_t k0 = (uint32_t)key, k1 = (uint32_t)(key >> 32);
+    uint32_t c0 = (uint32_t)counter, c1 = (uint32_t)(counter >> 32), c2 = 0, c3 = 0;
+    for (int r = 0; r < 10; ++r) {
+        if (r > 0) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0, hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        uint32_t n0 = hi1 ^ c1 ^ k0, n1 = lo1, n2 = hi0 ^ c3 ^ k1, n3 = lo0;
+        c0 = n0, c1 = n1, c2 = n2, c3 = n3;
+    }
+    return c0;
+}
+
+uint32_t oracle_philox(uint64_t key, uint64_t counter) { return philox_bits(key, counter); }
+
+/* ---- evaluation (reference/mod.rs:465-1151) ----------------------------------------------------------- */
+
+static Values *eval_graph(const Graph *g, Values *inputs);
+
+static i128 unsigned_bits(i128 x, int w) {
+    if (w >= 128) return x;
+    return (i128)((unsigned __int128)x & ((((unsigned __int128)1) << w) - 1));
+}
+static i128 signed_bits(i128 x, int w) {
+    i128 b = unsigned_bits(x, w);
+    if (w > 0 && b >= ((i128)1 << (w - 1))) return b - ((i128)1 << w);
+    return b;
+}
+static int popcount128(unsigned __int128 x) {
+    return __builtin_popcountll((uint64_t)x) + __builtin_popcountll((uint64_t)(x >> 64));
+}
+
+static Values gather_by(const Values *x, size_t n, const int64_t *src) {
+    Values v = vnew(x->is_float, n);
+    for (size_t k = 0; k < n; ++k) {
+        if (x->is_float) v.f[k] = x->f[src[k]];
+        else v.i[k] = x->i[src[k]];
+    }
+    return v;
+}
+
+static Values eval_node(const Node *nd, Values **args, const Type **types, const Type *out) {
+    const char *p = nd->name;
+    int dt = out->dtype;
+    size_t n = numel(out);
+#define IS(s) (!strcmp(p, s))
+    if (IS("add") || IS("sub") || IS("mul") || IS("div") || IS("max") || IS("eq") || IS("lt")) {
+        const Values *x = args[0], *y = args[1];
+        if (!x->is_float) {
+            Values v = vnew(0, n);
+            for (size_t k = 0; k < n; ++k) {
+                i128 a = x->i[k], b = y->i[k], r;
+                if (IS("add")) r = a + b;
+                else if (IS("sub")) r = a - b;
+                else if (IS("mul")) r = (i128)((unsigned __int128)a * (unsigned __int128)b);
+                else if (IS("div")) r = b == 0 ? -1 : a / b;
+                else if (IS("max")) r = a > b ? a : b;
+                else if (IS("eq")) r = a == b;
+                else r = a < b;
+                v.i[k] = wrap(r, dt);
+            }
+            return v;
+        }
+        if (IS("eq") || IS("lt")) {
+            Values v = vnew(0, n);
+            for (size_t k = 0; k < n; ++k) v.i[k] = IS("eq") ? x->f[k] == y->f[k] : x->f[k] < y->f[k];
+            return v;
+        }
+        Values v = vnew(1, n);
+        for (size_t k = 0; k < n; ++k) {
+            double a = x->f[k], b = y->f[k], r;
+            if (IS("add")) r = a + b;
+            else if (IS("sub")) r = a - b;
+            else if (IS("mul")) r = a * b;
+            else if (IS("div")) r = a / b;
+            else r = fmax_nan(a, b);
+            v.f[k] = round_to(r, dt);
+        }
+        return v;
+    }
+    if (IS("neg")) {
+        Values v = vnew(args[0]->is_float, n);
+        for (size_t k = 0; k < n; ++k) {
+            if (v.is_float) v.f[k] = -args[0]->f[k];
+            else v.i[k] = wrap(-args[0]->i[k], dt);
+        }
+        return v;
+    }
+    if (IS("exp") || IS("log") || IS("sqrt") || IS("tanh") || IS("logistic")) {
+        Values v = vnew(1, n);
+        for (size_t k = 0; k < n; ++k) {
+            double a = args[0]->f[k], r;
+            if (IS("exp")) r = exp(a);
+            else if (IS("log")) r = log(a);
+            else if (IS("sqrt")) r = sqrt(a);
+            else if (IS("tanh")) r = tanh(a);
+            else r = 1.0 / (1.0 + exp(-a));
+            v.f[k] = round_to(r, dt);
+        }
+        return v;
+    }
+    if (IS("cast")) {
+        const Values *x = args[0];
+        Values v = vnew(is_float(dt), n);
+        for (size_t k = 0; k < n; ++k) {
+            if (!x->is_float && is_float(dt)) {
+                i128 a = x->i[k];
+                v.f[k] = dt == F64 ? (double)a : dt == F32 ? (double)(float)a : round_to((double)a, dt);
+            } else if (!x->is_float) {
+                v.i[k] = wrap(x->i[k], dt);
+            } else if (is_float(dt)) {
+                v.f[k] = round_to(x->f[k], dt);
+            } else {
+                v.i[k] = saturate(x->f[k], dt);
+            }
+        }
+        return v;
+    }
+    if (IS("select")) {
+        Values v = vnew(args[1]->is_float, n);
+        for (size_t k = 0; k < n; ++k) {
+            int c = args[0]->i[k] != 0;
+            if (v.is_float) v.f[k] = c ? args[1]->f[k] : args[2]->f[k];
+            else v.i[k] = c ? args[1]->i[k] : args[2]->i[k];
+        }
+        return v;
+    }
+    if (IS("reduce_sum") || IS("reduce_max")) {
+        const Type *x = types[0];
+        const Param *ax = need(nd, "axes");
+        int sum = IS("reduce_sum");
+        int64_t ost[8], xst[8], idx[8] = {0};
+        strides_of(out, ost);
+        /* output stride each input dim moves by (0 for a reduced dim) */
+        int od = 0;
+        for (int d = 0; d < x->rank; ++d) {
+            if (contains(ax->ints, ax->nints, d)) xst[d] = 0;
+            else xst[d] = ost[od++];
+        }
+        Values v = vnew(args[0]->is_float, n);
+        for (size_t k = 0; k < n; ++k) {
+            if (v.is_float) v.f[k] = sum ? 0.0 : -INFINITY;
+            else if (sum) v.i[k] = 0;
+            else {
+                int s = dt == I8 || dt == I16 || dt == I32 || dt == I64;
+                v.i[k] = s ? -((i128)1 << (DT_BITS[dt] - 1)) : 0;
+            }
+        }
+        size_t total = numel(x);
+        for (size_t e = 0; e < total; ++e) {
+            int64_t t = 0;
+            for (int d = 0; d < x->rank; ++d) t += idx[d] * xst[d];
+            if (v.is_float) v.f[t] = sum ? round_to(v.f[t] + args[0]->f[e], dt) : fmax_nan(v.f[t], args[0]->f[e]);
+            else v.i[t] = sum ? wrap(v.i[t] + args[0]->i[e], dt) : (v.i[t] > args[0]->i[e] ? v.i[t] : args[0]->i[e]);
+            step_index(idx, x->shape, x->rank);
+        }
+        return v;
+    }
+    if (IS("cumsum")) {
+        const Type *x = types[0];
+        int axis = (int)need(nd, "axis")->ival;
+        int reverse = (int)need(nd, "reverse")->ival;
+        int64_t len = x->shape[axis], b = 1;
+        for (int d = axis + 1; d < x->rank; ++d) b *= x->shape[d];
+        size_t lines = len ? n / len : 0;
+        Values v = vnew(args[0]->is_float, n);
+        for (size_t line = 0; line < lines; ++line) {
+            size_t i = line / b, j = line % b;
+            double sf = 0.0;
+            i128 si = 0;
+            for (int64_t kk = 0; kk < len; ++kk) {
+                int64_t kx = reverse ? len - 1 - kk : kk;
+                size_t e = (i * len + kx) * b + j;
+                if (v.is_float) v.f[e] = sf = round_to(sf + args[0]->f[e], dt);
+                else v.i[e] = si = wrap(si + args[0]->i[e], dt);
+            }
+        }
+        return v;
+    }
+    if (IS("dot_general")) {
+        const Type *l = types[0], *r = types[1];
+        const Param *lc = need(nd, "lhs_contracting"), *rc = need(nd, "rhs_contracting");
+        const Param *lb = need(nd, "lhs_batch"), *rb = need(nd, "rhs_batch");
+        int accum = need(nd, "accum_dtype")->dtype;
+        int64_t lst[8], rst[8];
+        strides_of(l, lst);
+        strides_of(r, rst);
+        int lfree[8], rfree[8], nlf = 0, nrf = 0;
+        for (int d = 0; d < l->rank; ++d)
+            if (!contains(lc->ints, lc->nints, d) && !contains(lb->ints, lb->nints, d)) lfree[nlf++] = d;
+        for (int d = 0; d < r->rank; ++d)
+            if (!contains(rc->ints, rc->nints, d) && !contains(rb->ints, rb->nints, d)) rfree[nrf++] = d;
+        int nc = lc->nints;
+        int64_t cshape[8], cl[8], cr[8];
+        size_t csize = 1;
+        for (int i = 0; i < nc; ++i) {
+            cshape[i] = l->shape[lc->ints[i]];
+            cl[i] = lst[lc->ints[i]];
+            cr[i] = rst[rc->ints[i]];
+            csize *= (size_t)cshape[i];
+        }
+        Values v = vnew(args[0]->is_float, n);
+        int64_t oidx[8] = {0};
+        for (size_t o = 0; o < n; ++o) {
+            int64_t lo = 0, ro = 0, pos = 0;
+            for (int i = 0; i < lb->nints; ++i, ++pos) {
+                lo += oidx[pos] * lst[lb->ints[i]];
+                ro += oidx[pos] * rst[rb->ints[i]];
+            }
+            for (int i = 0; i < nlf; ++i, ++pos) lo += oidx[pos] * lst[lfree[i]];
+            for (int i = 0; i < nrf; ++i, ++pos) ro += oidx[pos] * rst[rfree[i]];
+            int64_t cidx[8] = {0};
+            if (v.is_float) {
+                double acc = 0.0;
+                const double *xf = args[0]->f, *yf = args[1]->f;
+                if (nc == 1) {
+                    int64_t sl = cl[0], sr = cr[0];
+                    for (int64_t c = 0; c < cshape[0]; ++c)
+                        acc = round_to(acc + round_to(xf[lo + c * sl] * yf[ro + c * sr], accum), accum);
+                } else if (csize) {
+                    do {
+                        int64_t a = lo, b = ro;
+                        for (int i = 0; i < nc; ++i) a += cidx[i] * cl[i], b += cidx[i] * cr[i];
+                        acc = round_to(acc + round_to(xf[a] * yf[b], accum), accum);
+                    } while (step_index(cidx, cshape, nc));
+                }
+                v.f[o] = round_to(acc, dt);
+            } else {
+                i128 acc = 0;
+                if (csize) {
+                    do {
+                        int64_t a = lo, b = ro;
+                        for (int i = 0; i < nc; ++i) a += cidx[i] * cl[i], b += cidx[i] * cr[i];
+                        acc = wrap(acc + (i128)((unsigned __int128)args[0]->i[a] * (unsigned __int128)args[1]->i[b]), dt);
+                    } while (step_index(cidx, cshape, nc));
+                }
+                v.i[o] = wrap(acc, dt);
+            }
+            step_index(oidx, out->shape, out->rank);
+        }
+        return v;
+    }
+    if (IS("reshape") || IS("host_wait") || IS("device_wait") || IS("to_host") || IS("to_device"))
+        return vclone(args[0]);
+    if (IS("broadcast_in_dim") || IS("transpose") || IS("slice") || IS("swap_pairs")) {
+        const Type *x = types[0];
+        int64_t xst[8], idx[8] = {0};
+        strides_of(x, xst);
+        int64_t *src = (int64_t *)malloc((n ? n : 1) * sizeof(int64_t));
+        for (size_t k = 0; k < n; ++k) {
+            int64_t s = 0;
+            if (IS("broadcast_in_dim")) {
+                const Param *bd = need(nd, "broadcast_dimensions");
+                for (int i = 0; i < bd->nints; ++i) s += (x->shape[i] == 1 ? 0 : idx[bd->ints[i]]) * xst[i];
+            } else if (IS("transpose")) {
+                const Param *pm = need(nd, "permutation");
+                for (int i = 0; i < pm->nints; ++i) s += idx[i] * xst[pm->ints[i]];
+            } else if (IS("slice")) {
+                const Param *st = need(nd, "start_indices");
+                for (int i = 0; i < x->rank; ++i) s += (idx[i] + st->ints[i]) * xst[i];
+            } else {
+                for (int i = 0; i < x->rank; ++i) s += (i == x->rank - 1 ? (idx[i] ^ 1) : idx[i]) * xst[i];
+            }
+            src[k] = s;
+            step_index(idx, out->shape, out->rank);
+        }
+        Values v = gather_by(args[0], n, src);
+        free(src);
+        return v;
+    }
+    if (IS("concatenate")) {
+        int d = (int)need(nd, "dimension")->ival;
+        Values v = vnew(args[0]->is_float, n);
+        int64_t idx[8] = {0};
+        int nops = nd->nin;
+        for (size_t k = 0; k < n; ++k) {
+            int64_t c = idx[d];
+            int op = 0;
+            while (op < nops - 1 && c >= types[op]->shape[d]) c -= types[op++]->shape[d];
+            int64_t st[8], s = 0;
+            strides_of(types[op], st);
+            for (int i = 0; i < out->rank; ++i) s += (i == d ? c : idx[i]) * st[i];
+            if (v.is_float) v.f[k] = args[op]->f[s];
+            else v.i[k] = args[op]->i[s];
+            step_index(idx, out->shape, out->rank);
+        }
+        return v;
+    }
+    if (IS("full")) {
+        const Param *fv = need(nd, "fill_value");
+        Values v = vnew(is_float(dt), n);
+        for (size_t k = 0; k < n; ++k) {
+            if (is_float(dt)) v.f[k] = round_to(fv->kind == 'f' ? fv->fval : (double)fv->ival, dt);
+            else if (fv->kind == 'f') v.i[k] = saturate(fv->fval, dt);
+            else v.i[k] = wrap(fv->ival, dt);
+        }
+        return v;
+    }
+    if (IS("iota")) {
+        int d = (int)need(nd, "dimension")->ival;
+        Values v = vnew(is_float(dt), n);
+        int64_t idx[8] = {0};
+        for (size_t k = 0; k < n; ++k) {
+            if (is_float(dt)) v.f[k] = round_to((double)idx[d], dt);
+            else v.i[k] = wrap(idx[d], dt);
+            step_index(idx, out->shape, out->rank);
+        }
+        return v;
+    }
+    if (IS("gather")) {
+        const Type *x = types[0], *ix = types[1];
+        int axis = (int)need(nd, "axis")->ival;
+        int64_t xst[8], ist[8], idx[8] = {0};
+        strides_of(x, xst);
+        strides_of(ix, ist);
+        int64_t *src = (int64_t *)malloc((n ? n : 1) * sizeof(int64_t));
+        int64_t hi = x->shape[axis] - 1 < 0 ? 0 : x->shape[axis] - 1;
+        for (size_t k = 0; k < n; ++k) {
+            int64_t at = 0, s = 0;
+            for (int i = 0; i < ix->rank; ++i) at += idx[axis + i] * ist[i];
+            int64_t pick = clampi(args[1]->i[at], 0, hi);
+            for (int i = 0; i < axis; ++i) s += idx[i] * xst[i];
+            s += pick * xst[axis];
+            for (int i = axis + 1; i < x->rank; ++i) s += idx[i - 1 + ix->rank] * xst[i];
+            src[k] = s;
+            step_index(idx, out->shape, out->rank);
+        }
+        Values v = gather_by(args[0], n, src);
+        free(src);
+        return v;
+    }
+    if (IS("take_along_axis")) {
+        const Type *x = types[0];
+        int axis = (int)need(nd, "axis")->ival;
+        int64_t xst[8], idx[8] = {0};
+        strides_of(x, xst);
+        int64_t *src = (int64_t *)malloc((n ? n : 1) * sizeof(int64_t));
+        int64_t hi = x->shape[axis] - 1 < 0 ? 0 : x->shape[axis] - 1;
+        for (size_t k = 0; k < n; ++k) {
+            int64_t pick = clampi(args[1]->i[k], 0, hi), s = 0;
+            for (int i = 0; i < x->rank; ++i) s += (i == axis ? pick : idx[i]) * xst[i];
+            src[k] = s;
+            step_index(idx, out->shape, out->rank);
+        }
+        Values v = gather_by(args[0], n, src);
+        free(src);
+        return v;
+    }
+    if (IS("scatter_add")) {
+        const Type *x = types[0], *ix = types[1], *u = types[2];
+        int axis = (int)need(nd, "axis")->ival;
+        int64_t xst[8], ist[8], idx[8] = {0};
+        strides_of(x, xst);
+        strides_of(ix, ist);
+        Values v = vclone(args[0]);
+        size_t un = numel(u);
+        int64_t hi = x->shape[axis] - 1 < 0 ? 0 : x->shape[axis] - 1;
+        for (size_t k = 0; k < un; ++k) {
+            int64_t at = 0, s = 0;
+            for (int i = 0; i < ix->rank; ++i) at += idx[axis + i] * ist[i];
+            int64_t pick = clampi(args[1]->i[at], 0, hi);
+            for (int i = 0; i < axis; ++i) s += idx[i] * xst[i];
+            s += pick * xst[axis];
+            for (int i = axis + 1; i < x->rank; ++i) s += idx[i - 1 + ix->rank] * xst[i];
+            if (v.is_float) v.f[s] = round_to(v.f[s] + args[2]->f[k], dt);
+            else v.i[s] = wrap(v.i[s] + args[2]->i[k], dt);
+            step_index(idx, u->shape, u->rank);
+        }
+        return v;
+    }
+    if (IS("dynamic_slice") || IS("dynamic_update_slice")) {
+        int upd = IS("dynamic_update_slice");
+        const Type *x = types[0];
+        const Type *blk = upd ? types[1] : out;
+        int first = upd ? 2 : 1;
+        int64_t xst[8], st[8], idx[8] = {0};
+        strides_of(x, xst);
+        for (int d = 0; d < x->rank; ++d) st[d] = clampi(args[first + d]->i[0], 0, x->shape[d] - blk->shape[d]);
+        size_t bn = numel(blk);
+        Values v = upd ? vclone(args[0]) : vnew(args[0]->is_float, n);
+        for (size_t k = 0; k < bn; ++k) {
+            int64_t s = 0;
+            for (int d = 0; d < x->rank; ++d) s += (idx[d] + st[d]) * xst[d];
+            if (upd) {
+                if (v.is_float) v.f[s] = args[1]->f[k];
+                else v.i[s] = args[1]->i[k];
+            } else {
+                if (v.is_float) v.f[k] = args[0]->f[s];
+                else v.i[k] = args[0]->i[s];
+            }
+            step_index(idx, blk->shape, blk->rank);
+        }
+        return v;
+    }
+    if (IS("random_bits")) {
+        uint64_t seed = (uint64_t)args[0]->i[0], start = (uint64_t)args[1]->i[0] + (uint64_t)need(nd, "offset")->ival;
+        Values v = vnew(0, n);
+        for (size_t k = 0; k < n; ++k) v.i[k] = philox_bits(seed, start + k);
+        return v;
+    }
+    if (IS("linear_cross_entropy")) {
+        int64_t b = types[0]->shape[0], d = types[0]->shape[1], vv = types[1]->shape[0];
+        Values v = vnew(1, n);
+        double *logits = (double *)malloc((vv ? vv : 1) * sizeof(double));
+        for (int64_t i = 0; i < b; ++i) {
+            for (int64_t j = 0; j < vv; ++j) {
+                double acc = 0.0;
+                for (int64_t k = 0; k < d; ++k)
+                    acc = round_to(acc + round_to(args[0]->f[i * d + k] * args[1]->f[j * d + k], F32), F32);
+                logits[j] = acc;
+            }
+            double mx = -INFINITY, s = 0.0;
+            for (int64_t j = 0; j < vv; ++j) mx = mx > logits[j] ? mx : logits[j];
+            for (int64_t j = 0; j < vv; ++j) s += exp(logits[j] - mx);
+            int64_t cls = clampi(args[2]->i[i], 0, vv - 1);
+            double l = round_to(mx + log(s), F32);
+            v.f[i] = round_to(l - logits[cls], F32);
+            v.f[b + i] = l;
+        }
+        free(logits);
+        return v;
+    }
+    if (IS("fusion")) {
+        const Param *body = need(nd, "body");
+        Values *ins = (Values *)calloc(nd->nin ? nd->nin : 1, sizeof(Values));
+        for (int i = 0; i < nd->nin; ++i) ins[i] = vclone(args[i]);
+        Values *outs = eval_graph(body->body, ins);
+        for (int i = 0; i < nd->nin; ++i) vfree(&ins[i]);
+        free(ins);
+        Values r = outs[0];
+        for (int i = 1; i < body->body->noutputs; ++i) vfree(&outs[i]);
+        free(outs);
+        return r;
+    }
+    /* unary ops beyond the core set */
+    if (nd->nin == 1) {
+        const Values *x = args[0];
+        int w = DT_BITS[types[0]->dtype];
+        if (IS("is_finite")) {
+            Values v = vnew(0, n);
+            for (size_t k = 0; k < n; ++k) v.i[k] = isfinite(x->f[k]);
+            return v;
+        }
+        if (!x->is_float) {
+            Values v = vnew(0, n);
+            for (size_t k = 0; k < n; ++k) {
+                i128 a = x->i[k], r;
+                if (IS("abs")) r = wrap(a < 0 ? -a : a, dt);
+                else if (IS("sign")) r = a > 0 ? 1 : (a < 0 ? -1 : 0);
+                else if (IS("not")) r = types[0]->dtype == BOOL ? 1 - a : wrap(~a, dt);
+                else if (IS("population_count")) r = popcount128((unsigned __int128)unsigned_bits(a, w));
+                else if (IS("clz")) {
+                    unsigned __int128 u = (unsigned __int128)unsigned_bits(a, w);
+                    int c = 0;
+                    for (int bit = w - 1; bit >= 0 && !((u >> bit) & 1); --bit) c++;
+                    r = c;
+                } else {
+                    set_err("%s of an integer", p);
+                    return vnew(0, n);
+                }
+                v.i[k] = r;
+            }
+            return v;
+        }
+        Values v = vnew(1, n);
+        for (size_t k = 0; k < n; ++k) {
+            double a = x->f[k], r;
+            if (IS("sin")) r = sin(a);
+            else if (IS("cos")) r = cos(a);
+            else if (IS("tan")) r = tan(a);
+            else if (IS("asin")) r = asin(a);
+            else if (IS("acos")) r = acos(a);
+            else if (IS("atan")) r = atan(a);
+            else if (IS("sinh")) r = sinh(a);
+            else if (IS("cosh")) r = cosh(a);
+            else if (IS("asinh")) r = asinh(a);
+            else if (IS("acosh")) r = acosh(a);
+            else if (IS("atanh")) r = atanh(a);
+            else if (IS("floor")) r = floor(a);
+            else if (IS("ceil")) r = ceil(a);
+            else if (IS("round")) r = nearbyint(a);
+            else if (IS("log1p")) r = log1p(a);
+            else if (IS("expm1")) r = expm1(a);
+            else if (IS("exp2")) r = exp2(a);
+            else if (IS("log2")) r = log2(a);
+            else if (IS("rsqrt")) r = 1.0 / sqrt(a);
+            else if (IS("cbrt")) r = cbrt(a);
+            else if (IS("erf_inv")) r = erf_inv(a);
+            else if (IS("reduce_precision"))
+                r = reduce_precision(a, (int)need(nd, "exponent_bits")->ival, (int)need(nd, "mantissa_bits")->ival);
+            else if (IS("abs")) r = fabs(a);
+            else if (IS("sign")) r = (a == 0.0 || isnan(a)) ? a : (a > 0 ? 1.0 : -1.0);
+            else {
+                set_err("unknown primitive %s", p);
+                r = NAN;
+            }
+            v.f[k] = round_to(r, dt);
+        }
+        return v;
+    }
+    /* binary ops beyond the core set */
+    {
+        const Values *x = args[0], *y = args[1];
+        int w = DT_BITS[types[0]->dtype];
+        if (!x->is_float) {
+            Values v = vnew(0, n);
+            for (size_t k = 0; k < n; ++k) {
+                i128 a = x->i[k], b = y->i[k], r;
+                if (IS("rem")) r = b == 0 ? a : a % b;
+                else if (IS("min")) r = a < b ? a : b;
+                else if (IS("and")) r = wrap(a & b, dt);
+                else if (IS("or")) r = wrap(a | b, dt);
+                else if (IS("xor")) r = wrap(a ^ b, dt);
+                else if (b < 0 || b >= w) r = (IS("shift_right_arithmetic") && signed_bits(a, w) < 0) ? wrap(-1, dt) : 0;
+                else if (IS("shift_left")) r = wrap((i128)((unsigned __int128)a << (int)b), dt);
+                else if (IS("shift_right_logical")) r = wrap(unsigned_bits(a, w) >> (int)b, dt);
+                else if (IS("shift_right_arithmetic")) r = wrap(signed_bits(a, w) >> (int)b, dt);
+                else {
+                    set_err("unknown primitive %s", p);
+                    r = 0;
+                }
+                v.i[k] = r;
+            }
+            return v;
+        }
+        Values v = vnew(1, n);
+        for (size_t k = 0; k < n; ++k) {
+            double a = x->f[k], r;
+            if (!y->is_float) r = round_to(pow(a, (double)y->i[k]), dt);
+            else if (IS("pow")) r = round_to(pow(a, y->f[k]), dt);
+            else if (IS("rem")) r = round_to(fmod(a, y->f[k]), dt);
+            else if (IS("min")) r = fmin_nan(a, y->f[k]);
+            else if (IS("nextafter")) r = next_after(a, y->f[k], dt);
+            else {
+                set_err("unknown primitive %s", p);
+                r = NAN;
+            }
+            v.f[k] = r;
+        }
+        return v;
+    }
+#undef IS
+}
+
+static Values *eval_graph(const Graph *g, Values *inputs) {
+    Values *env = (Values *)calloc(g->ntypes ? g->ntypes : 1, sizeof(Values));
+    char *have = (char *)calloc(g->ntypes ? g->ntypes : 1, 1);
+    /* extra outputs of multi-output fusions, read by fusion_output */
+    Values **extra = (Values **)calloc(g->ntypes ? g->ntypes : 1, sizeof(Values *));
+    int *nextra = (int *)calloc(g->ntypes ? g->ntypes : 1, sizeof(int));
+    for (int i = 0; i < g->ninputs; ++i) {
+        env[g->inputs[i]] = vclone(&inputs[i]);
+        have[g->inputs[i]] = 1;
+    }
+    for (int i = 0; i < g->nnodes; ++i) {
+        const Node *nd = &g->nodes[i];
+        Values *args[64];
+        const Type *types[64];
+        for (int k = 0; k < nd->nin; ++k) {
+            args[k] = &env[nd->ins[k]];
+            types[k] = &g->types[nd->ins[k]];
+        }
+        const Param *body = param(nd, "body");
+        if (!strcmp(nd->name, "fusion") && body && body->body->noutputs > 1) {
+            Values *ins = (Values *)calloc(nd->nin ? nd->nin : 1, sizeof(Values));
+            for (int k = 0; k < nd->nin; ++k) ins[k] = vclone(args[k]);
+            Values *outs = eval_graph(body->body, ins);
+            for (int k = 0; k < nd->nin; ++k) vfree(&ins[k]);
+            free(ins);
+            env[nd->out] = outs[0];
+            extra[nd->out] = outs;
+            nextra[nd->out] = body->body->noutputs;
+        } else if (!strcmp(nd->name, "fusion_output")) {
+            int index = (int)need(nd, "index")->ival;
+            env[nd->out] = vclone(&extra[nd->ins[0]][index]);
+        } else {
+            env[nd->out] = eval_node(nd, args, types, &g->types[nd->out]);
+        }
+        have[nd->out] = 1;
+    }
+    Values *outs = (Values *)calloc(g->noutputs ? g->noutputs : 1, sizeof(Values));
+    for (int i = 0; i < g->noutputs; ++i) outs[i] = vclone(&env[g->outputs[i]]);
+    for (int v = 0; v < g->ntypes; ++v) {
+        if (have[v]) vfree(&env[v]);
+        if (extra[v]) {
+            for (int k = 1; k < nextra[v]; ++k) vfree(&extra[v][k]);
+            free(extra[v]);
+        }
+    }
+    free(env);
+    free(have);
+    free(extra);
+    free(nextra);
+    return outs;
+}
+
+/* ---- raw buffers <-> values ------------------------------------------------------------------------------ */
+
+static Values load(const void *p, const Type *t) {
+    size_t n = numel(t);
+    int d = t->dtype;
+    Values v = vnew(is_float(d), n);
+    for (size_t k = 0; k < n; ++k) {
+        switch (d) {
+            case BOOL: v.i[k] = ((const uint8_t *)p)[k] != 0; break;
+            case U8: v.i[k] = ((const uint8_t *)p)[k]; break;
+            case U16: v.i[k] = ((const uint16_t *)p)[k]; break;
+            case U32: v.i[k] = ((const uint32_t *)p)[k]; break;
+            case U64: v.i[k] = ((const uint64_t *)p)[k]; break;
+            case I8: v.i[k] = ((const int8_t *)p)[k]; break;
+            case I16: v.i[k] = ((const int16_t *)p)[k]; break;
+            case I32: v.i[k] = ((const int32_t *)p)[k]; break;
+            case I64: v.i[k] = ((const int64_t *)p)[k]; break;
+            case F16: v.f[k] = f16_bits_to_double(((const uint16_t *)p)[k]); break;
+            case BF16: v.f[k] = bf16_bits_to_double(((const uint16_t *)p)[k]); break;
+            case F32: v.f[k] = ((const float *)p)[k]; break;
+            default: v.f[k] = ((const double *)p)[k]; break;
+        }
+    }
+    return v;
+}
+
+static void store(const Values *v, void *p, const Type *t) {
+    size_t n = numel(t);
+    int d = t->dtype;
+    for (size_t k = 0; k < n; ++k) {
+        double f = v->is_float ? v->f[k] : 0;
+        i128 i = v->is_float ? 0 : v->i[k];
+        switch (d) {
+            case BOOL: ((uint8_t *)p)[k] = (uint8_t)(i != 0); break;
+            case U8: ((uint8_t *)p)[k] = (uint8_t)i; break;
+            case U16: ((uint16_t *)p)[k] = (uint16_t)i; break;
+            case U32: ((uint32_t *)p)[k] = (uint32_t)i; break;
+            case U64: ((uint64_t *)p)[k] = (uint64_t)i; break;
+            case I8: ((int8_t *)p)[k] = (int8_t)i; break;
+            case I16: ((int16_t *)p)[k] = (int16_t)i; break;
+            case I32: ((int32_t *)p)[k] = (int32_t)i; break;
+            case I64: ((int64_t *)p)[k] = (int64_t)i; break;
+            case F16: ((uint16_t *)p)[k] = f32_to_f16_bits(round_to_odd(f)); break;
+            case BF16: ((uint16_t *)p)[k] = f32_to_bf16_bits(round_to_odd(f)); break;
+            case F32: ((float *)p)[k] = (float)f; break;
+            default: ((double *)p)[k] = f; break;
+        }
+    }
+}
+
+/* ---- C entry points (ctypes) ------------------------------------------------------------------------------- */
+
+const char *oracle_error(void) { return g_err; }
+
+/* Evaluates the serialized graph `text` on raw input buffers, writing each output's storage into
+ * `outputs[i]` (sized by the graph's output types). Returns 0 on success. */
+int oracle_run(const char *text, const void *const *inputs, void *const *outputs) {
+    g_err[0] = 0;
+    Cursor c = {text};
+    Graph *g = parse_graph(&c);
+    Values *ins = (Values *)calloc(g->ninputs ? g->ninputs : 1, sizeof(Values));
+    for (int i = 0; i < g->ninputs; ++i) ins[i] = load(inputs[i], &g->types[g->inputs[i]]);
+    Values *outs = eval_graph(g, ins);
+    for (int i = 0; i < g->noutputs; ++i) {
+        store(&outs[i], outputs[i], &g->types[g->outputs[i]]);
+        vfree(&outs[i]);
+    }
+    for (int i = 0; i < g->ninputs; ++i) vfree(&ins[i]);
+    free(ins);
+    free(outs);
+    free_graph(g);
+    return g_err[0] ? 1 : 0;
+}
+
+/* Rounding helpers exposed for the known-answer tests. */
+uint16_t oracle_to_bf16(double x) { return f32_to_bf16_bits(round_to_odd(x)); }
+uint16_t oracle_to_f16(double x) { return f32_to_f16_bits(round_to_odd(x)); }
+float oracle_round_to_odd(double x) { return round_to_odd(x); }
+double oracle_erf_inv(double x) { return erf_inv(x); }
+double oracle_reduce_precision(double x, int eb, int mb) { return reduce_precision(x, eb, mb); }

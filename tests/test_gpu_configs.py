@@ -1,0 +1,50 @@
+"""Parity of compiled plans on the GPU against the CPU oracle (the reference interpreter's restatement)."""
+
+import numpy as np
+import pytest
+
+import lumen_amd as L
+import lumen_amd.functional as F
+from lumen_amd import dtypes as D
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(a):
+    return D.bf16_bits(np.asarray(a, np.float32))
+
+
+def test_config1_relu_matmul_f32_is_bit_exact(hip):
+    """relu(matmul(x, w)) in float32: the plan's dot is the reference's sequential fold, so the GPU result
+    equals the oracle bit for bit."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((256, 512)).astype(np.float32)
+    w = rng.standard_normal((512, 1024)).astype(np.float32)
+    f = L.compile(lambda x, w: F.relu(F.matmul(x, w, "float32", "float32")), device="hip")
+    got = L.to_numpy(f(L.from_numpy(x), L.from_numpy(w)))
+    (want,) = oracle.run(L.make_graph(lambda x, w: F.relu(F.matmul(x, w, "float32", "float32")))(L.from_numpy(x), L.from_numpy(w)), [x, w])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _chain(x, a, b):
+    t = (x * a + b).float()
+    t = F.gelu(t)
+    t = F.layer_norm(t, x.shape[-1])
+    return F.softmax(t, -1).bfloat16()
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (37, 512), (16, 64), (8, 1000)])
+def test_config2_fused_chain_matches_oracle(hip, rows, cols):
+    """layernorm(gelu(x*a+b)) then softmax, bf16 in and out, float32 statistics: one row kernel, within
+    the bf16 tolerance (rtol 2e-2, atol 1e-2)."""
+    rng = np.random.default_rng(1)
+    x = _bf16(rng.standard_normal((rows, cols)))
+    a = _bf16(1.0 + 0.1 * rng.standard_normal(cols))
+    b = _bf16(0.1 * rng.standard_normal(cols))
+    args = [L.tensor(D.bf16_to_f32(v), "bfloat16") for v in (x, a, b)]
+    f = L.compile(_chain, device="hip")
+    got = L.to_numpy(f(*args))
+    assert [s["kind"] for s in f.plan.describe()] == ["row"]
+    (want,) = oracle.values(L.make_graph(_chain)(*args), [x, a, b])
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2)
