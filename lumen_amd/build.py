@@ -1,0 +1,49 @@
+"""Builds libnhip.so (the native runtime and built-in kernels) for gfx950 with hipcc.
+
+``python -m lumen_amd.build`` or ``__graft_entry__.build()``. Host code is C++17, device code HIP for gfx950
+only; packed FP32 instructions are disabled and FMA contraction is off (exact rounding of fused code).
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "libnhip.so")
+SOURCES = ["runtime.cpp", "kernels.hip"]
+FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-fPIC",
+    "-shared",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-Wno-unused-result",
+    "-Wl,--no-undefined",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def build(verbose=False):
+    """Compiles libnhip.so from csrc/ (always: this is the build check)."""
+    from lumen_amd.compiler.kcache import hipcc
+
+    cmd = [hipcc()] + FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", OUT + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("libnhip build failed:\n" + r.stderr[-6000:])
+    os.replace(OUT + ".tmp", OUT)
+    if verbose:
+        print("built", OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

@@ -1,8 +1,470 @@
-// Flash attention kernels for gfx950 (placeholder entry points; the kernels follow).
+// Flash attention for gfx950: forward, and the FlashAttention-2 backward as three kernels (delta, dK/dV per
+// key block, dQ per query block), following the algorithm of lumen/codegen/attention/triton/kernel.py:34-256.
+//
+// Layout choices (all MFMA v_mfma_f32_32x32x16_{bf16,f16}, float32 accumulation):
+//  * The forward computes S^T = K Q^T, so the 32x32 C layout puts one query in each lane (lane % 32) and its
+//    keys in the accumulator registers: the running max and sum of a query row never leave its lane but for
+//    one exchange between the two half-waves. P^T then is, register for register, the B operand of
+//    O^T = V^T P^T once the k order of the MFMA is permuted to match: lane half h holds keys
+//    {4h..4h+3, 8+4h..8+4h+3} of each 16-key step, and V^T is read with that same key order from LDS by two
+//    ds_read_tr16_b64 (4 consecutive keys at one head-dim column each). O^T accumulates in registers, one
+//    query a lane, so the per-query rescale of the online softmax is a multiply by a lane scalar.
+//  * K tiles are read row-wise with ds_read_b128 (pitch D + 8 elements: conflict-free for 8 lanes), V
+//    tiles transposed with ds_read_tr16_b64 (pitch D + 16: four rows of 32 bytes on disjoint banks).
+//  * P is rounded to the inputs' dtype before P V, as the reference does (kernel.py:99); LSE = m + log(l).
 #pragma once
 
 #include "device_common.h"
 #include "nhip_internal.h"
+
+namespace nhipk {
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+template <bool F16>
+__device__ __forceinline__ uint16_t to_half_bits(float f) {
+    return F16 ? f32_to_f16(f) : f32_to_bf16(f);
+}
+
+template <bool F16>
+__device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                       0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                        c, 0, 0, 0);
+}
+
+// Two transposed 64-bit LDS reads: 4 consecutive rows at one column each, concatenated (8 x 16-bit).
+__device__ __forceinline__ uint4 read_tr_pair(const uint16_t *p0, const uint16_t *p1) {
+    v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(p0));
+    v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(p1));
+    uint2 x = __builtin_bit_cast(uint2, a), y = __builtin_bit_cast(uint2, b);
+    return make_uint4(x.x, x.y, y.x, y.y);
+}
+
+struct AttnParams {
+    const uint16_t *q, *k, *v, *o_in, *d_o;
+    uint16_t *o, *dq, *dk, *dv;
+    float *lse;
+    const float *lse_in;
+    float *delta;
+    int64_t sq, sk, heads, kv_heads;
+    int64_t q_b, q_s, q_n, k_b, k_s, k_n, v_b, v_s, v_n, o_b, o_s, o_n;
+    int64_t do_b, do_s, do_n, dq_b, dq_s, dq_n, dk_b, dk_s, dk_n, dv_b, dv_s, dv_n;
+    float scale;
+};
+
+// ---- forward ------------------------------------------------------------------------------------------
+
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_fwd_kernel(AttnParams p) {
+    constexpr int BN = 64;                 // keys per tile
+    constexpr int PK = D + 8, PV = D + 16; // LDS pitches (elements)
+    constexpr int DS = D / 16;             // k-steps over the head dim
+    constexpr int DT = D / 32;             // 32-wide head-dim tiles of O^T
+    __shared__ __align__(16) uint16_t Ks[BN * PK];
+    __shared__ __align__(16) uint16_t Vs[BN * PV];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nkv = n / (p.heads / p.kv_heads);
+    const int64_t q0 = int64_t(blockIdx.x) * 128;
+    const int64_t qi = q0 + wave * 32 + l32;  // this lane's query
+    const bool qvalid = qi < p.sq;
+
+    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+
+    uint4 qf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t)
+        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+
+    f32x16_t acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    const int64_t shift = p.sk - p.sq;  // bottom-right aligned causal mask: key <= query + shift
+    int64_t kend = p.sk;
+    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
+    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int64_t k0 = int64_t(kt) * BN;
+        // cooperative tile loads: BN rows x D columns, 16 bytes a thread per pass
+        constexpr int CH = D / 8;
+#pragma unroll
+        for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
+            int r = idx / CH, c = idx % CH;
+            int64_t key = k0 + r;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+            if (key < p.sk) {
+                kv = *reinterpret_cast<const uint4 *>(kp + key * p.k_s + c * 8);
+                vv = *reinterpret_cast<const uint4 *>(vp + key * p.v_s + c * 8);
+            }
+            *reinterpret_cast<uint4 *>(Ks + r * PK + c * 8) = kv;
+            *reinterpret_cast<uint4 *>(Vs + r * PV + c * 8) = vv;
+        }
+        __syncthreads();
+
+        // S^T for the two 32-key halves of the tile
+        f32x16_t s[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[ks][e] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DS; ++t) {
+                uint4 a = *reinterpret_cast<const uint4 *>(Ks + (32 * ks + l32) * PK + 16 * t + 8 * h);
+                s[ks] = mfma32<F16>(a, qf[t], s[ks]);
+            }
+        }
+        // scale, mask, running max
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                int64_t key = k0 + 32 * ks + 8 * (e / 4) + 4 * h + (e % 4);
+                float x = s[ks][e] * p.scale;
+                bool ok = key < p.sk && (!CAUSAL || key <= qi + shift);
+                x = ok ? x : -INFINITY;
+                s[ks][e] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = (mnew == -INFINITY) ? 1.0f : __expf(m - mnew);
+        float rs = 0.0f;
+        uint4 pb[4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    float e0 = (mnew == -INFINITY) ? 0.0f : __expf(s[ks][8 * half + j] - mnew);
+                    float e1 = (mnew == -INFINITY) ? 0.0f : __expf(s[ks][8 * half + j + 1] - mnew);
+                    rs += e0 + e1;
+                    w[j / 2] = uint32_t(to_half_bits<F16>(e0)) | (uint32_t(to_half_bits<F16>(e1)) << 16);
+                }
+                pb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+        rs += __shfl_xor(rs, 32, 64);
+        l = l * alpha + rs;
+        m = mnew;
+#pragma unroll
+        for (int i = 0; i < DT; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][e] *= alpha;
+        // O^T += V^T P^T, 16 keys a step in the permuted order
+        const int g = lane >> 4, s16 = lane & 15;
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+            const int key0 = 16 * t2 + 4 * h + s16 / 4;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                uint4 a = read_tr_pair(Vs + key0 * PV + col, Vs + (key0 + 8) * PV + col);
+                acc[dt] = mfma32<F16>(a, pb[t2], acc[dt]);
+            }
+        }
+        __syncthreads();
+    }
+
+    if (!qvalid) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    uint16_t *op = p.o + b * p.o_b + n * p.o_n + qi * p.o_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            uint32_t w0 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 0] * inv)) |
+                          (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 1] * inv)) << 16);
+            uint32_t w1 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 2] * inv)) |
+                          (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 3] * inv)) << 16);
+            *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
+        }
+    if (h == 0 && p.lse) p.lse[(b * p.heads + n) * p.sq + qi] = m + __logf(l);
+}
+
+
+// ---- backward ---------------------------------------------------------------------------------------------
+
+// delta[b, n, q] = sum_d dO * O in float32 (flash.py:67-68 computes it as a dot); one wavefront a query row.
+template <bool F16>
+__device__ __forceinline__ float half_to_f32(uint16_t v) {
+    return F16 ? f16_to_f32(v) : bf16_to_f32(v);
+}
+
+template <int D, bool F16>
+__global__ __launch_bounds__(256) void flash_delta_kernel_t(AttnParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t b = blockIdx.y;
+    if (row >= p.heads * p.sq) return;
+    const int64_t n = row / p.sq, q = row % p.sq;
+    const uint16_t *o = p.o_in + b * p.o_b + n * p.o_n + q * p.o_s;
+    const uint16_t *g = p.d_o + b * p.do_b + n * p.do_n + q * p.do_s;
+    float acc = 0.0f;
+    for (int d = lane; d < D; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
+    acc = wave_sum(acc);
+    if (lane == 0) p.delta[(b * p.heads + n) * p.sq + q] = acc;
+}
+
+// dK and dV for 128 keys (32 a wavefront), looping over 64-query tiles of every query head that shares
+// the key/value head (grouped-query attention sums them, flash.py:80-84).
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p) {
+    constexpr int BM = 64;
+    constexpr int PQ = D + 16;  // Q and dO tiles: row reads and transposed reads
+    constexpr int DS = D / 16, DT = D / 32;
+    __shared__ __align__(16) uint16_t Qs[BM * PQ];
+    __shared__ __align__(16) uint16_t Gs[BM * PQ];
+    __shared__ float Ls[BM], Ds[BM];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t b = blockIdx.z, nkv = blockIdx.y;
+    const int64_t key0 = int64_t(blockIdx.x) * 128 + wave * 32;
+    const int64_t kj = key0 + l32;  // this lane's key (C-layout column)
+    const bool kvalid = kj < p.sk;
+    const int64_t group = p.heads / p.kv_heads;
+    const int64_t shift = p.sk - p.sq;
+
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+    uint4 kf[DS], vf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+        kf[t] = kvalid ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        vf[t] = kvalid ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+    }
+    f32x16_t adk[DT], adv[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) adk[i][e] = adv[i][e] = 0.0f;
+
+    // first query that can see the workgroup's first key
+    int64_t qstart = 0;
+    if (CAUSAL) qstart = max<int64_t>(0, int64_t(blockIdx.x) * 128 - shift);
+    qstart = qstart / BM * BM;
+    for (int64_t gi = 0; gi < group; ++gi) {
+        const int64_t n = nkv * group + gi;
+        const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
+        const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
+        const float *lse = p.lse_in + (b * p.heads + n) * p.sq;
+        const float *dl = p.delta + (b * p.heads + n) * p.sq;
+        for (int64_t q0 = qstart; q0 < p.sq; q0 += BM) {
+            constexpr int CH = D / 8;
+            for (int idx = threadIdx.x; idx < BM * CH; idx += 256) {
+                int r = idx / CH, c = idx % CH;
+                int64_t q = q0 + r;
+                uint4 a = make_uint4(0, 0, 0, 0), d = make_uint4(0, 0, 0, 0);
+                if (q < p.sq) {
+                    a = *reinterpret_cast<const uint4 *>(qp + q * p.q_s + c * 8);
+                    d = *reinterpret_cast<const uint4 *>(gp + q * p.do_s + c * 8);
+                }
+                *reinterpret_cast<uint4 *>(Qs + r * PQ + c * 8) = a;
+                *reinterpret_cast<uint4 *>(Gs + r * PQ + c * 8) = d;
+            }
+            if (threadIdx.x < BM) {
+                int64_t q = q0 + threadIdx.x;
+                Ls[threadIdx.x] = q < p.sq ? lse[q] : 0.0f;
+                Ds[threadIdx.x] = q < p.sq ? dl[q] : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs) {
+                // S and dP for 32 queries (rows) x this wave's 32 keys (columns)
+                f32x16_t sv, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DS; ++t) {
+                    uint4 a = *reinterpret_cast<const uint4 *>(Qs + (32 * qs + l32) * PQ + 16 * t + 8 * h);
+                    uint4 c = *reinterpret_cast<const uint4 *>(Gs + (32 * qs + l32) * PQ + 16 * t + 8 * h);
+                    sv = mfma32<F16>(a, kf[t], sv);
+                    dp = mfma32<F16>(c, vf[t], dp);
+                }
+                uint4 pb[2], sb[2];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    uint32_t wp[4], ws[4];
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        float pv[2], dv2[2];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const int e = 8 * half + j + u;
+                            const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
+                            const int64_t q = q0 + r;
+                            bool ok = q < p.sq && kvalid && (!CAUSAL || kj <= q + shift);
+                            float x = sv[e] * p.scale;
+                            float pe = ok ? __expf(x - Ls[r]) : 0.0f;
+                            pv[u] = pe;
+                            dv2[u] = pe * (dp[e] - Ds[r]) * p.scale;
+                        }
+                        wp[j / 2] = uint32_t(to_half_bits<F16>(pv[0])) | (uint32_t(to_half_bits<F16>(pv[1])) << 16);
+                        ws[j / 2] = uint32_t(to_half_bits<F16>(dv2[0])) | (uint32_t(to_half_bits<F16>(dv2[1])) << 16);
+                    }
+                    pb[half] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
+                    sb[half] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
+                }
+                // dV^T += dO^T P and dK^T += Q^T dS, 16 queries a step in the permuted order
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int r0 = 32 * qs + 16 * half + 4 * h + s16 / 4;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                        uint4 ga = read_tr_pair(Gs + r0 * PQ + col, Gs + (r0 + 8) * PQ + col);
+                        uint4 qa = read_tr_pair(Qs + r0 * PQ + col, Qs + (r0 + 8) * PQ + col);
+                        adv[dt] = mfma32<F16>(ga, pb[half], adv[dt]);
+                        adk[dt] = mfma32<F16>(qa, sb[half], adk[dt]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (!kvalid) return;
+    uint16_t *dkp = p.dk + b * p.dk_b + nkv * p.dk_n + kj * p.dk_s;
+    uint16_t *dvp = p.dv + b * p.dv_b + nkv * p.dv_n + kj * p.dv_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int d = 32 * dt + 8 * e4 + 4 * h;
+            uint32_t k0 = uint32_t(to_half_bits<F16>(adk[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 1])) << 16);
+            uint32_t k1 = uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 3])) << 16);
+            uint32_t v0 = uint32_t(to_half_bits<F16>(adv[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 1])) << 16);
+            uint32_t v1 = uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 3])) << 16);
+            *reinterpret_cast<uint2 *>(dkp + d) = make_uint2(k0, k1);
+            *reinterpret_cast<uint2 *>(dvp + d) = make_uint2(v0, v1);
+        }
+}
+
+// dQ for 128 queries (32 a wavefront), looping over 64-key tiles: S^T and dP^T one query a lane, dQ^T
+// accumulated in registers (deterministic: no atomics).
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_dq_kernel(AttnParams p) {
+    constexpr int BN = 64;
+    constexpr int PK = D + 16, PV = D + 8;
+    constexpr int DS = D / 16, DT = D / 32;
+    __shared__ __align__(16) uint16_t Ks[BN * PK];
+    __shared__ __align__(16) uint16_t Vs[BN * PV];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nkv = n / (p.heads / p.kv_heads);
+    const int64_t q0 = int64_t(blockIdx.x) * 128;
+    const int64_t qi = q0 + wave * 32 + l32;
+    const bool qvalid = qi < p.sq;
+    const int64_t shift = p.sk - p.sq;
+
+    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
+    const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+    uint4 qf[DS], gf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        gf[t] = qvalid ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+    }
+    const float lse = qvalid ? p.lse_in[(b * p.heads + n) * p.sq + qi] : 0.0f;
+    const float dl = qvalid ? p.delta[(b * p.heads + n) * p.sq + qi] : 0.0f;
+    f32x16_t acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    int64_t kend = p.sk;
+    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
+    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int64_t k0 = int64_t(kt) * BN;
+        constexpr int CH = D / 8;
+        for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
+            int r = idx / CH, c = idx % CH;
+            int64_t key = k0 + r;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+            if (key < p.sk) {
+                kv = *reinterpret_cast<const uint4 *>(kp + key * p.k_s + c * 8);
+                vv = *reinterpret_cast<const uint4 *>(vp + key * p.v_s + c * 8);
+            }
+            *reinterpret_cast<uint4 *>(Ks + r * PK + c * 8) = kv;
+            *reinterpret_cast<uint4 *>(Vs + r * PV + c * 8) = vv;
+        }
+        __syncthreads();
+        uint4 sb[4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            f32x16_t sv, dp;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DS; ++t) {
+                uint4 a = *reinterpret_cast<const uint4 *>(Ks + (32 * ks + l32) * PK + 16 * t + 8 * h);
+                uint4 c = *reinterpret_cast<const uint4 *>(Vs + (32 * ks + l32) * PV + 16 * t + 8 * h);
+                sv = mfma32<F16>(a, qf[t], sv);
+                dp = mfma32<F16>(c, gf[t], dp);
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    float ds2[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = 8 * half + j + u;
+                        const int64_t key = k0 + 32 * ks + 8 * (e / 4) + 4 * h + (e % 4);
+                        bool ok = qvalid && key < p.sk && (!CAUSAL || key <= qi + shift);
+                        float pe = ok ? __expf(sv[e] * p.scale - lse) : 0.0f;
+                        ds2[u] = pe * (dp[e] - dl) * p.scale;
+                    }
+                    w[j / 2] = uint32_t(to_half_bits<F16>(ds2[0])) | (uint32_t(to_half_bits<F16>(ds2[1])) << 16);
+                }
+                sb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+            const int r0 = 16 * t2 + 4 * h + s16 / 4;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                uint4 a = read_tr_pair(Ks + r0 * PK + col, Ks + (r0 + 8) * PK + col);
+                acc[dt] = mfma32<F16>(a, sb[t2], acc[dt]);
+            }
+        }
+        __syncthreads();
+    }
+    if (!qvalid) return;
+    uint16_t *dqp = p.dq + b * p.dq_b + n * p.dq_n + qi * p.dq_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            uint32_t w0 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 1])) << 16);
+            uint32_t w1 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 3])) << 16);
+            *reinterpret_cast<uint2 *>(dqp + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
+        }
+}
+
+}  // namespace nhipk
 
 namespace nhip {
 
@@ -10,13 +472,102 @@ inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
     return size_t(d->batch) * d->heads * d->sq * sizeof(float);
 }
 
-int flash_fwd_on(hipStream_t, const nhip_attn_desc *, const void *, const void *, const void *, void *, float *) {
-    return fail("flash attention: the hip backend has no kernel for it yet");
+inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
+    nhipk::AttnParams p{};
+    p.sq = d->sq;
+    p.sk = d->sk;
+    p.heads = d->heads;
+    p.kv_heads = d->kv_heads;
+    p.q_b = d->q_b, p.q_s = d->q_s, p.q_n = d->q_n;
+    p.k_b = d->k_b, p.k_s = d->k_s, p.k_n = d->k_n;
+    p.v_b = d->v_b, p.v_s = d->v_s, p.v_n = d->v_n;
+    p.o_b = d->o_b, p.o_s = d->o_s, p.o_n = d->o_n;
+    p.do_b = d->do_b, p.do_s = d->do_s, p.do_n = d->do_n;
+    p.dq_b = d->dq_b, p.dq_s = d->dq_s, p.dq_n = d->dq_n;
+    p.dk_b = d->dk_b, p.dk_s = d->dk_s, p.dk_n = d->dk_n;
+    p.dv_b = d->dv_b, p.dv_s = d->dv_s, p.dv_n = d->dv_n;
+    p.scale = d->scale;
+    return p;
 }
 
-int flash_bwd_on(hipStream_t, const nhip_attn_desc *, const void *, const void *, const void *, const void *,
-                        const void *, const float *, void *, void *, void *, void *) {
-    return fail("flash attention backward: the hip backend has no kernel for it yet");
+inline int check_attn(const nhip_attn_desc *d, const char *what) {
+    if (d->head_dim != 64 && d->head_dim != 128)
+        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
+    if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
+    if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
+    if (d->batch > 65535 || d->heads > 65535) return fail(std::string(what) + ": batch and heads must be below 65536");
+    return 0;
+}
+
+template <int D, bool F16, bool CAUSAL>
+int launch_fwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
+    dim3 grid(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
+    hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
+    return check(hipGetLastError(), "flash_fwd launch");
+}
+
+int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v, void *o,
+                 float *lse) {
+    if (check_attn(d, "flash attention")) return 1;
+    if (d->sq == 0 || d->batch == 0 || d->heads == 0) return 0;
+    nhipk::AttnParams p = attn_params(d);
+    p.q = static_cast<const uint16_t *>(q);
+    p.k = static_cast<const uint16_t *>(k);
+    p.v = static_cast<const uint16_t *>(v);
+    p.o = static_cast<uint16_t *>(o);
+    p.lse = lse;
+    bool f16 = d->dtype == NHIP_F16;
+#define NHIP_FWD(DD, FF, CC) return launch_fwd<DD, FF, CC>(s, p, d)
+    if (d->head_dim == 128) {
+        if (f16) { if (d->causal) NHIP_FWD(128, true, true); NHIP_FWD(128, true, false); }
+        if (d->causal) NHIP_FWD(128, false, true);
+        NHIP_FWD(128, false, false);
+    }
+    if (f16) { if (d->causal) NHIP_FWD(64, true, true); NHIP_FWD(64, true, false); }
+    if (d->causal) NHIP_FWD(64, false, true);
+    NHIP_FWD(64, false, false);
+#undef NHIP_FWD
+}
+
+template <int D, bool F16, bool CAUSAL>
+int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
+    dim3 gd(unsigned((d->heads * d->sq + 3) / 4), unsigned(d->batch));
+    hipLaunchKernelGGL((nhipk::flash_delta_kernel_t<D, F16>), gd, dim3(256), 0, s, p);
+    if (check(hipGetLastError(), "flash delta launch")) return 1;
+    dim3 gk(unsigned((d->sk + 127) / 128), unsigned(d->kv_heads), unsigned(d->batch));
+    hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p);
+    if (check(hipGetLastError(), "flash dkdv launch")) return 1;
+    dim3 gq(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
+    hipLaunchKernelGGL((nhipk::flash_dq_kernel<D, F16, CAUSAL>), gq, dim3(256), 0, s, p);
+    return check(hipGetLastError(), "flash dq launch");
+}
+
+int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v, const void *o,
+                 const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *ws) {
+    if (check_attn(d, "flash attention backward")) return 1;
+    if (d->batch == 0 || d->heads == 0) return 0;
+    nhipk::AttnParams p = attn_params(d);
+    p.q = static_cast<const uint16_t *>(q);
+    p.k = static_cast<const uint16_t *>(k);
+    p.v = static_cast<const uint16_t *>(v);
+    p.o_in = static_cast<const uint16_t *>(o);
+    p.d_o = static_cast<const uint16_t *>(d_o);
+    p.lse_in = lse;
+    p.dq = static_cast<uint16_t *>(dq);
+    p.dk = static_cast<uint16_t *>(dk);
+    p.dv = static_cast<uint16_t *>(dv);
+    p.delta = static_cast<float *>(ws);
+    bool f16 = d->dtype == NHIP_F16;
+#define NHIP_BWD(DD, FF, CC) return launch_bwd<DD, FF, CC>(s, p, d)
+    if (d->head_dim == 128) {
+        if (f16) { if (d->causal) NHIP_BWD(128, true, true); NHIP_BWD(128, true, false); }
+        if (d->causal) NHIP_BWD(128, false, true);
+        NHIP_BWD(128, false, false);
+    }
+    if (f16) { if (d->causal) NHIP_BWD(64, true, true); NHIP_BWD(64, true, false); }
+    if (d->causal) NHIP_BWD(64, false, true);
+    NHIP_BWD(64, false, false);
+#undef NHIP_BWD
 }
 
 }  // namespace nhip
