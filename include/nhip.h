@@ -53,7 +53,7 @@ int nhip_device_props(int device, nhip_props *props);
  * 256-byte blocks by nhip_alloc. Without a reservation nhip_alloc reserves 1 GiB on first use. */
 int nhip_region_reserve(int device, size_t bytes);
 /* Takes `bytes` at a multiple of `alignment` (a power of two; 256 when 0) from the region, or with its own
- * hipMalloc when the block is larger than the region itself (a plan workspace of tens of GB). */
+ * hipMalloc when the block is larger than a quarter of the region (a plan workspace of tens of GB). */
 int nhip_alloc(int device, size_t bytes, size_t alignment, void **ptr);
 /* Returns a block nhip_alloc gave (bytes as requested). Waits for the device's queued work first, since a
  * kernel may still read it. */

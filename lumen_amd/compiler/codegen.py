@@ -50,6 +50,15 @@ DEV float r_bf16(float f) { return lb_bf16(sb_bf16(f)); }
 DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
 DEV float r_f16(float f) { return lb_f16(sb_f16(f)); }
+// float64 -> float32 rounding to odd: composes with a later round to nearest into one correct rounding
+// (lumen/tensor/dtype.rs:215-224), for float64 values cast to 16-bit floats.
+DEV float ro_f32(double x) {
+  float f = (float)x;
+  uint32_t b = __float_as_uint(f);
+  if (!isfinite(f) || (double)f == x || (b & 1u)) return f;
+  bool outward = ((double)f < x) != (f < 0.0f || (f == 0.0f && signbit(f)));
+  return __uint_as_float(outward ? b + 1u : b - 1u);
+}
 DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
 DEV float fmin_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
@@ -362,7 +371,7 @@ class Emitter:
             if D.is_float(dt) and D.is_float(src):
                 expr = self.round(a, dt) if dt != "float64" else f"(double){a}"
                 if src == "float64" and dt in ("bfloat16", "float16"):
-                    raise Unfusable(var, "float64 to a 16-bit float needs round to odd")
+                    expr = self.round(f"ro_f32({a})", dt)
             elif D.is_float(dt):
                 expr = self.round(f"(float)({a})", dt) if dt != "float64" else f"(double)({a})"
             elif dt == "bool":
@@ -526,6 +535,8 @@ class LoopKernel:
 
     def source(self):
         st = self.step
+        if st.kind == "scatter_add":
+            return self._scatter()
         if st.kind == "row":
             return self._row()
         if st.kind == "reduce":
@@ -814,6 +825,48 @@ class LoopKernel:
         src += ["    " + l for l in body]
         src += ["    " + upd, "  }", "  " + store, "}"]
         return "\n".join(src)
+
+
+def _scatter_kernel(self):
+    """``scatter_add``: the output already holds the operand (a fill or copy step before it); each update
+    element is added atomically at the entry its index picks (float32; the order of the adds differs from the
+    reference's sequential one, within float32 rounding)."""
+    g, st = self.graph, self.step
+    n = st.nodes[0]
+    x, ix, u = (g.types[v] for v in n.inputs)
+    axis = n.params["axis"]
+    if x.dtype != "float32":
+        raise Unfusable(n.output, f"scatter_add into {x.dtype} (atomic adds are float32)")
+    em = Emitter(g, [], {v: (k, self.views[v]) for k, v in enumerate(st.inputs)})
+    um = em.multi(("flat", "e"), u.shape)
+    r = len(ix.shape)
+    iv = em.value(n.inputs[1], ("multi", tuple(um[axis : axis + r])))
+    val = em.value(n.inputs[2], ("multi", tuple(um)))
+    em.emit(f"const int64_t kk = min(max((int64_t){iv}, 0LL), {max(x.shape[axis] - 1, 0)}LL);")
+    xm = um[:axis] + ["kk"] + um[axis + r :]
+    ov = self.out_views[n.output]
+    terms = [f"({e}) * {s_}LL" for e, s_ in zip(xm, ov.strides) if s_ and e != "0"]
+    addr = "(" + (" + ".join(terms) if terms else "0") + ")"
+    NU = u.numel()
+    threads = 256
+    self.grid, self.block, self.lds = (max(1, min(-(-NU // threads), 65536)), 1, 1), (threads, 1, 1), 0
+    params = []
+    self.args = []
+    for k, v in enumerate(st.inputs):
+        params.append(f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k}")
+        self.args.append(("in", v))
+    params.append(f"float* __restrict__ out0")
+    self.args.append(("out", n.output))
+    src = [
+        f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({", ".join(params)}) {{',
+        f"  for (int64_t e = (int64_t)blockIdx.x * {threads} + threadIdx.x; e < {NU}LL; e += (int64_t)gridDim.x * {threads}) {{",
+    ]
+    src += ["    " + l for l in em.lines]
+    src += [f"    atomicAdd(&out0[{addr}], (float){val});", "  }", "}"]
+    return "\n".join(src)
+
+
+LoopKernel._scatter = _scatter_kernel
 
 
 def _declared(em):

@@ -26,8 +26,8 @@ INDEX_ONLY = {"full", "iota"}
 FUSIBLE = ELEMENTWISE | LAYOUT | INDEX_ONLY | {"gather", "take_along_axis", "reduce_sum", "reduce_max",
                                                "dynamic_slice", "host_wait", "device_wait"}
 # Built-in kernels: each node is a step of its own.
-OWN_STEP = {"dot_general", "flash_attention", "flash_attention_backward", "scatter_add", "cumsum",
-            "random_bits", "linear_cross_entropy", "dynamic_update_slice", "fusion_output"}
+OWN_STEP = {"dot_general", "fusion", "scatter_add", "cumsum", "random_bits", "linear_cross_entropy",
+            "dynamic_update_slice"}
 
 
 @dataclass
@@ -40,6 +40,7 @@ class Step:
     inputs: list = field(default_factory=list)   # values it reads from memory
     rows: tuple | None = None       # (R, C) of a row kernel
     name: str = ""
+    scratch: int = 0                # bytes of workspace the step needs while it runs
 
     def label(self):
         return " → ".join(n.prim for n in self.nodes[:6]) + (" → …" if len(self.nodes) > 6 else "")
@@ -69,7 +70,9 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
     # Operands of built-in steps live in memory; a layout op there is a strided view when it can be one.
     for n in graph.nodes:
         if n.prim in OWN_STEP:
-            for u in n.inputs:
+            for j, u in enumerate(n.inputs):
+                if n.prim == "scatter_add" and j == 0 and u in prod and prod[u].prim == "full":
+                    continue
                 while u in prod and prod[u].prim in VIEWABLE and u not in graph.outputs:
                     views.add(u)
                     u = prod[u].inputs[0]
@@ -105,9 +108,13 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
         memo[v] = r
         return r
 
+    extra_outs = {}
+    for n in graph.nodes:
+        if n.prim == "fusion_output":
+            extra_outs.setdefault(n.inputs[0], []).append(n.output)
     for n in reversed(graph.nodes):
         v = n.output
-        if v in kernel_of:
+        if v in kernel_of or n.prim == "fusion_output":
             continue
         if cheap(v) and v not in must and v not in views:
             continue
@@ -124,8 +131,10 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
             members.append({v})
             kinds.append("own")
             rows.append(None)
-            roots.append([v])
+            roots.append([v] + extra_outs.get(v, []))
             kernel_of[v] = k
+            for x in extra_outs.get(v, []):
+                kernel_of[x] = k
             continue
         k = len(members)
         mem = {v}
@@ -166,8 +175,19 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
             if outside or u in must:
                 if not _fits(graph, u, roots[k], rows[k] if p.prim not in ("reduce_sum", "reduce_max") else _row_space(graph, p)):
                     continue
-                memo = {}
-                if any(depends(m, c, memo) for c in outside for m in mem):
+                # computing u here must not make this kernel wait for a kernel that reads u: no member may
+                # depend on anything another reader's kernel writes
+                targets = set()
+                for c in outside:
+                    kc = kernel_of.get(c)
+                    targets.update(roots[kc] if kc is not None else [c])
+                cyc = False
+                for tv in targets:
+                    memo = {}
+                    if any(depends(m, tv, memo) for m in mem):
+                        cyc = True
+                        break
+                if cyc:
                     continue
                 roots[k].append(u)
                 must.add(u)
@@ -182,10 +202,17 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
         outs = list(roots[k])
         if kinds[k] == "own":
             node = nodes[0]
-            kind = {"dot_general": "dot", "flash_attention": "flash_fwd", "flash_attention_backward": "flash_bwd"}.get(
-                node.prim, node.prim
-            )
+            kind = {"dot_general": "dot"}.get(node.prim, node.prim)
+            if node.prim == "fusion":
+                kind = {"flash_attention": "flash_fwd", "flash_attention_backward": "flash_bwd"}[node.params["name"]]
             st = Step(kind, nodes, outs)
+            if kind in ("flash_fwd", "flash_bwd"):
+                q = graph.types[node.inputs[0]]
+                if kind == "flash_bwd":
+                    b, sq, nh, _ = q.shape
+                    st.scratch = b * nh * sq * 4
+                elif len(outs) == 1:
+                    st.scratch = graph.types[outs[0]].numel() // graph.types[outs[0]].shape[-1] * 4
         elif kinds[k] in ("view", "reduce"):
             st = Step(kinds[k], nodes, outs)
         else:
@@ -196,6 +223,8 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
             for u in m.inputs:
                 if u not in produced and u not in ins:
                     ins.append(u)
+        if st.kind == "scatter_add" and nodes[0].inputs[0] in prod and prod[nodes[0].inputs[0]].prim == "full":
+            ins = [u for u in ins if u != nodes[0].inputs[0]]
         st.inputs = ins
         steps.append(st)
     for st in steps:

@@ -138,6 +138,7 @@ class Plan:
     def _place(self):
         g = self.graph
         self.loc: dict[int, Loc] = {}
+        self.scratch: dict[int, Loc] = {}
         for i, v in enumerate(g.inputs):
             t = g.types[v]
             self.loc[v] = Loc(("in", i), 0, _contig(t.shape), t.dtype, t.shape)
@@ -204,6 +205,10 @@ class Plan:
                 off, size = take(t.nbytes())
                 live[v] = (off, size)
                 self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
+            if st.scratch:
+                off, size = take(st.scratch)
+                self.scratch[id(st)] = Loc(("ws", 0), off // 4, (1,), "float32", (st.scratch // 4,))
+                release(off, size)
             for v in list(live):
                 if last_use.get(v, -1) <= si and v not in g.outputs:
                     off, size = live.pop(v)
@@ -229,8 +234,14 @@ class Plan:
     def _gen_kernels(self):
         g = self.graph
         for si, st in enumerate(self.steps):
-            if st.kind not in ("loop", "row", "reduce"):
+            if st.kind not in ("loop", "row", "reduce", "scatter_add"):
                 continue
+            if st.kind == "scatter_add":
+                # the operand reaches the output buffer first (a fill of its constant, or a copy); the kernel
+                # then reads only the indices and updates
+                n = st.nodes[0]
+                st.prefill = self._prefill(n)
+                st.inputs = [v for v in n.inputs[1:]]
             views = {v: self.loc[v].view() for v in st.inputs}
             outs = {v: self.loc[v].view() for v in st.outputs}
             k = codegen.LoopKernel(g, st, "KNAME", views, outs)
@@ -243,6 +254,16 @@ class Plan:
             src = codegen.HEADER + body.replace("KNAME", name)
             self.kernels[si] = k
             self.sources[si] = src
+
+    def _prefill(self, n):
+        """How a scatter_add's output gets its operand: ``("fill", value)`` for a constant, else ``("copy", loc)``."""
+        prod = self.graph.producers()
+        x = prod.get(n.inputs[0])
+        if x is not None and x.prim == "full":
+            if float(x.params["fill_value"]) != 0.0:
+                raise NotImplementedError("scatter_add into a nonzero constant: the hip backend has no kernel for it yet")
+            return ("fill", 0)
+        return ("copy", self.loc[n.inputs[0]])
 
     def build(self):
         """Compiles every generated kernel (hipcc, cached)."""
@@ -272,7 +293,19 @@ class Plan:
             return r
 
         for si, st in enumerate(self.steps):
-            if st.kind in ("loop", "row", "reduce"):
+            if st.kind == "scatter_add":
+                out = self.loc[st.outputs[0]]
+                nbytes = g.types[st.outputs[0]].nbytes()
+                kind_, arg = st.prefill
+                if kind_ == "fill":
+                    desc = struct.pack("<QI", nbytes, 0) + b"\0" * 4
+                    rr = (nv.Reloc * 1)(reloc(0, out))
+                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), rr, 1)
+                else:
+                    desc = struct.pack("<Q", nbytes)
+                    rr = (nv.Reloc * 2)(reloc(0, out), reloc(1, arg))
+                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
+            if st.kind in ("loop", "row", "reduce", "scatter_add"):
                 k = self.kernels[si]
                 fn = nv.module_function(self.objects[si], k.name)
                 if st.kind == "reduce" and getattr(k, "atomic", False):

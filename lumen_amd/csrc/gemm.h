@@ -1,8 +1,9 @@
 // dot_general kernels for gfx950.
 //
 //  * gemm_mfma: bf16/f16 operands on the matrix cores (v_mfma_f32_32x32x16_{bf16,f16}), float32
-//    accumulation, LDS-staged double-buffered tiles. Both operands are read k-contiguous (A as [m][k],
-//    B as [n][k]); the plan gives a transposed operand a layout pass first.
+//    accumulation, LDS-staged double-buffered tiles. Each operand may be k-contiguous or mn-contiguous in
+//    memory: an mn-contiguous tile is kept [k][mn] in LDS and its MFMA fragments are read transposed with
+//    ds_read_tr16_b64, so transposed operands (the weight and input gradients) need no layout pass.
 //  * gemm_exact: any strides and dtypes; each output is the reference's sequential k-order fold with the
 //    product and every partial sum rounded to float32 (lumen/reference/mod.rs:981-993), so float32 dots are
 //    bit-identical to the reference interpreter.
@@ -143,19 +144,60 @@ struct Pitch {
     static constexpr int value = BK + 8;
 };
 
-template <bool F16, int BM, int BN, int BK, int WM, int WN, class Epi>
+// Output of any float dtype chosen at run time (one kernel instantiation serves all three).
+// The dtype branch is taken once, outside the unrolled store loops (a branch per element keeps the
+// compiler from unrolling them, which sends the accumulators to scratch memory).
+struct AnyStore {
+    void *d;
+    int32_t dtype;  // 0 f32, 1 bf16, 2 f16
+    template <class F>
+    __device__ __forceinline__ void visit(F &&f) const {
+        if (dtype == 0) f(StoreEpilogue<float>{static_cast<float *>(d)});
+        else if (dtype == 1) f(StoreEpilogue<bf16_t>{static_cast<bf16_t *>(d)});
+        else f(StoreEpilogue<f16_t>{static_cast<f16_t *>(d)});
+    }
+};
+
+typedef short gv4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gv4i16_t glds_v4i16_t;
+
+// Two transposed 64-bit LDS reads, 4 rows apart, of a [k][mn] tile: 8 consecutive k at one mn column.
+__device__ __forceinline__ uint4 gemm_read_tr(const uint16_t *p0, const uint16_t *p1) {
+    gv4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p0));
+    gv4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p1));
+    uint2 x = __builtin_bit_cast(uint2, a), y = __builtin_bit_cast(uint2, b);
+    return make_uint4(x.x, x.y, y.x, y.y);
+}
+
+// A tile of one operand in LDS: k-major rows ([rows][BK], read with ds_read_b128) when the operand is
+// k-contiguous in memory, else mn-major rows ([BK][rows], read transposed with ds_read_tr16_b64). Either way
+// global loads are 16-byte chunks along the contiguous dimension, so every load is coalesced.
+template <int ROWS, int BK, bool T>
+struct TileLayout {
+    static constexpr int pitch = T ? ROWS + 16 : BK + 8;
+    static constexpr int elems = T ? BK * pitch : ROWS * pitch;
+    static constexpr int chunks_per_line = T ? ROWS / 8 : BK / 8;
+};
+
+template <bool T, int P>
+struct FragLayout {
+    static constexpr bool transposed = T;
+    static constexpr int pitch = P;
+};
+
+template <bool F16, int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, class Epi>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_mfma(GemmShape s, const uint16_t *__restrict__ a,
                                                            const uint16_t *__restrict__ b, Epi epi) {
     constexpr int T = WM * WN * 64;
-    constexpr int P = Pitch<BK>::value;
+    using LA = TileLayout<BM, BK, AT>;
+    using LB = TileLayout<BN, BK, BT>;
     constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 32, FN = TN / 32;
-    constexpr int CH = BK / 8;                 // 16-byte chunks per tile row
-    constexpr int VA = BM * CH / T, VB = BN * CH / T;
-    static_assert(BM * CH % T == 0 && BN * CH % T == 0, "tile loads must divide evenly");
+    constexpr int VA = BM * BK / 8 / T, VB = BN * BK / 8 / T;
+    static_assert(BM * BK / 8 % T == 0 && BN * BK / 8 % T == 0, "tile loads must divide evenly");
     extern __shared__ __align__(16) uint16_t lds[];
-    uint16_t *As = lds;                        // [2][BM][P]
-    uint16_t *Bs = lds + 2 * BM * P;           // [2][BN][P]
+    uint16_t *As = lds;                 // [2][LA::elems]
+    uint16_t *Bs = lds + 2 * LA::elems; // [2][LB::elems]
 
     int tm, tn;
     tile_of(blockIdx.x, s.tiles_m, s.tiles_n, tm, tn);
@@ -164,6 +206,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_mfma(GemmShape s, const uint
     const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / WN, wn = wave % WN;
+    const int h = lane >> 5, l32 = lane & 31, g = lane >> 4, s16 = lane & 15;
 
     const uint16_t *pa = a + oa;
     const uint16_t *pb = b + ob;
@@ -172,29 +215,49 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_mfma(GemmShape s, const uint
     auto load = [&](int64_t k0) {
 #pragma unroll
         for (int v = 0; v < VA; ++v) {
-            int idx = t + v * T, row = idx / CH, ch = idx % CH;
-            int64_t gm = m0 + row, gk = k0 + ch * 8;
-            ra[v] = (gm < s.m && gk < s.k) ? *reinterpret_cast<const uint4 *>(pa + gm * s.a_m + gk) : make_uint4(0, 0, 0, 0);
+            int idx = t + v * T, line = idx / LA::chunks_per_line, ch = idx % LA::chunks_per_line;
+            int64_t gm, gk;
+            if (AT) gk = k0 + line, gm = m0 + ch * 8;
+            else gm = m0 + line, gk = k0 + ch * 8;
+            bool ok = gm < s.m && gk < s.k;
+            const uint16_t *src = AT ? pa + gk * s.a_k + gm : pa + gm * s.a_m + gk;
+            ra[v] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int v = 0; v < VB; ++v) {
-            int idx = t + v * T, row = idx / CH, ch = idx % CH;
-            int64_t gn = n0 + row, gk = k0 + ch * 8;
-            rb[v] = (gn < s.n && gk < s.k) ? *reinterpret_cast<const uint4 *>(pb + gn * s.b_n + gk) : make_uint4(0, 0, 0, 0);
+            int idx = t + v * T, line = idx / LB::chunks_per_line, ch = idx % LB::chunks_per_line;
+            int64_t gn, gk;
+            if (BT) gk = k0 + line, gn = n0 + ch * 8;
+            else gn = n0 + line, gk = k0 + ch * 8;
+            bool ok = gn < s.n && gk < s.k;
+            const uint16_t *src = BT ? pb + gk * s.b_k + gn : pb + gn * s.b_n + gk;
+            rb[v] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
         }
     };
     auto store = [&](int buf) {
 #pragma unroll
         for (int v = 0; v < VA; ++v) {
-            int idx = t + v * T, row = idx / CH, ch = idx % CH;
-            *reinterpret_cast<uint4 *>(As + (buf * BM + row) * P + ch * 8) = ra[v];
+            int idx = t + v * T, line = idx / LA::chunks_per_line, ch = idx % LA::chunks_per_line;
+            *reinterpret_cast<uint4 *>(As + buf * LA::elems + line * LA::pitch + ch * 8) = ra[v];
         }
 #pragma unroll
         for (int v = 0; v < VB; ++v) {
-            int idx = t + v * T, row = idx / CH, ch = idx % CH;
-            *reinterpret_cast<uint4 *>(Bs + (buf * BN + row) * P + ch * 8) = rb[v];
+            int idx = t + v * T, line = idx / LB::chunks_per_line, ch = idx % LB::chunks_per_line;
+            *reinterpret_cast<uint4 *>(Bs + buf * LB::elems + line * LB::pitch + ch * 8) = rb[v];
         }
     };
+    // Fragment reads: 8 consecutive k at this lane's row (m or n), k offset 8 * half-wave.
+    auto frag = [&](const uint16_t *base, int row0, int kk, auto layout) -> uint4 {
+        using L = decltype(layout);
+        if constexpr (L::transposed) {
+            const uint16_t *p0 = base + (kk + 8 * h + s16 / 4) * L::pitch + row0 + 16 * (g & 1) + 4 * (s16 & 3);
+            return gemm_read_tr(p0, p0 + 4 * L::pitch);
+        } else {
+            return *reinterpret_cast<const uint4 *>(base + (row0 + l32) * L::pitch + kk + 8 * h);
+        }
+    };
+    using LAT = FragLayout<AT, LA::pitch>;
+    using LBT = FragLayout<BT, LB::pitch>;
 
     f32x16_t acc[FM][FN];
 #pragma unroll
@@ -208,19 +271,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_mfma(GemmShape s, const uint
     load(0);
     store(0);
     __syncthreads();
-    const int lrow = lane & 31, lk = (lane >> 5) * 8;
     for (int kt = 0; kt < ktiles; ++kt) {
         const int buf = kt & 1;
         if (kt + 1 < ktiles) load(int64_t(kt + 1) * BK);
-        const uint16_t *as = As + (buf * BM + wm * TM + lrow) * P + lk;
-        const uint16_t *bs = Bs + (buf * BN + wn * TN + lrow) * P + lk;
+        const uint16_t *as = As + buf * LA::elems;
+        const uint16_t *bs = Bs + buf * LB::elems;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 16) {
             uint4 fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const uint4 *>(as + i * 32 * P + kk);
+            for (int i = 0; i < FM; ++i) fa[i] = frag(as, wm * TM + i * 32, kk, LAT{});
 #pragma unroll
-            for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const uint4 *>(bs + j * 32 * P + kk);
+            for (int j = 0; j < FN; ++j) fb[j] = frag(bs, wn * TN + j * 32, kk, LBT{});
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -231,21 +293,24 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_mfma(GemmShape s, const uint
     }
 
     // C layout of a 32x32 block: lane holds column lane % 32, rows 8 * (e / 4) + 4 * (lane / 32) + e % 4.
+    epi.visit([&](auto st) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                int64_t r = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                int64_t c = n0 + wn * TN + j * 32 + (lane & 31);
-                if (r < s.m && c < s.n) epi(s, od, r, c, acc[i][j][e]);
-            }
+                for (int e = 0; e < 16; ++e) {
+                    int64_t r = m0 + wm * TM + i * 32 + 8 * (e / 4) + 4 * h + (e % 4);
+                    int64_t c = n0 + wn * TN + j * 32 + l32;
+                    if (r < s.m && c < s.n) st(s, od, r, c, acc[i][j][e]);
+                }
+    });
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, bool AT, bool BT>
 constexpr int gemm_mfma_lds_bytes() {
-    return 2 * (BM + BN) * Pitch<BK>::value * 2;
+    return 2 * (TileLayout<BM, BK, AT>::elems + TileLayout<BN, BK, BT>::elems) * 2;
 }
+
 
 }  // namespace nhipk

@@ -19,8 +19,9 @@ struct TileConfig {
 // Candidates for bf16/f16 GEMMs, largest first (lumen/codegen/dot_general/cuda/mod.rs:430-633 keeps a
 // similar list for SM80; these are sized for 160 KiB of LDS and wave64).
 constexpr TileConfig kConfigs[] = {
-    {256, 256, 64, 2, 2},
+    {256, 256, 64, 2, 4},
     {256, 128, 64, 2, 2},
+    {128, 256, 64, 2, 2},
     {128, 128, 64, 2, 2},
     {128, 64, 64, 2, 2},
     {64, 64, 64, 2, 2},
@@ -83,12 +84,12 @@ int launch_exact(hipStream_t st, GemmShape s, const nhip_gemm_desc *d, const voi
     return check(hipGetLastError(), "gemm_exact launch");
 }
 
-template <bool F16, int BM, int BN, int BK, int WM, int WN, typename TD>
-int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out) {
+template <bool F16, int BM, int BN, int BK, int WM, int WN, bool AT, bool BT>
+int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype) {
     s.tiles_m = int((s.m + BM - 1) / BM);
     s.tiles_n = int((s.n + BN - 1) / BN);
-    constexpr int lds = gemm_mfma_lds_bytes<BM, BN, BK>();
-    auto kern = gemm_mfma<F16, BM, BN, BK, WM, WN, StoreEpilogue<TD>>;
+    constexpr int lds = gemm_mfma_lds_bytes<BM, BN, BK, AT, BT>();
+    auto kern = gemm_mfma<F16, BM, BN, BK, WM, WN, AT, BT, AnyStore>;
     static bool attr = false;
     if (!attr) {
         if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
@@ -98,28 +99,44 @@ int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const
     }
     dim3 grid(s.tiles_m * s.tiles_n, unsigned(z));
     hipLaunchKernelGGL(kern, grid, dim3(WM * WN * 64), lds, st, s, static_cast<const uint16_t *>(a),
-                       static_cast<const uint16_t *>(b), StoreEpilogue<TD>{static_cast<TD *>(out)});
+                       static_cast<const uint16_t *>(b), AnyStore{out, dtype});
     return check(hipGetLastError(), "gemm_mfma launch");
 }
 
-template <bool F16, typename TD>
-int launch_mfma(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out) {
+template <bool F16, bool AT, bool BT>
+int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype) {
     switch (cfg) {
-        case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 2, TD>(st, s, z, a, b, out);
-        case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, TD>(st, s, z, a, b, out);
-        case 2: return launch_mfma_cfg<F16, 128, 128, 64, 2, 2, TD>(st, s, z, a, b, out);
-        case 3: return launch_mfma_cfg<F16, 128, 64, 64, 2, 2, TD>(st, s, z, a, b, out);
-        default: return launch_mfma_cfg<F16, 64, 64, 64, 2, 2, TD>(st, s, z, a, b, out);
+        case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
+        case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
+        case 2: return launch_mfma_cfg<F16, 128, 256, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
+        case 3: return launch_mfma_cfg<F16, 128, 128, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
+        case 4: return launch_mfma_cfg<F16, 128, 64, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
+        default: return launch_mfma_cfg<F16, 64, 64, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
     }
+}
+
+template <bool F16>
+int launch_mfma(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
+                bool at, bool bt) {
+    if (at) return bt ? launch_mfma_layout<F16, true, true>(st, cfg, s, z, a, b, out, dtype)
+                      : launch_mfma_layout<F16, true, false>(st, cfg, s, z, a, b, out, dtype);
+    return bt ? launch_mfma_layout<F16, false, true>(st, cfg, s, z, a, b, out, dtype)
+              : launch_mfma_layout<F16, false, false>(st, cfg, s, z, a, b, out, dtype);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Whether the MFMA kernel reads these operands: k-contiguous rows starting on 16-byte boundaries.
-bool mfma_ready(const nhip_gemm_desc *d, const void *a, const void *b) {
+// Whether the MFMA kernel reads these operands: each k-contiguous or mn-contiguous, with 16-byte aligned
+// rows along its contiguous dimension. `at` / `bt` say an operand is mn-contiguous.
+bool mfma_ready(const nhip_gemm_desc *d, const void *a, const void *b, bool &at, bool &bt) {
     if (d->a_dtype != d->b_dtype || d->a_dtype == NHIP_F32) return false;
-    if (d->a_k != 1 || d->b_k != 1 || d->k % 8 || d->a_m % 8 || d->b_n % 8) return false;
     if (!aligned16(a) || !aligned16(b)) return false;
+    if (d->a_k == 1 && d->k % 8 == 0 && (d->a_m % 8 == 0 || d->m == 1)) at = false;
+    else if (d->a_m == 1 && d->m % 8 == 0 && d->a_k % 8 == 0) at = true;
+    else return false;
+    if (d->b_k == 1 && d->k % 8 == 0 && (d->b_n % 8 == 0 || d->n == 1)) bt = false;
+    else if (d->b_n == 1 && d->n % 8 == 0 && d->b_k % 8 == 0) bt = true;
+    else return false;
     for (int i = 0; i < d->nbatch; ++i)
         if (d->a_batch[i] % 8 || d->b_batch[i] % 8) return false;
     return true;
@@ -135,18 +152,12 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     int64_t z = batch_count(d);
     if (d->m == 0 || d->n == 0 || z == 0) return 0;
     if (z > 65535) return fail("nhip_gemm: more than 65535 batches");
-    if (d->k > 0 && mfma_ready(d, a, b)) {  // k == 0 folds nothing: the exact kernel writes zeros
+    bool at = false, bt = false;
+    if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
-        bool f16 = d->a_dtype == NHIP_F16;
-        switch (d->d_dtype) {
-            case NHIP_F32:
-                return f16 ? launch_mfma<true, float>(st, cfg, s, z, a, b, out) : launch_mfma<false, float>(st, cfg, s, z, a, b, out);
-            case NHIP_BF16:
-                return f16 ? launch_mfma<true, bf16_t>(st, cfg, s, z, a, b, out) : launch_mfma<false, bf16_t>(st, cfg, s, z, a, b, out);
-            default:
-                return f16 ? launch_mfma<true, f16_t>(st, cfg, s, z, a, b, out) : launch_mfma<false, f16_t>(st, cfg, s, z, a, b, out);
-        }
+        if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
+        return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
     }
     switch (d->d_dtype) {
         case NHIP_F32: return launch_exact<float>(st, s, d, a, b, out);

@@ -220,8 +220,9 @@ int nhip_alloc(int device, size_t bytes, size_t alignment, void **ptr) {
     if (device_locked(device, &d)) return 1;
     Region &r = d->region;
     if (!r.base && reserve_locked(device, r, 0)) return 1;
-    if (n > r.capacity) {
-        // Larger than the whole region (a plan workspace): a block of its own, freed with it.
+    if (n > r.capacity / 4) {
+        // A large block (a plan workspace, a weight matrix): an allocation of its own, freed with it, so
+        // large blocks never fragment the region the small ones share.
         int prev = 0;
         hipGetDevice(&prev);
         hipSetDevice(device);

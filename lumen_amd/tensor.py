@@ -13,6 +13,7 @@ import math
 import numpy as np
 
 from lumen_amd import dtypes as D
+from lumen_amd import native
 
 
 def device_name(d) -> str:
@@ -40,16 +41,12 @@ class DeviceBuffer:
     __slots__ = ("ptr", "nbytes", "device", "__weakref__")
 
     def __init__(self, device: int, nbytes: int):
-        from lumen_amd import native
-
         native.set_device(device)
         self.device, self.nbytes = device, int(nbytes)
         self.ptr = native.alloc(device, max(1, self.nbytes))
 
     def __del__(self):
-        from lumen_amd import native
-
-        if getattr(self, "ptr", None) and native._lib is not None:
+        if getattr(self, "ptr", None) and native is not None and native._lib is not None:
             try:
                 native.free(self.device, self.ptr, self.nbytes)
             except Exception:

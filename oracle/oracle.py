@@ -67,7 +67,7 @@ def _param(key, v) -> list[str]:
 
 
 # Parameters the oracle does not read (labels, compiler annotations).
-_SKIP = {"label", "name", "ty", "view", "in_place", "kernel", "role"}
+_SKIP = {"label", "name", "ty", "view", "in_place", "kernel", "role", "q_dims", "k_dims", "v_dims", "scale", "causal"}
 
 
 def serialize(g: Graph) -> str:
@@ -96,7 +96,7 @@ def run(graph: Graph, inputs: list) -> list:
         ty = graph.types[v]
         if hasattr(x, "raw"):
             x = x.raw()
-        a = np.ascontiguousarray(np.asarray(x), D.storage(ty.dtype))
+        a = np.ascontiguousarray(np.asarray(x), D.storage(ty.dtype)).reshape(np.asarray(x).shape)
         if tuple(a.shape) != tuple(ty.shape):
             raise ValueError(f"input %{v} must be {ty}, got shape {list(a.shape)}")
         arrays.append(a)

@@ -1,0 +1,90 @@
+"""nhip_gemm (the dot_general kernel) through the C ABI: every operand layout, batches, edges and dtypes."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from lumen_amd import dtypes as D
+from lumen_amd import native as nv
+from tests.hiputil import Dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _desc(m, n, k, a_m, a_k, b_k, b_n, dt=nv.NHIP_BF16, out=nv.NHIP_F32, cfg=-1, batch=(), sa=(), sb=(), sd=()):
+    d = nv.GemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.nbatch = len(batch)
+    for i, (z, x, y, w) in enumerate(zip(batch, sa, sb, sd)):
+        d.batch[i], d.a_batch[i], d.b_batch[i], d.d_batch[i] = z, x, y, w
+    d.a_dtype = d.b_dtype = dt
+    d.d_dtype = out
+    d.a_m, d.a_k, d.b_k, d.b_n, d.d_m, d.d_n = a_m, a_k, b_k, b_n, n, 1
+    d.config = cfg
+    return d
+
+
+@pytest.mark.parametrize("at,bt", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("m,n,k,cfg", [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0)])
+def test_gemm_layouts(hip, at, bt, m, n, k, cfg):
+    """A as [m][k] or [k][m] in memory, B as [n][k] or [k][n]: float32 results within float32 rounding of
+    the float64 product of the bf16 operands."""
+    rng = np.random.default_rng(m + n + k)
+    a = D.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    b = D.bf16_bits(rng.standard_normal((k, n)).astype(np.float32))
+    want = D.bf16_to_f32(a).astype(np.float64) @ D.bf16_to_f32(b).astype(np.float64)
+    am = np.ascontiguousarray(a.T) if at else a
+    bm = b if bt else np.ascontiguousarray(b.T)
+    da, db, dd = Dev(am), Dev(bm), Dev(nbytes=m * n * 4)
+    desc = _desc(m, n, k, 1 if at else k, m if at else 1, n if bt else 1, 1 if bt else k, cfg=cfg)
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    got = dd.get((m, n), np.float32)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
+
+
+def test_gemm_batched_bf16_output(hip):
+    rng = np.random.default_rng(0)
+    z, m, n, k = 3, 96, 80, 48
+    a = D.bf16_bits(rng.standard_normal((z, m, k)).astype(np.float32))
+    b = D.bf16_bits(rng.standard_normal((z, n, k)).astype(np.float32))
+    want = np.einsum("zmk,znk->zmn", D.bf16_to_f32(a).astype(np.float64), D.bf16_to_f32(b).astype(np.float64))
+    da, db, dd = Dev(a), Dev(b), Dev(nbytes=z * m * n * 2)
+    desc = _desc(m, n, k, k, 1, 1, k, out=nv.NHIP_BF16, batch=(z,), sa=(m * k,), sb=(n * k,), sd=(m * n,))
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    got = D.bf16_to_f32(dd.get((z, m, n), np.uint16))
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+def test_gemm_f32_is_the_sequential_fold(hip):
+    """float32 operands: every output equals the k-order fold rounded after each product and sum."""
+    rng = np.random.default_rng(3)
+    m, n, k = 33, 65, 129
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    acc = np.zeros((m, n), np.float32)
+    for kk in range(k):
+        acc = (acc + (a[:, kk : kk + 1] * b[kk : kk + 1, :]).astype(np.float32)).astype(np.float32)
+    da, db, dd = Dev(a), Dev(b), Dev(nbytes=m * n * 4)
+    desc = _desc(m, n, k, k, 1, n, 1, dt=nv.NHIP_F32)
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    assert np.array_equal(dd.get((m, n), np.float32).view(np.uint32), acc.view(np.uint32))
+
+
+@pytest.mark.parametrize("at,bt", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_throughput(hip, at, bt):
+    """Times 8192^3 bf16 in every layout (random data) and prints TFLOP/s."""
+    m = n = k = 8192
+    rng = np.random.default_rng(0)
+    a = D.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    da, db, dd = Dev(a), Dev(a), Dev(nbytes=m * n * 2)
+    desc = _desc(m, n, k, 1 if at else k, m if at else 1, n if bt else 1, 1 if bt else k, out=nv.NHIP_BF16)
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    nv.sync()
+    e0, e1 = nv.Event(), nv.Event()
+    e0.record()
+    for _ in range(5):
+        nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / 5
+    print(f"gemm 8192^3 at={at} bt={bt}: {ms * 1e3:.1f} us {2 * m * n * k / ms / 1e9:.1f} TFLOP/s")

@@ -1,0 +1,78 @@
+"""The decoder training step (the BASELINE transformer at a small size) compiled for hip against the CPU
+oracle running the same traced graph: loss, every gradient, and the SGD-updated weights."""
+
+import numpy as np
+import pytest
+
+import lumen_amd as L
+from lumen_amd import dtypes as D
+from lumen_amd import workloads as W
+from lumen_amd.graph.trace import trace
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _grads(model, ids, targets):
+    loss = W.loss_fn(model, ids, targets)
+    loss.backward()
+    return [loss] + [p.grad for p in model.parameters()]
+
+
+def _setup(cfg, fn, *extra):
+    model, opt = W.build(cfg, lr=1.0)
+    weights = W.init_weights(model)
+    W.load(model, weights)
+    ids, targets = W.batch(cfg)
+    args = (model,) + extra + (L.from_numpy(ids), L.from_numpy(targets))
+    return model, opt, weights, ids, targets, args
+
+
+def _oracle_inputs(traced, ids, targets, weights, names, scalars=()):
+    ins = []
+    by_id = {id(p): names[id(p)] for p in traced.weights}
+    args = [ids, targets]
+    for kind, k in traced.layout:
+        if kind == "arg":
+            ins.append(args[k])
+        elif kind == "scalar":
+            ins.append(np.array(scalars[k], np.float64))
+        else:
+            ins.append(weights[by_id[id(traced.weights[k])]])
+    return ins
+
+
+def test_transformer_gradients_match_oracle(hip):
+    """Loss within 1e-2 relative, every gradient within 5% relative norm of the oracle's (the reference's
+    transformer test bounds, tests/test_transformer_example.py:318-331)."""
+    cfg = W.TINY
+    model, opt, weights, ids, targets, args = _setup(cfg, _grads)
+    names = {id(p): n for n, p in model.named_parameters()}
+    f = L.compile(_grads, device="hip")
+    got = [L.to_numpy(t) for t in f(*args)]
+    traced = trace(_grads, args)
+    want = oracle.values(traced.graph, _oracle_inputs(traced, ids, targets, weights, names))
+    assert abs(got[0] - want[0]) <= 1e-2 * abs(want[0]), (got[0], want[0])
+    pnames = [n for n, _ in model.named_parameters()]
+    for name, a, b in zip(pnames, got[1:], want[1:]):
+        err = np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30)
+        assert err <= 5e-2, (name, err)
+
+
+def test_transformer_train_step_updates_weights(hip):
+    """One SGD step (lr 1.0): the loss, and the written-back weights within bf16 rounding of the oracle's."""
+    cfg = W.TINY
+    model, opt, weights, ids, targets, args = _setup(cfg, W.train_step)
+    args = (model, opt) + args[1:]
+    names = {id(p): n for n, p in model.named_parameters()}
+    f = L.compile(W.train_step, device="hip")
+    loss = float(L.to_numpy(f(*args)))
+    traced = trace(W.train_step, args)
+    want = oracle.values(traced.graph, _oracle_inputs(traced, ids, targets, weights, names, scalars=[1.0]))
+    assert abs(loss - want[0]) <= 1e-2 * abs(want[0])
+    for j, k in enumerate(traced.written):
+        p = traced.weights[k]
+        got = D.bf16_to_f32(p._placed("hip:0").raw())
+        w = want[1 + j]
+        tol = 2e-2 * np.abs(w) + 1e-2 * np.abs(w).max()
+        assert (np.abs(got - w) <= tol).mean() > 0.999, names[id(p)]
