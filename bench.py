@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark: the transformer training step compiled for hip on one MI355X (BASELINE.json's metric).
+
+One step = one call of the compiled ``train_step`` (forward, autograd backward and SGD update of every weight,
+one static plan) on synthetic data of the configured shape, inputs resident on the device. The timed region
+is ``--steps`` calls between two stream synchronizations, after ``--warmup`` untimed calls.
+
+It prints one JSON line: the step time (``value``, ms/step), throughput, a per-kind breakdown of the step
+(dots and flash attention against the bf16 MFMA peak, loop kernels against the HBM peak), the roofline of
+the dominant kernel (measured with HIP events on the plan's stream in a profiled pass after the timed
+region), and the CPU oracle timed on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "transformer train-step ms on 1 MI355X; dot/attn MFMA % + fused-kernel HBM GB/s"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def cpu_baseline(cfg, budget_s=12.0):
+    """The oracle (1 thread) on a bounded sample: the first layer's QKV projection dot for a slice of the
+    tokens, scaled by the step's FLOPs (the step is dot-dominated)."""
+    import numpy as np
+
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from lumen_amd import dtypes as D
+    from oracle import oracle
+
+    d = cfg.dim
+    rows = 8
+    rng = np.random.default_rng(0)
+    total, flops = 0.0, 0
+    while total < budget_s / 4:
+        g = L.make_graph(lambda x, w: F.matmul(x, w.t(), "float32", "bfloat16"))(
+            L.empty([rows, d], "bfloat16", "meta"), L.empty([3 * d, d], "bfloat16", "meta")
+        )
+        x = D.bf16_bits(rng.standard_normal((rows, d)).astype(np.float32))
+        w = D.bf16_bits((0.02 * rng.standard_normal((3 * d, d))).astype(np.float32))
+        t = time.perf_counter()
+        oracle.run(g, [x, w])
+        total = time.perf_counter() - t
+        flops = 2 * rows * d * 3 * d
+        rows *= 2
+    rate = flops / total
+    step_s = cfg.step_flops() / rate
+    return {
+        "value": round(step_s * 1e3, 1),
+        "unit": "ms/step",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"oracle (C restatement of lumen/reference/mod.rs) on the QKV dot [{rows // 2},{d}]x[{d},{3 * d}] "
+        f"bf16 ({flops / 1e9:.2f} GFLOP in {total:.2f} s, {rate / 1e9:.3f} GFLOP/s), scaled to the step's "
+        f"{cfg.step_flops() / 1e12:.1f} TFLOP; nproc={os.cpu_count()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="5", choices=["4", "5", "tiny"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus}: this build measures one MI355X; multi-GPU runs are not part of it "
+            "(data parallel sharding is designed, not built)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import numpy as np
+
+    import lumen_amd as L
+    from lumen_amd import native
+    from lumen_amd import workloads as W
+
+    cfg = {"4": W.CONFIG4, "5": W.CONFIG5, "tiny": W.TINY}[args.config]
+    native.set_device(0)
+    model, opt = W.build(cfg, lr=1e-2)
+    W.load(model, W.init_weights(model))
+    ids, targets = W.batch(cfg)
+    ids_d = L.from_numpy(ids).to("hip")
+    tg_d = L.from_numpy(targets).to("hip")
+    step = L.compile(W.train_step, device="hip")
+    t0 = time.perf_counter()
+    loss = step(model, opt, ids_d, tg_d)
+    native.sync()
+    compile_s = time.perf_counter() - t0
+    print(f"[bench] compiled and ran the first step in {compile_s:.1f} s, loss {float(L.to_numpy(loss)):.4f}",
+          file=sys.stderr, flush=True)
+    for _ in range(max(0, args.warmup - 1)):
+        step(model, opt, ids_d, tg_d)
+    native.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step(model, opt, ids_d, tg_d)
+    native.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    final_loss = float(L.to_numpy(loss))
+    print(f"[bench] {ms:.2f} ms/step over {args.steps} steps, loss {final_loss:.4f}", file=sys.stderr, flush=True)
+
+    # profiled pass: per-step kernel times on the plan's stream
+    plan = step.plan
+    plan.profile(True)
+    reps = max(1, min(args.steps, 3))
+    per_step = {}
+    for _ in range(reps):
+        step(model, opt, ids_d, tg_d)
+        for si, t in plan.step_ms():
+            per_step[si] = per_step.get(si, 0.0) + t / reps
+    plan.profile(False)
+    kinds = {}
+    for si, t in per_step.items():
+        f, b = plan.cost(si)
+        k = plan.steps[si].kind
+        k = "dot" if k == "dot" else ("attention" if k.startswith("flash") else "loop")
+        e = kinds.setdefault(k, {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "steps": 0})
+        e["ms"] += t
+        e["flops"] += f
+        e["bytes"] += b
+        e["steps"] += 1
+    breakdown = {}
+    for k, e in kinds.items():
+        entry = {"ms": round(e["ms"], 3), "steps": e["steps"]}
+        if k in ("dot", "attention"):
+            tf = e["flops"] / (e["ms"] * 1e-3) / 1e12 if e["ms"] else 0.0
+            entry.update(tflops=round(tf, 1), mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        else:
+            gbs = e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] else 0.0
+            entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
+        breakdown[k] = entry
+    # dominant kernel: the step taking the most time
+    dom = max(per_step, key=per_step.get)
+    f, b = plan.cost(dom)
+    st = plan.steps[dom]
+    t_dom = per_step[dom]
+    if f:
+        achieved = f / (t_dom * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    else:
+        achieved = b / (t_dom * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+    roof["kernel"] = f"{st.kind} step {dom}: {_describe(plan, dom)}"
+    roof["per_launch"] = {"flops": f, "bytes": b, "ms": round(t_dom, 4)}
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms, 3),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: uniform token ids, N(0, 0.02) bf16 weights (seeded)",
+        "config": {
+            "workload": f"config{args.config}: {cfg.layers}-layer decoder training step (fwd + autograd bwd + SGD)",
+            "vocab": cfg.vocab, "d_model": cfg.dim, "heads": cfg.heads, "ffn": cfg.ffn,
+            "seq_len": cfg.seq, "global_batch": cfg.batch, "parallelism": "none (1 GPU)",
+        },
+        "tokens_per_s": round(cfg.tokens / (ms * 1e-3), 1),
+        "step_tflops": round(cfg.step_flops() / (ms * 1e-3) / 1e12, 1),
+        "loss": round(final_loss, 5),
+        "breakdown": breakdown,
+        "roofline": roof,
+        "compile_s": round(compile_s, 1),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(out), flush=True)
+    del np
+
+
+def _describe(plan, si):
+    st = plan.steps[si]
+    g = plan.graph
+    if st.kind == "dot":
+        n = st.nodes[0]
+        a, b = (g.types[v] for v in n.inputs)
+        return f"dot_general {list(a.shape)}x{list(b.shape)} -> {list(g.types[n.output].shape)}"
+    if st.kind.startswith("flash"):
+        return f"{st.nodes[0].params['name']} q={list(g.types[st.nodes[0].inputs[0]].shape)}"
+    return st.label()
+
+
+if __name__ == "__main__":
+    main()

@@ -195,6 +195,11 @@ int nhip_plan_add_builtin(void *plan, int kind, const void *desc, size_t desc_by
 int nhip_plan_run(void *plan, void *workspace, void *const *inputs, size_t ninputs);
 /* Number of steps (for tests). */
 int nhip_plan_steps(void *plan, size_t *count);
+/* Profiling: with `enable`, each run records a HIP event before every step and after the last, on the
+ * stream the steps launch on (lumen/plan/run.rs:418-422 times each step for the profiler). */
+int nhip_plan_profile(void *plan, int enable);
+/* Milliseconds of each of the first `n` steps of the last profiled run (waits for it to finish). */
+int nhip_plan_step_ms(void *plan, float *ms, size_t n);
 
 #ifdef __cplusplus
 }

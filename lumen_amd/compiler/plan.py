@@ -283,6 +283,15 @@ class Plan:
         plan = C.c_void_p()
         nv.call("nhip_plan_create", C.byref(plan))
         g = self.graph
+        self.native_steps = []  # python step index of each native step (fills and copies included)
+        _call = nv.call
+
+        def call(name, *args):
+            if name in ("nhip_plan_add_launch", "nhip_plan_add_builtin"):
+                self.native_steps.append(current[0])
+            return _call(name, *args)
+
+        current = [0]
 
         def reloc(slot, loc: Loc):
             r = nv.Reloc()
@@ -293,6 +302,7 @@ class Plan:
             return r
 
         for si, st in enumerate(self.steps):
+            current[0] = si
             if st.kind == "scatter_add":
                 out = self.loc[st.outputs[0]]
                 nbytes = g.types[st.outputs[0]].nbytes()
@@ -300,11 +310,11 @@ class Plan:
                 if kind_ == "fill":
                     desc = struct.pack("<QI", nbytes, 0) + b"\0" * 4
                     rr = (nv.Reloc * 1)(reloc(0, out))
-                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), rr, 1)
+                    call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), rr, 1)
                 else:
                     desc = struct.pack("<Q", nbytes)
                     rr = (nv.Reloc * 2)(reloc(0, out), reloc(1, arg))
-                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
+                    call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
             if st.kind in ("loop", "row", "reduce", "scatter_add"):
                 k = self.kernels[si]
                 fn = nv.module_function(self.objects[si], k.name)
@@ -312,7 +322,7 @@ class Plan:
                     out = self.loc[st.outputs[0]]
                     desc = struct.pack("<QI", g.types[st.outputs[0]].nbytes(), 0) + b"\0" * 4
                     relocs = (nv.Reloc * 1)(reloc(0, out))
-                    nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), relocs, 1)
+                    call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), relocs, 1)
                 relocs = []
                 for j, (kind, v) in enumerate(k.args):
                     relocs.append(reloc(8 * j, self.loc[v]))
@@ -320,20 +330,20 @@ class Plan:
                 grid = (C.c_uint32 * 3)(*k.grid)
                 block = (C.c_uint32 * 3)(*k.block)
                 rr = (nv.Reloc * max(1, len(relocs)))(*relocs)
-                nv.call("nhip_plan_add_launch", plan, fn, grid, block, k.lds, args, len(args), rr, len(relocs))
+                call("nhip_plan_add_launch", plan, fn, grid, block, k.lds, args, len(args), rr, len(relocs))
             elif st.kind == "dot":
                 desc, ops = self._gemm_desc(st.nodes[0])
                 rr = (nv.Reloc * 3)(*[reloc(i, l) for i, l in enumerate(ops)])
-                nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_GEMM, C.byref(desc), C.sizeof(desc), rr, 3)
+                call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_GEMM, C.byref(desc), C.sizeof(desc), rr, 3)
             elif st.kind in ("flash_fwd", "flash_bwd"):
                 kind, desc, ops = attn_pass.lower(self, st)
                 rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
-                nv.call("nhip_plan_add_builtin", plan, kind, C.byref(desc), C.sizeof(desc), rr, len(ops))
+                call("nhip_plan_add_builtin", plan, kind, C.byref(desc), C.sizeof(desc), rr, len(ops))
             elif st.kind == "copy":
                 src, dst = self._copies[si]
                 desc = struct.pack("<Q", g.types[st.outputs[0]].nbytes())
                 rr = (nv.Reloc * 2)(reloc(0, dst), reloc(1, src))
-                nv.call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
+                call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
             elif st.kind == "view":
                 continue
             else:
@@ -414,6 +424,58 @@ class Plan:
                 nv.lib().nhip_plan_destroy(self._native)
             except Exception:
                 pass
+
+    # ---- measurement
+    def profile(self, enable=True):
+        """Records a HIP event around every native step of each run (per-kernel times)."""
+        from lumen_amd import native as nv
+
+        nv.call("nhip_plan_profile", self._native_plan(), int(enable))
+
+    def step_ms(self):
+        """Milliseconds of each native step of the last profiled run, as ``(python step index, ms)``."""
+        from lumen_amd import native as nv
+
+        n = len(self.native_steps)
+        arr = (C.c_float * max(1, n))()
+        nv.call("nhip_plan_step_ms", self._native_plan(), arr, n)
+        return [(self.native_steps[i], arr[i]) for i in range(n)]
+
+    def cost(self, si):
+        """Algorithmic ``(flops, bytes)`` of step ``si``: dots 2 m n k, flash attention 4 B N Sq Sk D (half of it
+        causal; the backward 2.5x), loop kernels the bytes of their operands' distinct elements and outputs."""
+        st = self.steps[si]
+        g = self.graph
+
+        def vbytes(v):
+            loc = self.loc[v]
+            n = 1
+            for d, st_ in zip(loc.shape, loc.strides):
+                if st_ != 0:
+                    n *= d
+            return n * D.size_of(loc.dtype)
+
+        io = sum(vbytes(v) for v in st.inputs if v in self.loc) + sum(g.types[v].nbytes() for v in st.outputs)
+        if st.kind == "dot":
+            n = st.nodes[0]
+            lt = g.types[n.inputs[0]]
+            out = g.types[n.output]
+            k = math.prod(lt.shape[d] for d in n.params["lhs_contracting"])
+            return 2 * out.numel() * k, io
+        if st.kind in ("flash_fwd", "flash_bwd"):
+            n = st.nodes[0]
+            q = g.types[n.inputs[0]]
+            k = g.types[n.inputs[1]]
+            if st.kind == "flash_fwd":
+                qd, kd = n.params["q_dims"], n.params["k_dims"]
+                b, h, sq, d = q.shape[qd[0][0]], q.shape[qd[0][1]], q.shape[qd[1]], q.shape[qd[2]]
+                sk = k.shape[kd[1]]
+            else:
+                b, sq, h, d = q.shape
+                sk = k.shape[1]
+            f = 4 * b * h * sq * sk * d * (0.5 if n.params["causal"] else 1.0)
+            return (f if st.kind == "flash_fwd" else 2.5 * f), io
+        return 0, io
 
     def describe(self):
         """One line per step: its kind, name and label (``Plan.steps()``)."""

@@ -41,7 +41,10 @@ class CompilerFlags:
 @dataclasses.dataclass
 class Config:
     compiler: CompilerFlags = dataclasses.field(default_factory=CompilerFlags)
-    static_allocator_bytes: int = 1 << 30
+    # The static region weights and small tensors are carved from on each device (the reference's default is
+    # 1 GiB, allocator/config.rs:14-25; an MI355X has 288 GB, and the 12-layer step's weights alone are 1.5 GB).
+    # Blocks over a quarter of it (plan workspaces) get allocations of their own.
+    static_allocator_bytes: int = 16 << 30
 
 
 config = Config()

@@ -406,6 +406,8 @@ struct Step {
 struct Plan {
     std::vector<Step> steps;
     std::vector<unsigned char> scratch;
+    bool profile = false;
+    std::vector<hipEvent_t> events;  // one before each step and one after the last, when profiling
 };
 
 }  // namespace
@@ -416,7 +418,29 @@ int nhip_plan_create(void **plan) {
 }
 
 int nhip_plan_destroy(void *plan) {
-    delete static_cast<Plan *>(plan);
+    Plan *p = static_cast<Plan *>(plan);
+    for (hipEvent_t e : p->events) (void)hipEventDestroy(e);
+    delete p;
+    return 0;
+}
+
+int nhip_plan_profile(void *plan, int enable) {
+    Plan *p = static_cast<Plan *>(plan);
+    p->profile = enable != 0;
+    while (p->profile && p->events.size() < p->steps.size() + 1) {
+        hipEvent_t e;
+        if (check(hipEventCreate(&e), "hipEventCreate")) return 1;
+        p->events.push_back(e);
+    }
+    return 0;
+}
+
+int nhip_plan_step_ms(void *plan, float *ms, size_t n) {
+    Plan *p = static_cast<Plan *>(plan);
+    if (!p->profile || p->events.size() < p->steps.size() + 1) return fail("nhip_plan_step_ms: profiling is off");
+    if (check(hipEventSynchronize(p->events[p->steps.size()]), "hipEventSynchronize")) return 1;
+    for (size_t i = 0; i < n && i < p->steps.size(); ++i)
+        if (check(hipEventElapsedTime(&ms[i], p->events[i], p->events[i + 1]), "hipEventElapsedTime")) return 1;
     return 0;
 }
 
@@ -468,6 +492,7 @@ int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninp
     char *ws = static_cast<char *>(workspace);
     for (size_t i = 0; i < plan->steps.size(); ++i) {
         Step &st = plan->steps[i];
+        if (plan->profile && check(hipEventRecord(plan->events[i], s), "hipEventRecord")) return 1;
         auto resolve = [&](const nhip_reloc &r, void **out) -> int {
             char *base;
             if (r.base == NHIP_BASE_WORKSPACE) {
@@ -525,6 +550,7 @@ int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninp
         }
         if (rc) return fail("plan step " + std::to_string(i) + ": " + g_error);
     }
+    if (plan->profile && check(hipEventRecord(plan->events[plan->steps.size()], s), "hipEventRecord")) return 1;
     return 0;
 }
 

@@ -39,9 +39,17 @@ class DeviceBuffer:
     """A block of device memory from ``nhip_alloc``, freed when the last reference goes."""
 
     __slots__ = ("ptr", "nbytes", "device", "__weakref__")
+    # devices whose static region is reserved (lumen_amd.config.static_allocator_bytes)
+
+    _reserved: set = set()
 
     def __init__(self, device: int, nbytes: int):
         native.set_device(device)
+        if device not in DeviceBuffer._reserved:
+            from lumen_amd.config import config
+
+            native.call("nhip_region_reserve", device, int(config.static_allocator_bytes))
+            DeviceBuffer._reserved.add(device)
         self.device, self.nbytes = device, int(nbytes)
         self.ptr = native.alloc(device, max(1, self.nbytes))
 
