@@ -110,13 +110,18 @@ def trace(fn, args) -> Traced:
     for i, a in enumerate(traced_args):
         if isinstance(a, float):
             traced_args[i] = scalar(i, (), a)
+    # graph inputs in the reference's order: tensor arguments, runtime scalars, weights (tracer.py:371-500)
+    created = {}
+    for i, a in enumerate(traced_args):
+        if isinstance(a, (nn.Module, list, tuple)):
+            nn.map_tensors(a, lambda t: t, lambda path, v, i=i: created.setdefault((i, path), scalar(i, path, v)))
     weights = weights_of(args)
     winputs = {}
     for k, w in enumerate(weights):
         winputs[id(w)] = TracedTensor(graph, graph.input(w.dtype, w.shape))
         layout.append(("weight", k))
     mapped = [
-        nn.map_tensors(a, lambda t: winputs.get(id(t), t), lambda path, v, i=i: scalar(i, path, v))
+        nn.map_tensors(a, lambda t: winputs.get(id(t), t), lambda path, v, i=i: created.get((i, path), v))
         if isinstance(a, (nn.Module, list, tuple))
         else a
         for i, a in enumerate(traced_args)

@@ -428,10 +428,10 @@ static double next_after(double x, double y, int d) {
 static double fmax_nan(double a, double b) { return (isnan(a) || isnan(b)) ? NAN : (a > b ? a : b); }
 static double fmin_nan(double a, double b) { return (isnan(a) || isnan(b)) ? NAN : (a < b ? a : b); }
 
-/* Philox4x32-10 (reference/mod.rs:1162-1188). */
-static uint32_t philox_bits(uint64_t key, uint64_t counter) {
-    uint32_t k0 = (uint32_t)key, k1 = (uint32_t)(key >> 32);
-    uint32_t c0 = (uint32_t)counter, c1 = (uint32_t)(counter >> 32), c2 = 0, c3 = 0;
+/* Philox4x32-10: a 2-word key and 4-word counter to 4 random words (reference/mod.rs:1168-1188). */
+static void philox4x32(const uint32_t key[2], const uint32_t ctr[4], uint32_t out[4]) {
+    uint32_t k0 = key[0], k1 = key[1];
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
     for (int r = 0; r < 10; ++r) {
         if (r > 0) {
             k0 += 0x9E3779B9u;
@@ -442,8 +442,18 @@ static uint32_t philox_bits(uint64_t key, uint64_t counter) {
         uint32_t n0 = hi1 ^ c1 ^ k0, n1 = lo1, n2 = hi0 ^ c3 ^ k1, n3 = lo0;
         c0 = n0, c1 = n1, c2 = n2, c3 = n3;
     }
-    return c0;
+    out[0] = c0, out[1] = c1, out[2] = c2, out[3] = c3;
 }
+
+/* The first word of the block at counter (lo, hi, 0, 0) for a 64-bit key (reference/mod.rs:1162-1165). */
+static uint32_t philox_bits(uint64_t key, uint64_t counter) {
+    uint32_t k[2] = {(uint32_t)key, (uint32_t)(key >> 32)};
+    uint32_t c[4] = {(uint32_t)counter, (uint32_t)(counter >> 32), 0, 0}, o[4];
+    philox4x32(k, c, o);
+    return o[0];
+}
+
+void oracle_philox4x32(const uint32_t key[2], const uint32_t ctr[4], uint32_t out[4]) { philox4x32(key, ctr, out); }
 
 uint32_t oracle_philox(uint64_t key, uint64_t counter) { return philox_bits(key, counter); }
 

@@ -47,6 +47,8 @@ def lib():
         _lib.oracle_reduce_precision.restype = C.c_double
         _lib.oracle_philox.argtypes = [C.c_uint64, C.c_uint64]
         _lib.oracle_philox.restype = C.c_uint32
+        _lib.oracle_philox4x32.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
+        _lib.oracle_philox4x32.restype = None
     return _lib
 
 
@@ -111,3 +113,12 @@ def run(graph: Graph, inputs: list) -> list:
 def values(graph: Graph, inputs: list) -> list:
     """``run``'s outputs as NumPy values (bfloat16 widened to float32)."""
     return [D.to_numpy_values(o, graph.types[v].dtype) for o, v in zip(run(graph, inputs), graph.outputs)]
+
+
+def philox4x32(key, counter):
+    """Philox4x32-10 block of the oracle (for the Random123 known-answer tests)."""
+    k = (C.c_uint32 * 2)(*key)
+    c = (C.c_uint32 * 4)(*counter)
+    o = (C.c_uint32 * 4)()
+    lib().oracle_philox4x32(k, c, o)
+    return list(o)

@@ -1,0 +1,113 @@
+"""Compiler passes preserve values (the reference's pass tests run rewritten graphs through
+reference::run, lumen/graph_compiler/tests/mod.rs:140-148): cse, simplify, flash-attention matching and
+the fusion grouping, checked bit for bit with the oracle."""
+
+import numpy as np
+import pytest
+
+import lumen_amd as L
+import lumen_amd.functional as F
+from lumen_amd import dtypes as D
+from lumen_amd import workloads as W
+from lumen_amd.compiler import attention, fusion, passes
+from lumen_amd.graph.trace import trace
+from oracle import oracle
+
+
+def _inputs(g, seed=0):
+    rng = np.random.default_rng(seed)
+    out = []
+    for v in g.inputs:
+        t = g.types[v]
+        if t.dtype in ("int64", "int32"):
+            out.append(rng.integers(0, 7, t.shape).astype(D.storage(t.dtype)))
+        elif t.dtype == "bfloat16":
+            out.append(D.bf16_bits(rng.standard_normal(t.shape).astype(np.float32)))
+        else:
+            out.append(rng.standard_normal(t.shape).astype(D.storage(t.dtype)))
+    return out
+
+
+def _same(g0, g1, seed=0):
+    xs = _inputs(g0, seed)
+    for a, b in zip(oracle.run(g0, xs), oracle.run(g1, xs)):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+PROGRAMS = {
+    "mlp": (lambda x, w: F.softmax(F.relu(F.matmul(x, w, "float32", "float32")), -1) * 2.0,
+            [((8, 16), "float32"), ((16, 8), "float32")]),
+    "dup": (lambda x: F.exp(x) + F.exp(x) * F.exp(x), [((5, 3), "float32")]),
+    "casts": (lambda x, w: F.matmul(x, w, "float32", "bfloat16").float().bfloat16(),
+              [((4, 8), "bfloat16"), ((8, 4), "bfloat16")]),
+    "layouts": (lambda x: x.t().t().reshape(6, 2).reshape(3, 4) + 1.0, [((3, 4), "float32")]),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PROGRAMS))
+def test_frontend_preserves_values(name):
+    fn, shapes = PROGRAMS[name]
+    g = L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in shapes])
+    _same(g, passes.cse(g))
+    _same(g, passes.frontend(g))
+    assert len(passes.frontend(g).nodes) <= len(g.nodes)
+
+
+def test_cse_merges_duplicates():
+    fn, shapes = PROGRAMS["dup"]
+    g = L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in shapes])
+    assert sum(n.prim == "exp" for n in passes.cse(g).nodes) == 1
+
+
+def test_simplify_folds_narrowing_cast_into_dot():
+    fn, shapes = PROGRAMS["casts"]
+    g = passes.frontend(L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in shapes]))
+    dots = [n for n in g.nodes if n.prim == "dot_general"]
+    assert dots[0].params["output_dtype"] == "bfloat16"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_attention_match_preserves_values(causal):
+    def grads(q, k, v, do):
+        out, pull = L.vjp(lambda q, k, v: F.flash_attention(q, k, v, is_causal=causal), q, k, v)
+        return (out,) + pull(do)
+
+    g = L.make_graph(grads)(*[L.empty([1, 32, 2, 64], "bfloat16", "meta") for _ in range(4)])
+    m = attention.match(passes.frontend(g))
+    names = [n.params.get("name") for n in m.nodes if n.prim == "fusion"]
+    assert names == ["flash_attention", "flash_attention_backward"]
+    _same(g, m)
+
+
+def test_written_attention_matches():
+    """Attention written as matmul -> scale -> causal mask -> softmax -> matmul is recognized too."""
+
+    def attn(q, k, v):
+        s = F.matmul(q, k.transpose(-1, -2), "float32", "float32") * 0.125
+        rows = L.prims.iota("int64", s.shape, 2)
+        cols = L.prims.iota("int64", s.shape, 3)
+        s = F.where(cols <= rows, s, float("-inf"))
+        p = F.softmax(s, -1).bfloat16()
+        return F.matmul(p, v, "float32", "bfloat16")
+
+    g = L.make_graph(attn)(*[L.empty([2, 2, 32, 64], "bfloat16", "meta") for _ in range(3)])
+    m = attention.match(passes.frontend(g))
+    assert [n.params.get("name") for n in m.nodes if n.prim == "fusion"] == ["flash_attention"]
+    assert [n for n in m.nodes if n.prim == "fusion"][0].params["causal"] is True
+    _same(g, m)
+
+
+def test_fusion_of_the_training_step_preserves_dependencies():
+    """Every step reads only values computed by earlier steps or graph inputs, and every graph output is
+    written by some step (the tiny transformer step)."""
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    g = attention.match(passes.frontend(trace(W.train_step, (model, opt, ids, ids)).graph))
+    steps = fusion.fuse(g)
+    have = set(g.inputs)
+    for st in steps:
+        assert all(u in have for u in st.inputs), st.label()
+        have.update(st.outputs)
+    assert set(g.outputs) <= have
+    kinds = {st.kind for st in steps}
+    assert {"dot", "row", "flash_fwd", "flash_bwd", "scatter_add"} <= kinds

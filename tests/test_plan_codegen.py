@@ -1,0 +1,62 @@
+"""Plans on the CPU (no GPU needed): workspace placement never overlaps live values, layout ops feeding
+dots are strided views, and every generated loop kernel compiles for gfx950 with hipcc."""
+
+import pytest
+
+import lumen_amd as L
+import lumen_amd.functional as F
+from lumen_amd import workloads as W
+from lumen_amd.compiler.plan import Plan
+from lumen_amd.graph.trace import trace
+
+
+def _plan(fn, *metas, build=False):
+    g = L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in metas])
+    return Plan(g, build_kernels=build)
+
+
+def test_placement_never_overlaps_live_values():
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=False)
+    g = p.graph
+    first, last = {}, {}
+    for si, st in enumerate(p.steps):
+        for v in st.outputs:
+            first.setdefault(v, si)
+        for u in st.inputs:
+            last[u] = si
+    for v in g.outputs:
+        last[v] = len(p.steps)
+    spans = []
+    for v, si in first.items():
+        loc = p.loc[v]
+        if loc.base[0] != "ws" or p.steps[si].kind == "view":
+            continue
+        start = loc.offset * g.types[v].nbytes() // max(1, g.types[v].numel())
+        spans.append((si, last.get(v, si), start, start + g.types[v].nbytes(), v))
+    for a in spans:
+        for b in spans:
+            if a[4] < b[4] and a[0] <= b[1] and b[0] <= a[1]:
+                assert a[3] <= b[2] or b[3] <= a[2], (a, b)
+    assert p.workspace_bytes % 256 == 0
+
+
+def test_transposed_weight_feeds_the_dot_as_a_view():
+    p = _plan(lambda x, w: F.matmul(x, w.t(), "float32", "bfloat16"), ((64, 32), "bfloat16"), ((48, 32), "bfloat16"))
+    assert [s.kind for s in p.steps] == ["view", "dot"]
+    desc, ops = p._gemm_desc(p.steps[1].nodes[0])
+    assert (desc.m, desc.n, desc.k, desc.b_k, desc.b_n) == (64, 48, 32, 1, 32)
+
+
+def test_one_row_kernel_for_a_normalization_chain():
+    p = _plan(lambda x, w: F.softmax(F.rms_norm(x, 256, w) * 3.0, -1), ((32, 256), "float32"), ((256,), "float32"))
+    assert [s.kind for s in p.steps] == ["row"]
+
+
+@pytest.mark.timeout(600)
+def test_generated_kernels_compile_for_gfx950():
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=True)
+    assert len(p.objects) == len(p.sources) > 10
