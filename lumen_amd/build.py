@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libnhip.so")
-SOURCES = ["runtime.cpp", "kernels.hip"]
+SOURCES = ["runtime.cpp", "kernels.hip", "attention.hip"]
 FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -34,10 +34,25 @@ def build(verbose=False):
     """Compiles libnhip.so from csrc/ (always: this is the build check)."""
     from lumen_amd.compiler.kcache import hipcc
 
-    cmd = [hipcc()] + FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", OUT + ".tmp"]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    procs, objs = [], []
+    for src in SOURCES:  # one translation unit a process, in parallel
+        obj = os.path.join(objdir, src + ".o")
+        objs.append(obj)
+        cmd = [hipcc()] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    errors = []
+    for src, p in procs:
+        _, err = p.communicate()
+        if p.returncode != 0:
+            errors.append(f"{src}:\n{err[-6000:]}")
+    if errors:
+        raise RuntimeError("libnhip build failed:\n" + "\n".join(errors))
+    cmd = [hipcc()] + FLAGS + objs + ["-o", OUT + ".tmp"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError("libnhip build failed:\n" + r.stderr[-6000:])
+        raise RuntimeError("libnhip link failed:\n" + r.stderr[-6000:])
     os.replace(OUT + ".tmp", OUT)
     if verbose:
         print("built", OUT)

@@ -210,7 +210,7 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
                 q = graph.types[node.inputs[0]]
                 if kind == "flash_bwd":
                     b, sq, nh, _ = q.shape
-                    st.scratch = b * nh * sq * 4
+                    st.scratch = 2 * b * nh * sq * 4  # delta and base-2 LSE (nhip_flash_bwd_workspace)
                 elif len(outs) == 1:
                     st.scratch = graph.types[outs[0]].numel() // graph.types[outs[0]].shape[-1] * 4
         elif kinds[k] in ("view", "reduce"):

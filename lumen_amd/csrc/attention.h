@@ -27,6 +27,21 @@ __device__ __forceinline__ uint16_t to_half_bits(float f) {
     return F16 ? f32_to_f16(f) : f32_to_bf16(f);
 }
 
+// Two floats rounded (nearest even) to the 16-bit dtype and packed, the first in the low half. bf16 uses the
+// gfx950 conversion v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (F16) {
+        f16x2_t v = {_Float16(a), _Float16(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        bf16x2_t v = {__bf16(a), __bf16(b)};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+}
+
 template <bool F16>
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
     if constexpr (F16)
@@ -60,7 +75,7 @@ struct AttnParams {
 // ---- forward ------------------------------------------------------------------------------------------
 
 template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void flash_fwd_kernel_v1(AttnParams p) {
     constexpr int BN = 64;                 // keys per tile
     constexpr int PK = D + 8, PV = D + 16; // LDS pitches (elements)
     constexpr int DS = D / 16;             // k-steps over the head dim
@@ -197,6 +212,198 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(AttnParams p) {
 }
 
 
+// ---- forward, pipelined ------------------------------------------------------------------------------------
+//
+// Same algorithm and lane layout as above, arranged for the CDNA4 pipeline:
+//  * K and V tiles go from HBM straight into LDS (global_load_lds_dwordx4: no VGPR staging), double
+//    buffered: tile t+1 is in flight while tile t is computed; two workgroups share a CU (<= 256 registers
+//    a lane, 64 KiB LDS), so one's softmax VALU work overlaps the other's MFMAs.
+//  * A wave's 16-byte LDS writes are contiguous (lane i writes bytes 16i..16i+15 of a 1 KiB segment), so
+//    rows are unpadded and bank conflicts are avoided by an XOR swizzle of the 16-byte chunks of each row
+//    (chunk c of row r holds the row's chunk c ^ swz(r)); swz keeps both the row-wise K reads (16 rows,
+//    one chunk) and the transposed V reads (4 rows, 4 chunks) on distinct banks.
+//  * Softmax in base 2: p = 2^(s * scale * log2 e - m), with m a running maximum that is only raised
+//    when a row's maximum grows by more than 2^8 (so the O rescale runs rarely; P stays below 2^8 and
+//    its bf16 rounding has the same relative error). LSE = (m + log2 l) ln 2.
+//  * Masking code runs only on tiles that cross the causal diagonal or the end of the keys.
+//  * Causal workgroups start with the longest rows (query blocks in reverse order).
+
+template <int D>
+__device__ __forceinline__ int kv_swz(int r) {
+    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+}
+
+// Byte offset of element `col` (a multiple of 4) of row `r` in a swizzled tile of D-element rows.
+template <int D>
+__device__ __forceinline__ int kv_off(int r, int col) {
+    return r * (D * 2) + ((((col >> 3) ^ kv_swz<D>(r))) << 4) + ((col & 7) << 1);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Issues the loads of rows [k0, k0 + 64) of a [*, D] operand (row stride `rs` elements) into the swizzled
+// tile `dst`; rows past `rows` are clamped to the last row (their scores are masked).
+template <int D>
+__device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs, int64_t k0, int64_t rows,
+                                                uint16_t *dst, int wave, int lane) {
+    constexpr int RPS = 1024 / (D * 2);  // rows a wave instruction covers
+    constexpr int SEGS = 64 / RPS;       // 1 KiB segments in the tile
+#pragma unroll
+    for (int seg = wave; seg < SEGS; seg += 4) {
+        const int r = seg * RPS + lane / (D / 8);
+        const int c = lane % (D / 8);
+        int64_t row = k0 + r;
+        row = row < rows ? row : rows - 1;
+        const uint16_t *g = src + row * rs + ((c ^ kv_swz<D>(r)) << 3);
+        __builtin_amdgcn_global_load_lds(g, (lds_void_t *)(dst + seg * 512), 16, 0, 0);
+    }
+}
+
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
+    constexpr int BN = 64;
+    constexpr int DS = D / 16, DT = D / 32;
+    constexpr int TILE = BN * D;  // elements
+    __shared__ __align__(1024) uint16_t smem[4 * TILE];  // K0 V0 K1 V1
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nkv = n / (p.heads / p.kv_heads);
+    const int64_t qblk = CAUSAL ? int64_t(gridDim.x - 1 - blockIdx.x) : int64_t(blockIdx.x);
+    const int64_t q0 = qblk * 128;
+    const int64_t qi = q0 + wave * 32 + l32;
+    const bool qvalid = qi < p.sq;
+
+    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+
+    const int64_t shift = p.sk - p.sq;  // key j is visible to query i when j <= i + shift
+    int64_t kend = p.sk;
+    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
+    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
+    // tiles before `nfull` need no mask for any query of the workgroup
+    int64_t full_end = p.sk;
+    if (CAUSAL) full_end = min(full_end, q0 + shift + 1);
+    const int nfull = full_end > 0 ? int(full_end / BN) : 0;
+
+    if (ntiles > 0) {
+        load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane);
+        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
+    }
+
+    uint4 qf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t)
+        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+
+    f32x16_t acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+    const float c2 = p.scale * 1.4426950408889634f;  // scale * log2(e)
+    float m = -1e30f, l = 0.0f;                       // running max (base 2, scaled) and sum
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int64_t k0 = int64_t(kt) * BN;
+        const uint16_t *Ks = smem + (kt & 1) * 2 * TILE;
+        const uint16_t *Vs = Ks + TILE;
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile kt have landed
+        __syncthreads();                // ... and every thread's; tile kt-1's buffer is free
+        if (kt + 1 < ntiles) {
+            uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
+            load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
+            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
+        }
+        const char *Kb = reinterpret_cast<const char *>(Ks);
+        const char *Vb = reinterpret_cast<const char *>(Vs);
+
+        f32x16_t s[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[ks][e] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DS; ++t) {
+                uint4 a = *reinterpret_cast<const uint4 *>(Kb + kv_off<D>(32 * ks + l32, 16 * t + 8 * h));
+                s[ks] = mfma32<F16>(a, qf[t], s[ks]);
+            }
+        }
+        float mx = -INFINITY;
+        if (kt >= nfull) {  // diagonal or ragged tile
+            const int64_t lim = min(CAUSAL ? qi + shift : p.sk - 1, p.sk - 1) - k0 - 4 * h;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int kk = 32 * ks + 8 * (e / 4) + (e % 4);
+                    s[ks][e] = (kk <= lim) ? s[ks][e] : -INFINITY;
+                }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[ks][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c2;
+        // raise m only when some row's maximum outgrew it by 2^8
+        if (__any(mx > m + 8.0f)) {
+            const float mnew = fmaxf(m, mx);
+            const float alpha = exp2f(m - mnew);
+            l *= alpha;
+#pragma unroll
+            for (int i = 0; i < DT; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][e] *= alpha;
+            m = mnew;
+        }
+        float rs = 0.0f;
+        uint4 pb[4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const float e0 = exp2f(fmaf(s[ks][8 * half + j], c2, -m));
+                    const float e1 = exp2f(fmaf(s[ks][8 * half + j + 1], c2, -m));
+                    rs += e0 + e1;
+                    w[j / 2] = pack2<F16>(e0, e1);
+                }
+                pb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        l += rs + __shfl_xor(rs, 32, 64);
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+            const int key = 16 * t2 + 4 * h + s16 / 4;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Vb + kv_off<D>(key, col)));
+                v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Vb + kv_off<D>(key + 8, col)));
+                uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                acc[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), pb[t2], acc[dt]);
+            }
+        }
+    }
+
+    if (!qvalid) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    uint16_t *op = p.o + b * p.o_b + n * p.o_n + qi * p.o_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const uint32_t w0 = pack2<F16>(acc[dt][4 * e4 + 0] * inv, acc[dt][4 * e4 + 1] * inv);
+            const uint32_t w1 = pack2<F16>(acc[dt][4 * e4 + 2] * inv, acc[dt][4 * e4 + 3] * inv);
+            *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
+        }
+    if (h == 0 && p.lse) p.lse[(b * p.heads + n) * p.sq + qi] = l > 0.0f ? (m + __log2f(l)) * 0.6931471805599453f : -INFINITY;
+}
+
 // ---- backward ---------------------------------------------------------------------------------------------
 
 // delta[b, n, q] = sum_d dO * O in float32 (flash.py:67-68 computes it as a dot); one wavefront a query row.
@@ -223,7 +430,7 @@ __global__ __launch_bounds__(256) void flash_delta_kernel_t(AttnParams p) {
 // dK and dV for 128 keys (32 a wavefront), looping over 64-query tiles of every query head that shares
 // the key/value head (grouped-query attention sums them, flash.py:80-84).
 template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void flash_dkdv_kernel_v1(AttnParams p) {
     constexpr int BM = 64;
     constexpr int PQ = D + 16;  // Q and dO tiles: row reads and transposed reads
     constexpr int DS = D / 16, DT = D / 32;
@@ -357,7 +564,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p) {
 // dQ for 128 queries (32 a wavefront), looping over 64-key tiles: S^T and dP^T one query a lane, dQ^T
 // accumulated in registers (deterministic: no atomics).
 template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_dq_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void flash_dq_kernel_v1(AttnParams p) {
     constexpr int BN = 64;
     constexpr int PK = D + 16, PV = D + 8;
     constexpr int DS = D / 16, DT = D / 32;
@@ -464,12 +671,319 @@ __global__ __launch_bounds__(256) void flash_dq_kernel(AttnParams p) {
         }
 }
 
+// ---- backward, pipelined -----------------------------------------------------------------------------------
+//
+// The FA-2 backward arranged like the pipelined forward: operand tiles stream HBM -> LDS with
+// global_load_lds into swizzled, double-buffered tiles; P = 2^(s * scale * log2 e - lse * log2 e) with the
+// base-2 LSE written once by the delta kernel; masks only on tiles that cross the diagonal or the end of the
+// queries.
+
+// delta = rowsum(dO * O) and lse2 = lse * log2(e), float32 [B, N, Sq] each; one wavefront a query row.
+template <int D, bool F16>
+__global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *lse2) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t b = blockIdx.y;
+    if (row >= p.heads * p.sq) return;
+    const int64_t n = row / p.sq, q = row % p.sq;
+    const uint16_t *o = p.o_in + b * p.o_b + n * p.o_n + q * p.o_s;
+    const uint16_t *g = p.d_o + b * p.do_b + n * p.do_n + q * p.do_s;
+    float acc = 0.0f;
+    for (int d = lane; d < D; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
+    acc = wave_sum(acc);
+    const int64_t i = (b * p.heads + n) * p.sq + q;
+    if (lane == 0) {
+        p.delta[i] = acc;
+        lse2[i] = p.lse_in[i] * 1.4426950408889634f;
+    }
+}
+
+// 64 floats [k0, k0 + 64) of `src` (clamped to `rows`) into LDS by one wavefront.
+__device__ __forceinline__ void load_row64_async(const float *src, int64_t k0, int64_t rows, float *dst, int lane) {
+    int64_t r = k0 + lane;
+    r = r < rows ? r : rows - 1;
+    __builtin_amdgcn_global_load_lds(src + r, (lds_void_t *)dst, 4, 0, 0);
+}
+
+// dK and dV for 128 keys (32 a wavefront, one key a lane of the C layout), looping over 64-query tiles of
+// every query head sharing the key/value head.
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const float *lse2) {
+    constexpr int BM = 64;
+    constexpr int DS = D / 16, DT = D / 32;
+    constexpr int TILE = BM * D;
+    __shared__ __align__(1024) uint16_t smem[4 * TILE];  // Q0 dO0 Q1 dO1
+    __shared__ float Ls[2][BM], Dl[2][BM];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t b = blockIdx.z, nkv = blockIdx.y;
+    const int64_t kb0 = int64_t(blockIdx.x) * 128;
+    const int64_t kj = kb0 + wave * 32 + l32;
+    const bool kvalid = kj < p.sk;
+    const int64_t group = p.heads / p.kv_heads;
+    const int64_t shift = p.sk - p.sq;
+
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+
+    // query tiles: [qstart, sq) for every head of the group; tile j < nfull needs no mask
+    int64_t qstart = 0;
+    if (CAUSAL) qstart = max<int64_t>(0, kb0 - shift) / BM * BM;
+    const int per_head = p.sq > qstart ? int((p.sq - qstart + BM - 1) / BM) : 0;
+    const int total = per_head * int(group);
+    auto tile_src = [&](int j, const uint16_t *&qp, const uint16_t *&gp, const float *&ls, const float *&dl,
+                        int64_t &q0) {
+        const int64_t gi = j / per_head;
+        q0 = qstart + int64_t(j % per_head) * BM;
+        const int64_t n = nkv * group + gi;
+        qp = p.q + b * p.q_b + n * p.q_n;
+        gp = p.d_o + b * p.do_b + n * p.do_n;
+        ls = lse2 + (b * p.heads + n) * p.sq;
+        dl = p.delta + (b * p.heads + n) * p.sq;
+    };
+    auto issue = [&](int j) {
+        const uint16_t *qp, *gp;
+        const float *ls, *dl;
+        int64_t q0;
+        tile_src(j, qp, gp, ls, dl, q0);
+        uint16_t *dst = smem + (j & 1) * 2 * TILE;
+        load_tile_async<D>(qp, p.q_s, q0, p.sq, dst, wave, lane);
+        load_tile_async<D>(gp, p.do_s, q0, p.sq, dst + TILE, wave, lane);
+        if (wave == 0) load_row64_async(ls, q0, p.sq, Ls[j & 1], lane);
+        if (wave == 1) load_row64_async(dl, q0, p.sq, Dl[j & 1], lane);
+    };
+    if (total > 0) issue(0);
+
+    uint4 kf[DS], vf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+        kf[t] = kvalid ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        vf[t] = kvalid ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+    }
+    f32x16_t adk[DT], adv[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) adk[i][e] = adv[i][e] = 0.0f;
+    const float c2 = p.scale * 1.4426950408889634f;
+
+    for (int j = 0; j < total; ++j) {
+        int64_t q0;
+        {
+            const uint16_t *qp, *gp;
+            const float *ls, *dl;
+            tile_src(j, qp, gp, ls, dl, q0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 1 < total) issue(j + 1);
+        const char *Qb = reinterpret_cast<const char *>(smem + (j & 1) * 2 * TILE);
+        const char *Gb = Qb + TILE * 2;
+        const float *Lt = Ls[j & 1], *Dt = Dl[j & 1];
+        // rows q with q > sq - 1 or (causal) kj > q + shift are masked
+        const bool masked = q0 + BM > p.sq || (CAUSAL && q0 + shift < kb0 + 127);
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            f32x16_t sv, dp;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DS; ++t) {
+                const int off = kv_off<D>(32 * qs + l32, 16 * t + 8 * h);
+                uint4 a = *reinterpret_cast<const uint4 *>(Qb + off);
+                uint4 c = *reinterpret_cast<const uint4 *>(Gb + off);
+                sv = mfma32<F16>(a, kf[t], sv);
+                dp = mfma32<F16>(c, vf[t], dp);
+            }
+            uint4 pb[2], sb[2];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t wp[4], ws[4];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj += 2) {
+                    float pv[2], dv2[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = 8 * half + jj + u;
+                        const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
+                        float pe = exp2f(fmaf(sv[e], c2, -Lt[r]));
+                        if (masked) {
+                            const int64_t q = q0 + r;
+                            const bool ok = q < p.sq && (!CAUSAL || kj <= q + shift);
+                            pe = ok ? pe : 0.0f;
+                        }
+                        pv[u] = pe;
+                        dv2[u] = pe * (dp[e] - Dt[r]) * p.scale;
+                    }
+                    wp[jj / 2] = pack2<F16>(pv[0], pv[1]);
+                    ws[jj / 2] = pack2<F16>(dv2[0], dv2[1]);
+                }
+                pb[half] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
+                sb[half] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int r0 = 32 * qs + 16 * half + 4 * h + s16 / 4;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                    const int o0 = kv_off<D>(r0, col), o1 = kv_off<D>(r0 + 8, col);
+                    v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o0));
+                    v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o1));
+                    uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                    adv[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), pb[half], adv[dt]);
+                    x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o0));
+                    y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o1));
+                    xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                    adk[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), sb[half], adk[dt]);
+                }
+            }
+        }
+    }
+    if (!kvalid) return;
+    uint16_t *dkp = p.dk + b * p.dk_b + nkv * p.dk_n + kj * p.dk_s;
+    uint16_t *dvp = p.dv + b * p.dv_b + nkv * p.dv_n + kj * p.dv_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int d = 32 * dt + 8 * e4 + 4 * h;
+            *reinterpret_cast<uint2 *>(dkp + d) =
+                make_uint2(pack2<F16>(adk[dt][4 * e4], adk[dt][4 * e4 + 1]), pack2<F16>(adk[dt][4 * e4 + 2], adk[dt][4 * e4 + 3]));
+            *reinterpret_cast<uint2 *>(dvp + d) =
+                make_uint2(pack2<F16>(adv[dt][4 * e4], adv[dt][4 * e4 + 1]), pack2<F16>(adv[dt][4 * e4 + 2], adv[dt][4 * e4 + 3]));
+        }
+}
+
+// dQ for 128 queries (32 a wavefront), looping over 64-key tiles: S^T and dP^T one query a lane, dQ^T
+// accumulated in registers (deterministic: no atomics).
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const float *lse2) {
+    constexpr int BN = 64;
+    constexpr int DS = D / 16, DT = D / 32;
+    constexpr int TILE = BN * D;
+    __shared__ __align__(1024) uint16_t smem[4 * TILE];  // K0 V0 K1 V1
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nkv = n / (p.heads / p.kv_heads);
+    const int64_t qblk = CAUSAL ? int64_t(gridDim.x - 1 - blockIdx.x) : int64_t(blockIdx.x);
+    const int64_t q0 = qblk * 128;
+    const int64_t qi = q0 + wave * 32 + l32;
+    const bool qvalid = qi < p.sq;
+    const int64_t shift = p.sk - p.sq;
+
+    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
+    const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
+
+    int64_t kend = p.sk;
+    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
+    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
+    int64_t full_end = p.sk;
+    if (CAUSAL) full_end = min(full_end, q0 + shift + 1);
+    const int nfull = full_end > 0 ? int(full_end / BN) : 0;
+    if (ntiles > 0) {
+        load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane);
+        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
+    }
+
+    uint4 qf[DS], gf[DS];
+#pragma unroll
+    for (int t = 0; t < DS; ++t) {
+        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        gf[t] = qvalid ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+    }
+    const float l2 = qvalid ? lse2[(b * p.heads + n) * p.sq + qi] : 0.0f;
+    const float dl = qvalid ? p.delta[(b * p.heads + n) * p.sq + qi] : 0.0f;
+    const float c2 = p.scale * 1.4426950408889634f;
+    f32x16_t acc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int64_t k0 = int64_t(kt) * BN;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (kt + 1 < ntiles) {
+            uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
+            load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
+            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
+        }
+        const char *Kb = reinterpret_cast<const char *>(smem + (kt & 1) * 2 * TILE);
+        const char *Vb = Kb + TILE * 2;
+        const bool masked = kt >= nfull;
+        const int64_t lim = min(CAUSAL ? qi + shift : p.sk - 1, p.sk - 1) - k0 - 4 * h;
+        uint4 sb[4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            f32x16_t sv, dp;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DS; ++t) {
+                const int off = kv_off<D>(32 * ks + l32, 16 * t + 8 * h);
+                uint4 a = *reinterpret_cast<const uint4 *>(Kb + off);
+                uint4 c = *reinterpret_cast<const uint4 *>(Vb + off);
+                sv = mfma32<F16>(a, qf[t], sv);
+                dp = mfma32<F16>(c, gf[t], dp);
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t w[4];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj += 2) {
+                    float ds2[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int e = 8 * half + jj + u;
+                        float pe = exp2f(fmaf(sv[e], c2, -l2));
+                        if (masked) {
+                            const int kk = 32 * ks + 8 * (e / 4) + (e % 4);
+                            pe = (qvalid && kk <= lim) ? pe : 0.0f;
+                        }
+                        ds2[u] = pe * (dp[e] - dl) * p.scale;
+                    }
+                    w[jj / 2] = pack2<F16>(ds2[0], ds2[1]);
+                }
+                sb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+#pragma unroll
+        for (int t2 = 0; t2 < 4; ++t2) {
+            const int r0 = 16 * t2 + 4 * h + s16 / 4;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Kb + kv_off<D>(r0, col)));
+                v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Kb + kv_off<D>(r0 + 8, col)));
+                uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                acc[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), sb[t2], acc[dt]);
+            }
+        }
+    }
+    if (!qvalid) return;
+    uint16_t *dqp = p.dq + b * p.dq_b + n * p.dq_n + qi * p.dq_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+            *reinterpret_cast<uint2 *>(dqp + 32 * dt + 8 * e4 + 4 * h) =
+                make_uint2(pack2<F16>(acc[dt][4 * e4], acc[dt][4 * e4 + 1]), pack2<F16>(acc[dt][4 * e4 + 2], acc[dt][4 * e4 + 3]));
+}
+
 }  // namespace nhipk
 
 namespace nhip {
 
+// delta and the base-2 LSE, float32 [B, N, Sq] each.
 inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
-    return size_t(d->batch) * d->heads * d->sq * sizeof(float);
+    return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
 }
 
 inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
@@ -502,7 +1016,10 @@ inline int check_attn(const nhip_attn_desc *d, const char *what) {
 template <int D, bool F16, bool CAUSAL>
 int launch_fwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
     dim3 grid(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
-    hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
+    if (d->config == 1)
+        hipLaunchKernelGGL((nhipk::flash_fwd_kernel_v1<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
     return check(hipGetLastError(), "flash_fwd launch");
 }
 
@@ -532,13 +1049,22 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
 template <int D, bool F16, bool CAUSAL>
 int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
     dim3 gd(unsigned((d->heads * d->sq + 3) / 4), unsigned(d->batch));
-    hipLaunchKernelGGL((nhipk::flash_delta_kernel_t<D, F16>), gd, dim3(256), 0, s, p);
-    if (check(hipGetLastError(), "flash delta launch")) return 1;
     dim3 gk(unsigned((d->sk + 127) / 128), unsigned(d->kv_heads), unsigned(d->batch));
-    hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p);
-    if (check(hipGetLastError(), "flash dkdv launch")) return 1;
     dim3 gq(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
-    hipLaunchKernelGGL((nhipk::flash_dq_kernel<D, F16, CAUSAL>), gq, dim3(256), 0, s, p);
+    if (d->config == 1) {
+        hipLaunchKernelGGL((nhipk::flash_delta_kernel_t<D, F16>), gd, dim3(256), 0, s, p);
+        if (check(hipGetLastError(), "flash delta launch")) return 1;
+        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel_v1<D, F16, CAUSAL>), gk, dim3(256), 0, s, p);
+        if (check(hipGetLastError(), "flash dkdv launch")) return 1;
+        hipLaunchKernelGGL((nhipk::flash_dq_kernel_v1<D, F16, CAUSAL>), gq, dim3(256), 0, s, p);
+        return check(hipGetLastError(), "flash dq launch");
+    }
+    float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
+    hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
+    if (check(hipGetLastError(), "flash delta launch")) return 1;
+    hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p, lse2);
+    if (check(hipGetLastError(), "flash dkdv launch")) return 1;
+    hipLaunchKernelGGL((nhipk::flash_dq_kernel<D, F16, CAUSAL>), gq, dim3(256), 0, s, p, lse2);
     return check(hipGetLastError(), "flash dq launch");
 }
 

@@ -1,9 +1,7 @@
-// Built-in kernels of libnhip and their C entry points: nhip_gemm (dot_general), the flash attention
-// forward and backward, and the fill used by plans (a kernel, not hipMemsetAsync, so a captured plan
-// replays it correctly).
+// Built-in kernels of libnhip and their C entry points: nhip_gemm (dot_general) and the fill used by plans
+// (a kernel, not hipMemsetAsync, so a captured plan replays it correctly).
 #include <cstring>
 
-#include "attention.h"
 #include "gemm.h"
 #include "nhip_internal.h"
 
@@ -202,24 +200,6 @@ int nhip_gemm(const nhip_gemm_desc *desc, const void *a, const void *b, void *d)
 
 int nhip_gemm_config_count(int *count) {
     *count = kNumConfigs;
-    return 0;
-}
-
-int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, void *o, float *lse) {
-    hipStream_t s = stream_of_current();
-    if (!s) return fail("no HIP stream: call nhip_set_device first");
-    return flash_fwd_on(s, desc, q, k, v, o, lse);
-}
-
-int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
-                   const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace) {
-    hipStream_t s = stream_of_current();
-    if (!s) return fail("no HIP stream: call nhip_set_device first");
-    return flash_bwd_on(s, desc, q, k, v, o, d_o, lse, dq, dk, dv, workspace);
-}
-
-int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes) {
-    *bytes = flash_bwd_workspace_bytes(desc);
     return 0;
 }
 

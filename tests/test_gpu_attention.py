@@ -22,6 +22,7 @@ CASES = [
     (2, 200, 200, 2, 1, 128, True),
     (1, 64, 192, 4, 2, 128, True),
     (1, 96, 160, 1, 1, 64, False),
+    (1, 1024, 1024, 2, 1, 128, True),
 ]
 
 
