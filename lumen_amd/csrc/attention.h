@@ -1,5 +1,6 @@
-// Flash attention for gfx950: forward, and the FlashAttention-2 backward as three kernels (delta, dK/dV per
-// key block, dQ per query block), following the algorithm of lumen/codegen/attention/triton/kernel.py:34-256.
+// Flash attention for gfx950: forward, and the FlashAttention-2 backward as three kernels (prep: delta and
+// base-2 LSE; dK/dV per key block; dQ per query block), following the algorithm of
+// lumen/codegen/attention/triton/kernel.py:34-256.
 //
 // Layout choices (all MFMA v_mfma_f32_32x32x16_{bf16,f16}, float32 accumulation):
 //  * The forward computes S^T = K Q^T, so the 32x32 C layout puts one query in each lane (lane % 32) and its
@@ -9,9 +10,7 @@
 //    {4h..4h+3, 8+4h..8+4h+3} of each 16-key step, and V^T is read with that same key order from LDS by two
 //    ds_read_tr16_b64 (4 consecutive keys at one head-dim column each). O^T accumulates in registers, one
 //    query a lane, so the per-query rescale of the online softmax is a multiply by a lane scalar.
-//  * K tiles are read row-wise with ds_read_b128 (pitch D + 8 elements: conflict-free for 8 lanes), V
-//    tiles transposed with ds_read_tr16_b64 (pitch D + 16: four rows of 32 bytes on disjoint banks).
-//  * P is rounded to the inputs' dtype before P V, as the reference does (kernel.py:99); LSE = m + log(l).
+//  * P is rounded to the inputs' dtype before P V, as the reference does (kernel.py:99).
 #pragma once
 
 #include "device_common.h"
@@ -72,147 +71,7 @@ struct AttnParams {
     float scale;
 };
 
-// ---- forward ------------------------------------------------------------------------------------------
-
-template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_fwd_kernel_v1(AttnParams p) {
-    constexpr int BN = 64;                 // keys per tile
-    constexpr int PK = D + 8, PV = D + 16; // LDS pitches (elements)
-    constexpr int DS = D / 16;             // k-steps over the head dim
-    constexpr int DT = D / 32;             // 32-wide head-dim tiles of O^T
-    __shared__ __align__(16) uint16_t Ks[BN * PK];
-    __shared__ __align__(16) uint16_t Vs[BN * PV];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
-    const int64_t b = blockIdx.z, n = blockIdx.y;
-    const int64_t nkv = n / (p.heads / p.kv_heads);
-    const int64_t q0 = int64_t(blockIdx.x) * 128;
-    const int64_t qi = q0 + wave * 32 + l32;  // this lane's query
-    const bool qvalid = qi < p.sq;
-
-    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
-    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
-    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
-
-    uint4 qf[DS];
-#pragma unroll
-    for (int t = 0; t < DS; ++t)
-        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-
-    f32x16_t acc[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-    const int64_t shift = p.sk - p.sq;  // bottom-right aligned causal mask: key <= query + shift
-    int64_t kend = p.sk;
-    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
-    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
-
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int64_t k0 = int64_t(kt) * BN;
-        // cooperative tile loads: BN rows x D columns, 16 bytes a thread per pass
-        constexpr int CH = D / 8;
-#pragma unroll
-        for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
-            int r = idx / CH, c = idx % CH;
-            int64_t key = k0 + r;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (key < p.sk) {
-                kv = *reinterpret_cast<const uint4 *>(kp + key * p.k_s + c * 8);
-                vv = *reinterpret_cast<const uint4 *>(vp + key * p.v_s + c * 8);
-            }
-            *reinterpret_cast<uint4 *>(Ks + r * PK + c * 8) = kv;
-            *reinterpret_cast<uint4 *>(Vs + r * PV + c * 8) = vv;
-        }
-        __syncthreads();
-
-        // S^T for the two 32-key halves of the tile
-        f32x16_t s[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[ks][e] = 0.0f;
-#pragma unroll
-            for (int t = 0; t < DS; ++t) {
-                uint4 a = *reinterpret_cast<const uint4 *>(Ks + (32 * ks + l32) * PK + 16 * t + 8 * h);
-                s[ks] = mfma32<F16>(a, qf[t], s[ks]);
-            }
-        }
-        // scale, mask, running max
-        float mx = -INFINITY;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                int64_t key = k0 + 32 * ks + 8 * (e / 4) + 4 * h + (e % 4);
-                float x = s[ks][e] * p.scale;
-                bool ok = key < p.sk && (!CAUSAL || key <= qi + shift);
-                x = ok ? x : -INFINITY;
-                s[ks][e] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx);
-        const float alpha = (mnew == -INFINITY) ? 1.0f : __expf(m - mnew);
-        float rs = 0.0f;
-        uint4 pb[4];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint32_t w[4];
-#pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    float e0 = (mnew == -INFINITY) ? 0.0f : __expf(s[ks][8 * half + j] - mnew);
-                    float e1 = (mnew == -INFINITY) ? 0.0f : __expf(s[ks][8 * half + j + 1] - mnew);
-                    rs += e0 + e1;
-                    w[j / 2] = uint32_t(to_half_bits<F16>(e0)) | (uint32_t(to_half_bits<F16>(e1)) << 16);
-                }
-                pb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        }
-        rs += __shfl_xor(rs, 32, 64);
-        l = l * alpha + rs;
-        m = mnew;
-#pragma unroll
-        for (int i = 0; i < DT; ++i)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][e] *= alpha;
-        // O^T += V^T P^T, 16 keys a step in the permuted order
-        const int g = lane >> 4, s16 = lane & 15;
-#pragma unroll
-        for (int t2 = 0; t2 < 4; ++t2) {
-            const int key0 = 16 * t2 + 4 * h + s16 / 4;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
-                uint4 a = read_tr_pair(Vs + key0 * PV + col, Vs + (key0 + 8) * PV + col);
-                acc[dt] = mfma32<F16>(a, pb[t2], acc[dt]);
-            }
-        }
-        __syncthreads();
-    }
-
-    if (!qvalid) return;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    uint16_t *op = p.o + b * p.o_b + n * p.o_n + qi * p.o_s;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-            uint32_t w0 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 0] * inv)) |
-                          (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 1] * inv)) << 16);
-            uint32_t w1 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 2] * inv)) |
-                          (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 3] * inv)) << 16);
-            *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
-        }
-    if (h == 0 && p.lse) p.lse[(b * p.heads + n) * p.sq + qi] = m + __logf(l);
-}
-
-
-// ---- forward, pipelined ------------------------------------------------------------------------------------
+// ---- forward ------------------------------------------------------------------------------------
 //
 // Same algorithm and lane layout as above, arranged for the CDNA4 pipeline:
 //  * K and V tiles go from HBM straight into LDS (global_load_lds_dwordx4: no VGPR staging), double
@@ -227,6 +86,26 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel_v1(AttnParams p) {
 //    its bf16 rounding has the same relative error). LSE = (m + log2 l) ln 2.
 //  * Masking code runs only on tiles that cross the causal diagonal or the end of the keys.
 //  * Causal workgroups start with the longest rows (query blocks in reverse order).
+
+// 2^x by the hardware v_exp_f32 (no denormal-range fixup: results below 2^-126 may flush to zero, which
+// rounds away in P's 16-bit dtype anyway).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup order: `units` independent units (a batch-head pair) of `per` workgroups each. Workgroups are
+// dispatched round-robin over the 8 XCDs by linear id, so when units divide evenly each XCD gets whole
+// units, in order, and the workgroups running together on an XCD share their unit's K/V (or Q/dO) in its
+// L2. Returns the unit and the workgroup's index in it.
+__device__ __forceinline__ void xcd_order(int64_t units, int64_t per, int64_t &unit, int64_t &idx) {
+    const int64_t lin = blockIdx.x;
+    if (units % 8 == 0) {
+        const int64_t x = lin % 8, j = lin / 8;
+        unit = (j / per) * 8 + x;
+        idx = j % per;
+    } else {
+        unit = lin / per;
+        idx = lin % per;
+    }
+}
 
 template <int D>
 __device__ __forceinline__ int kv_swz(int r) {
@@ -269,12 +148,16 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
-    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nqb = (p.sq + 127) / 128;
+    int64_t unit, qblk;
+    xcd_order(int64_t(gridDim.x) / nqb, nqb, unit, qblk);
+    if (CAUSAL) qblk = nqb - 1 - qblk;  // longest rows first
+    const int64_t b = unit / p.heads, n = unit % p.heads;
     const int64_t nkv = n / (p.heads / p.kv_heads);
-    const int64_t qblk = CAUSAL ? int64_t(gridDim.x - 1 - blockIdx.x) : int64_t(blockIdx.x);
     const int64_t q0 = qblk * 128;
     const int64_t qi = q0 + wave * 32 + l32;
     const bool qvalid = qi < p.sq;
+    const int64_t wq_last = q0 + wave * 32 + 31;  // the wave's last query
 
     const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
     const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
@@ -318,6 +201,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
             load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
             load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
         }
+        if (CAUSAL && k0 > wq_last + shift) continue;  // every key of the tile is masked for this wave
         const char *Kb = reinterpret_cast<const char *>(Ks);
         const char *Vb = reinterpret_cast<const char *>(Vs);
 
@@ -351,7 +235,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
         // raise m only when some row's maximum outgrew it by 2^8
         if (__any(mx > m + 8.0f)) {
             const float mnew = fmaxf(m, mx);
-            const float alpha = exp2f(m - mnew);
+            const float alpha = fast_exp2(m - mnew);
             l *= alpha;
 #pragma unroll
             for (int i = 0; i < DT; ++i)
@@ -368,8 +252,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
                 uint32_t w[4];
 #pragma unroll
                 for (int j = 0; j < 8; j += 2) {
-                    const float e0 = exp2f(fmaf(s[ks][8 * half + j], c2, -m));
-                    const float e1 = exp2f(fmaf(s[ks][8 * half + j + 1], c2, -m));
+                    const float e0 = fast_exp2(fmaf(s[ks][8 * half + j], c2, -m));
+                    const float e1 = fast_exp2(fmaf(s[ks][8 * half + j + 1], c2, -m));
                     rs += e0 + e1;
                     w[j / 2] = pack2<F16>(e0, e1);
                 }
@@ -404,274 +288,12 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
     if (h == 0 && p.lse) p.lse[(b * p.heads + n) * p.sq + qi] = l > 0.0f ? (m + __log2f(l)) * 0.6931471805599453f : -INFINITY;
 }
 
-// ---- backward ---------------------------------------------------------------------------------------------
-
-// delta[b, n, q] = sum_d dO * O in float32 (flash.py:67-68 computes it as a dot); one wavefront a query row.
 template <bool F16>
 __device__ __forceinline__ float half_to_f32(uint16_t v) {
     return F16 ? f16_to_f32(v) : bf16_to_f32(v);
 }
 
-template <int D, bool F16>
-__global__ __launch_bounds__(256) void flash_delta_kernel_t(AttnParams p) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int64_t b = blockIdx.y;
-    if (row >= p.heads * p.sq) return;
-    const int64_t n = row / p.sq, q = row % p.sq;
-    const uint16_t *o = p.o_in + b * p.o_b + n * p.o_n + q * p.o_s;
-    const uint16_t *g = p.d_o + b * p.do_b + n * p.do_n + q * p.do_s;
-    float acc = 0.0f;
-    for (int d = lane; d < D; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
-    acc = wave_sum(acc);
-    if (lane == 0) p.delta[(b * p.heads + n) * p.sq + q] = acc;
-}
-
-// dK and dV for 128 keys (32 a wavefront), looping over 64-query tiles of every query head that shares
-// the key/value head (grouped-query attention sums them, flash.py:80-84).
-template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_dkdv_kernel_v1(AttnParams p) {
-    constexpr int BM = 64;
-    constexpr int PQ = D + 16;  // Q and dO tiles: row reads and transposed reads
-    constexpr int DS = D / 16, DT = D / 32;
-    __shared__ __align__(16) uint16_t Qs[BM * PQ];
-    __shared__ __align__(16) uint16_t Gs[BM * PQ];
-    __shared__ float Ls[BM], Ds[BM];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
-    const int g = lane >> 4, s16 = lane & 15;
-    const int64_t b = blockIdx.z, nkv = blockIdx.y;
-    const int64_t key0 = int64_t(blockIdx.x) * 128 + wave * 32;
-    const int64_t kj = key0 + l32;  // this lane's key (C-layout column)
-    const bool kvalid = kj < p.sk;
-    const int64_t group = p.heads / p.kv_heads;
-    const int64_t shift = p.sk - p.sq;
-
-    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
-    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
-    uint4 kf[DS], vf[DS];
-#pragma unroll
-    for (int t = 0; t < DS; ++t) {
-        kf[t] = kvalid ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        vf[t] = kvalid ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-    }
-    f32x16_t adk[DT], adv[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) adk[i][e] = adv[i][e] = 0.0f;
-
-    // first query that can see the workgroup's first key
-    int64_t qstart = 0;
-    if (CAUSAL) qstart = max<int64_t>(0, int64_t(blockIdx.x) * 128 - shift);
-    qstart = qstart / BM * BM;
-    for (int64_t gi = 0; gi < group; ++gi) {
-        const int64_t n = nkv * group + gi;
-        const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
-        const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
-        const float *lse = p.lse_in + (b * p.heads + n) * p.sq;
-        const float *dl = p.delta + (b * p.heads + n) * p.sq;
-        for (int64_t q0 = qstart; q0 < p.sq; q0 += BM) {
-            constexpr int CH = D / 8;
-            for (int idx = threadIdx.x; idx < BM * CH; idx += 256) {
-                int r = idx / CH, c = idx % CH;
-                int64_t q = q0 + r;
-                uint4 a = make_uint4(0, 0, 0, 0), d = make_uint4(0, 0, 0, 0);
-                if (q < p.sq) {
-                    a = *reinterpret_cast<const uint4 *>(qp + q * p.q_s + c * 8);
-                    d = *reinterpret_cast<const uint4 *>(gp + q * p.do_s + c * 8);
-                }
-                *reinterpret_cast<uint4 *>(Qs + r * PQ + c * 8) = a;
-                *reinterpret_cast<uint4 *>(Gs + r * PQ + c * 8) = d;
-            }
-            if (threadIdx.x < BM) {
-                int64_t q = q0 + threadIdx.x;
-                Ls[threadIdx.x] = q < p.sq ? lse[q] : 0.0f;
-                Ds[threadIdx.x] = q < p.sq ? dl[q] : 0.0f;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int qs = 0; qs < 2; ++qs) {
-                // S and dP for 32 queries (rows) x this wave's 32 keys (columns)
-                f32x16_t sv, dp;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
-#pragma unroll
-                for (int t = 0; t < DS; ++t) {
-                    uint4 a = *reinterpret_cast<const uint4 *>(Qs + (32 * qs + l32) * PQ + 16 * t + 8 * h);
-                    uint4 c = *reinterpret_cast<const uint4 *>(Gs + (32 * qs + l32) * PQ + 16 * t + 8 * h);
-                    sv = mfma32<F16>(a, kf[t], sv);
-                    dp = mfma32<F16>(c, vf[t], dp);
-                }
-                uint4 pb[2], sb[2];
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    uint32_t wp[4], ws[4];
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        float pv[2], dv2[2];
-#pragma unroll
-                        for (int u = 0; u < 2; ++u) {
-                            const int e = 8 * half + j + u;
-                            const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
-                            const int64_t q = q0 + r;
-                            bool ok = q < p.sq && kvalid && (!CAUSAL || kj <= q + shift);
-                            float x = sv[e] * p.scale;
-                            float pe = ok ? __expf(x - Ls[r]) : 0.0f;
-                            pv[u] = pe;
-                            dv2[u] = pe * (dp[e] - Ds[r]) * p.scale;
-                        }
-                        wp[j / 2] = uint32_t(to_half_bits<F16>(pv[0])) | (uint32_t(to_half_bits<F16>(pv[1])) << 16);
-                        ws[j / 2] = uint32_t(to_half_bits<F16>(dv2[0])) | (uint32_t(to_half_bits<F16>(dv2[1])) << 16);
-                    }
-                    pb[half] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
-                    sb[half] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
-                }
-                // dV^T += dO^T P and dK^T += Q^T dS, 16 queries a step in the permuted order
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int r0 = 32 * qs + 16 * half + 4 * h + s16 / 4;
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) {
-                        const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
-                        uint4 ga = read_tr_pair(Gs + r0 * PQ + col, Gs + (r0 + 8) * PQ + col);
-                        uint4 qa = read_tr_pair(Qs + r0 * PQ + col, Qs + (r0 + 8) * PQ + col);
-                        adv[dt] = mfma32<F16>(ga, pb[half], adv[dt]);
-                        adk[dt] = mfma32<F16>(qa, sb[half], adk[dt]);
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    if (!kvalid) return;
-    uint16_t *dkp = p.dk + b * p.dk_b + nkv * p.dk_n + kj * p.dk_s;
-    uint16_t *dvp = p.dv + b * p.dv_b + nkv * p.dv_n + kj * p.dv_s;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-            const int d = 32 * dt + 8 * e4 + 4 * h;
-            uint32_t k0 = uint32_t(to_half_bits<F16>(adk[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 1])) << 16);
-            uint32_t k1 = uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(adk[dt][4 * e4 + 3])) << 16);
-            uint32_t v0 = uint32_t(to_half_bits<F16>(adv[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 1])) << 16);
-            uint32_t v1 = uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(adv[dt][4 * e4 + 3])) << 16);
-            *reinterpret_cast<uint2 *>(dkp + d) = make_uint2(k0, k1);
-            *reinterpret_cast<uint2 *>(dvp + d) = make_uint2(v0, v1);
-        }
-}
-
-// dQ for 128 queries (32 a wavefront), looping over 64-key tiles: S^T and dP^T one query a lane, dQ^T
-// accumulated in registers (deterministic: no atomics).
-template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256) void flash_dq_kernel_v1(AttnParams p) {
-    constexpr int BN = 64;
-    constexpr int PK = D + 16, PV = D + 8;
-    constexpr int DS = D / 16, DT = D / 32;
-    __shared__ __align__(16) uint16_t Ks[BN * PK];
-    __shared__ __align__(16) uint16_t Vs[BN * PV];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
-    const int g = lane >> 4, s16 = lane & 15;
-    const int64_t b = blockIdx.z, n = blockIdx.y;
-    const int64_t nkv = n / (p.heads / p.kv_heads);
-    const int64_t q0 = int64_t(blockIdx.x) * 128;
-    const int64_t qi = q0 + wave * 32 + l32;
-    const bool qvalid = qi < p.sq;
-    const int64_t shift = p.sk - p.sq;
-
-    const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
-    const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
-    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
-    const uint16_t *vp = p.v + b * p.v_b + nkv * p.v_n;
-    uint4 qf[DS], gf[DS];
-#pragma unroll
-    for (int t = 0; t < DS; ++t) {
-        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        gf[t] = qvalid ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-    }
-    const float lse = qvalid ? p.lse_in[(b * p.heads + n) * p.sq + qi] : 0.0f;
-    const float dl = qvalid ? p.delta[(b * p.heads + n) * p.sq + qi] : 0.0f;
-    f32x16_t acc[DT];
-#pragma unroll
-    for (int i = 0; i < DT; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
-    int64_t kend = p.sk;
-    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
-    const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int64_t k0 = int64_t(kt) * BN;
-        constexpr int CH = D / 8;
-        for (int idx = threadIdx.x; idx < BN * CH; idx += 256) {
-            int r = idx / CH, c = idx % CH;
-            int64_t key = k0 + r;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (key < p.sk) {
-                kv = *reinterpret_cast<const uint4 *>(kp + key * p.k_s + c * 8);
-                vv = *reinterpret_cast<const uint4 *>(vp + key * p.v_s + c * 8);
-            }
-            *reinterpret_cast<uint4 *>(Ks + r * PK + c * 8) = kv;
-            *reinterpret_cast<uint4 *>(Vs + r * PV + c * 8) = vv;
-        }
-        __syncthreads();
-        uint4 sb[4];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            f32x16_t sv, dp;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
-#pragma unroll
-            for (int t = 0; t < DS; ++t) {
-                uint4 a = *reinterpret_cast<const uint4 *>(Ks + (32 * ks + l32) * PK + 16 * t + 8 * h);
-                uint4 c = *reinterpret_cast<const uint4 *>(Vs + (32 * ks + l32) * PV + 16 * t + 8 * h);
-                sv = mfma32<F16>(a, qf[t], sv);
-                dp = mfma32<F16>(c, gf[t], dp);
-            }
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint32_t w[4];
-#pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    float ds2[2];
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const int e = 8 * half + j + u;
-                        const int64_t key = k0 + 32 * ks + 8 * (e / 4) + 4 * h + (e % 4);
-                        bool ok = qvalid && key < p.sk && (!CAUSAL || key <= qi + shift);
-                        float pe = ok ? __expf(sv[e] * p.scale - lse) : 0.0f;
-                        ds2[u] = pe * (dp[e] - dl) * p.scale;
-                    }
-                    w[j / 2] = uint32_t(to_half_bits<F16>(ds2[0])) | (uint32_t(to_half_bits<F16>(ds2[1])) << 16);
-                }
-                sb[2 * ks + half] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        }
-#pragma unroll
-        for (int t2 = 0; t2 < 4; ++t2) {
-            const int r0 = 16 * t2 + 4 * h + s16 / 4;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
-                uint4 a = read_tr_pair(Ks + r0 * PK + col, Ks + (r0 + 8) * PK + col);
-                acc[dt] = mfma32<F16>(a, sb[t2], acc[dt]);
-            }
-        }
-        __syncthreads();
-    }
-    if (!qvalid) return;
-    uint16_t *dqp = p.dq + b * p.dq_b + n * p.dq_n + qi * p.dq_s;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-            uint32_t w0 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4])) | (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 1])) << 16);
-            uint32_t w1 = uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 2])) | (uint32_t(to_half_bits<F16>(acc[dt][4 * e4 + 3])) << 16);
-            *reinterpret_cast<uint2 *>(dqp + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
-        }
-}
-
-// ---- backward, pipelined -----------------------------------------------------------------------------------
+// ---- backward -----------------------------------------------------------------------------------
 //
 // The FA-2 backward arranged like the pipelined forward: operand tiles stream HBM -> LDS with
 // global_load_lds into swizzled, double-buffered tiles; P = 2^(s * scale * log2 e - lse * log2 e) with the
@@ -717,8 +339,11 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
-    const int64_t b = blockIdx.z, nkv = blockIdx.y;
-    const int64_t kb0 = int64_t(blockIdx.x) * 128;
+    const int64_t nkb = (p.sk + 127) / 128;
+    int64_t unit, kblk;
+    xcd_order(int64_t(gridDim.x) / nkb, nkb, unit, kblk);  // causal: key block 0 has the most queries
+    const int64_t b = unit / p.kv_heads, nkv = unit % p.kv_heads;
+    const int64_t kb0 = kblk * 128;
     const int64_t kj = kb0 + wave * 32 + l32;
     const bool kvalid = kj < p.sk;
     const int64_t group = p.heads / p.kv_heads;
@@ -785,6 +410,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         const bool masked = q0 + BM > p.sq || (CAUSAL && q0 + shift < kb0 + 127);
 #pragma unroll
         for (int qs = 0; qs < 2; ++qs) {
+            if (CAUSAL && q0 + 32 * qs + 31 + shift < kb0 + 32 * wave) continue;  // all masked for this wave
             f32x16_t sv, dp;
 #pragma unroll
             for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
@@ -807,7 +433,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                     for (int u = 0; u < 2; ++u) {
                         const int e = 8 * half + jj + u;
                         const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
-                        float pe = exp2f(fmaf(sv[e], c2, -Lt[r]));
+                        float pe = fast_exp2(fmaf(sv[e], c2, -Lt[r]));
                         if (masked) {
                             const int64_t q = q0 + r;
                             const bool ok = q < p.sq && (!CAUSAL || kj <= q + shift);
@@ -867,13 +493,17 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
-    const int64_t b = blockIdx.z, n = blockIdx.y;
+    const int64_t nqb = (p.sq + 127) / 128;
+    int64_t unit, qblk;
+    xcd_order(int64_t(gridDim.x) / nqb, nqb, unit, qblk);
+    if (CAUSAL) qblk = nqb - 1 - qblk;
+    const int64_t b = unit / p.heads, n = unit % p.heads;
     const int64_t nkv = n / (p.heads / p.kv_heads);
-    const int64_t qblk = CAUSAL ? int64_t(gridDim.x - 1 - blockIdx.x) : int64_t(blockIdx.x);
     const int64_t q0 = qblk * 128;
     const int64_t qi = q0 + wave * 32 + l32;
     const bool qvalid = qi < p.sq;
     const int64_t shift = p.sk - p.sq;
+    const int64_t wq_last = q0 + wave * 32 + 31;
 
     const uint16_t *qp = p.q + b * p.q_b + n * p.q_n;
     const uint16_t *gp = p.d_o + b * p.do_b + n * p.do_n;
@@ -915,6 +545,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
             load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
             load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
         }
+        if (CAUSAL && k0 > wq_last + shift) continue;
         const char *Kb = reinterpret_cast<const char *>(smem + (kt & 1) * 2 * TILE);
         const char *Vb = Kb + TILE * 2;
         const bool masked = kt >= nfull;
@@ -942,7 +573,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const int e = 8 * half + jj + u;
-                        float pe = exp2f(fmaf(sv[e], c2, -l2));
+                        float pe = fast_exp2(fmaf(sv[e], c2, -l2));
                         if (masked) {
                             const int kk = 32 * ks + 8 * (e / 4) + (e % 4);
                             pe = (qvalid && kk <= lim) ? pe : 0.0f;
@@ -1009,17 +640,15 @@ inline int check_attn(const nhip_attn_desc *d, const char *what) {
         return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
-    if (d->batch > 65535 || d->heads > 65535) return fail(std::string(what) + ": batch and heads must be below 65536");
+    if ((d->sq + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31) || (d->sk + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31))
+        return fail(std::string(what) + ": more than 2^31 workgroups");
     return 0;
 }
 
 template <int D, bool F16, bool CAUSAL>
 int launch_fwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
-    dim3 grid(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
-    if (d->config == 1)
-        hipLaunchKernelGGL((nhipk::flash_fwd_kernel_v1<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
-    else
-        hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
+    dim3 grid(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
+    hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
     return check(hipGetLastError(), "flash_fwd launch");
 }
 
@@ -1049,16 +678,8 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
 template <int D, bool F16, bool CAUSAL>
 int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
     dim3 gd(unsigned((d->heads * d->sq + 3) / 4), unsigned(d->batch));
-    dim3 gk(unsigned((d->sk + 127) / 128), unsigned(d->kv_heads), unsigned(d->batch));
-    dim3 gq(unsigned((d->sq + 127) / 128), unsigned(d->heads), unsigned(d->batch));
-    if (d->config == 1) {
-        hipLaunchKernelGGL((nhipk::flash_delta_kernel_t<D, F16>), gd, dim3(256), 0, s, p);
-        if (check(hipGetLastError(), "flash delta launch")) return 1;
-        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel_v1<D, F16, CAUSAL>), gk, dim3(256), 0, s, p);
-        if (check(hipGetLastError(), "flash dkdv launch")) return 1;
-        hipLaunchKernelGGL((nhipk::flash_dq_kernel_v1<D, F16, CAUSAL>), gq, dim3(256), 0, s, p);
-        return check(hipGetLastError(), "flash dq launch");
-    }
+    dim3 gk(unsigned((d->sk + 127) / 128 * d->kv_heads * d->batch));
+    dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
     float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
     hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
     if (check(hipGetLastError(), "flash delta launch")) return 1;
