@@ -230,6 +230,8 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
     for st in steps:
         if st.kind in ("loop", "row"):
             _pull_index_math(graph, st, prod, done_inputs=set(graph.inputs))
+    if fuse_loops:
+        steps = _rematerialize(graph, steps, prod)
     done, ordered = set(graph.inputs), []
     pending = steps[:]
     while pending:
@@ -243,6 +245,90 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
         if not progressed:
             raise RuntimeError("fusion produced a cycle: " + ", ".join(s.label() for s in pending))
     return ordered
+
+
+REMAT = ELEMENTWISE | INDEX_ONLY | VIEWABLE
+REMAT_BUDGET = 32  # nodes a kernel may recompute in place of one value it reads
+
+
+def _inputs_of(nodes):
+    produced = {m.output for m in nodes}
+    ins = []
+    for m in nodes:
+        for u in m.inputs:
+            if u not in produced and u not in ins:
+                ins.append(u)
+    return ins
+
+
+def _rematerialize(graph, steps, prod):
+    """Recomputes values instead of storing them (``passes/fusion/mod.rs`` duplicates cheap producers the
+    same way). A loop or row kernel that reads a value computed elementwise from values already in memory
+    computes it itself, when that adds at most one new operand read: the training graph's backward kernels
+    then recompute an activation's intermediates (GELU's tanh argument and friends) from its input instead
+    of reading them back, and the forward kernels stop writing them."""
+    in_memory = set(graph.inputs)
+    for st in steps:
+        in_memory.update(st.outputs)
+    for st in steps:
+        if st.kind not in ("loop", "row"):
+            continue
+        changed = True
+        while changed:
+            changed = False
+            for u in list(st.inputs):
+                n = prod.get(u)
+                if n is None or n.prim not in REMAT:
+                    continue
+                expr, leaves, stack = {}, set(), [u]
+                ok = True
+                while stack and ok:
+                    v = stack.pop()
+                    if v in expr:
+                        continue
+                    m = prod.get(v)
+                    if m is None or m.prim not in REMAT:
+                        if v not in in_memory:
+                            ok = False
+                        leaves.add(v)
+                        continue
+                    expr[v] = m
+                    if len(expr) > REMAT_BUDGET:
+                        ok = False
+                    stack.extend(m.inputs)
+                if not ok:
+                    continue
+                new = [v for v in leaves if v not in st.inputs]
+                if len(new) > 1:
+                    continue
+                have = {m.output for m in st.nodes}
+                st.nodes.extend(m for v, m in expr.items() if v not in have)
+                st.nodes.sort(key=lambda m: m.output)
+                st.inputs = _inputs_of(st.nodes)
+                changed = True
+                break
+    # values nobody reads any more: a kernel stops writing its extra outputs and computing what fed only them
+    read = set(graph.outputs)
+    for st in steps:
+        read.update(st.inputs)
+    kept = []
+    for st in steps:
+        if st.kind in ("loop", "row") and len(st.outputs) > 1:
+            outs = [st.outputs[0]] + [v for v in st.outputs[1:] if v in read]
+            if len(outs) < len(st.outputs):
+                st.outputs = outs
+                by_out = {m.output: m for m in st.nodes}
+                live, stack = set(), list(outs)
+                while stack:
+                    v = stack.pop()
+                    if v in live or v not in by_out:
+                        continue
+                    live.add(v)
+                    stack.extend(by_out[v].inputs)
+                st.nodes = [m for m in st.nodes if m.output in live]
+                st.inputs = _inputs_of(st.nodes)
+        kept.append(st)
+    return kept
 
 
 def _index_only(v, prod, done):
