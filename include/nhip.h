@@ -112,13 +112,20 @@ typedef struct {
     int64_t b_k, b_n;             /* element strides of B along k and n */
     int64_t d_m, d_n;             /* element strides of D along m and n */
     int32_t config;               /* tile config index; -1 picks the default for the shape */
-    int32_t reserved;
+    int32_t splits;               /* split-k factor for nhip_gemm_splitk (0 or 1: none) */
 } nhip_gemm_desc;
 
 /* Queues D = A.B on the stream. A and B must be float dtypes of one kind (bf16/f16 together, or f32). */
 int nhip_gemm(const nhip_gemm_desc *desc, const void *a, const void *b, void *d);
 /* Number of tile configs nhip_gemm accepts in desc->config for bf16/f16 (autotuning, autotune/mod.rs). */
 int nhip_gemm_config_count(int *count);
+/* Split-k: D = A.B with k cut into desc->splits equal parts computed by separate workgroups (for shapes with
+ * too few output tiles to fill the GPU, such as weight gradients), their float32 partial products summed in
+ * split order by a second kernel. Needs 16-bit operands in the MFMA layouts, k a multiple of 64 * splits,
+ * and `workspace` of nhip_gemm_workspace bytes (the scratch of a plan step,
+ * lumen/plan/step/mod.rs:65-66). */
+int nhip_gemm_splitk(const nhip_gemm_desc *desc, const void *a, const void *b, void *d, void *workspace);
+int nhip_gemm_workspace(const nhip_gemm_desc *desc, size_t *bytes);
 
 /* ---- flash attention (lumen/codegen/attention/cuda/mod.rs:33-59 Forward/Operand; Triton algorithm
  * lumen/codegen/attention/triton/kernel.py:34-256) ------------------------------------------------------ *
@@ -175,7 +182,7 @@ typedef struct {
 } nhip_reloc;
 
 enum {
-    NHIP_STEP_GEMM = 1,       /* desc: nhip_gemm_desc; pointers: a, b, d */
+    NHIP_STEP_GEMM = 1,       /* desc: nhip_gemm_desc; pointers: a, b, d (and the workspace when splits > 1) */
     NHIP_STEP_FLASH_FWD = 2,  /* desc: nhip_attn_desc; pointers: q, k, v, o, lse */
     NHIP_STEP_FLASH_BWD = 3,  /* desc: nhip_attn_desc; pointers: q, k, v, o, do, lse, dq, dk, dv, ws */
     NHIP_STEP_COPY = 4,       /* desc: uint64 bytes; pointers: dst, src */

@@ -43,6 +43,20 @@ class Loc:
         return codegen.View(self.dtype, self.shape, self.offset, self.strides)
 
 
+def _mfma_layout(d) -> bool:
+    """Whether the MFMA kernels read a dot's operands (each k- or mn-contiguous with 16-byte aligned lines):
+    the host-side twin of kernels.hip's mfma_ready, without the pointer alignment."""
+    if d.a_k == 1 and d.k % 8 == 0 and (d.a_m % 8 == 0 or d.m == 1):
+        pass
+    elif not (d.a_m == 1 and d.m % 8 == 0 and d.a_k % 8 == 0):
+        return False
+    if d.b_k == 1 and d.k % 8 == 0 and (d.b_n % 8 == 0 or d.n == 1):
+        pass
+    elif not (d.b_n == 1 and d.n % 8 == 0 and d.b_k % 8 == 0):
+        return False
+    return all(d.a_batch[i] % 8 == 0 and d.b_batch[i] % 8 == 0 for i in range(d.nbatch))
+
+
 def _contig(shape):
     return codegen._contig(shape)
 
@@ -205,6 +219,11 @@ class Plan:
                 off, size = take(t.nbytes())
                 live[v] = (off, size)
                 self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
+            if st.kind == "dot":
+                st.splits = self._split_count(st.nodes[0])
+                if st.splits > 1:
+                    d, _ = self._gemm_desc(st.nodes[0])
+                    st.scratch = st.splits * max(1, math.prod(d.batch[i] for i in range(d.nbatch))) * d.m * d.n * 4
             if st.scratch:
                 off, size = take(st.scratch)
                 self.scratch[id(st)] = Loc(("ws", 0), off // 4, (1,), "float32", (st.scratch // 4,))
@@ -333,8 +352,11 @@ class Plan:
                 call("nhip_plan_add_launch", plan, fn, grid, block, k.lds, args, len(args), rr, len(relocs))
             elif st.kind == "dot":
                 desc, ops = self._gemm_desc(st.nodes[0])
-                rr = (nv.Reloc * 3)(*[reloc(i, l) for i, l in enumerate(ops)])
-                call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_GEMM, C.byref(desc), C.sizeof(desc), rr, 3)
+                if getattr(st, "splits", 1) > 1:
+                    desc.splits = st.splits
+                    ops = ops + [self.scratch[id(st)]]
+                rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
+                call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_GEMM, C.byref(desc), C.sizeof(desc), rr, len(ops))
             elif st.kind in ("flash_fwd", "flash_bwd"):
                 kind, desc, ops = attn_pass.lower(self, st)
                 rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
@@ -407,6 +429,28 @@ class Plan:
         d.a_m, d.a_k, d.b_k, d.b_n, d.d_m, d.d_n = a_m, a_k, b_k, b_n, d_m, d_n
         d.config = -1
         return d, [lhs, rhs, out]
+
+    # Split-k policy: a bf16/f16 dot whose 256 x 256 output tiles cannot fill the 256 CUs is cut along k (in
+    # powers of two, each part at least 1024 deep) until they do; its float32 partials live in the step's
+    # scratch (nhip_gemm_splitk).
+    SPLIT_MIN_K = 1024
+
+    def _split_count(self, n):
+        lhs, rhs, out = self.loc[n.inputs[0]], self.loc[n.inputs[1]], self.loc[n.output]
+        if lhs.dtype not in ("bfloat16", "float16") or rhs.dtype != lhs.dtype:
+            return 1
+        try:
+            d, _ = self._gemm_desc(n)
+        except NotImplementedError:
+            return 1
+        if not _mfma_layout(d) or any((loc.offset * D.size_of(loc.dtype)) % 16 for loc in (lhs, rhs)):
+            return 1
+        z = max(1, math.prod(d.batch[i] for i in range(d.nbatch)))
+        tiles = -(-d.m // 256) * -(-d.n // 256) * z
+        s = 1
+        while tiles * s * 2 <= 256 and d.k % (64 * s * 2) == 0 and d.k // (s * 2) >= self.SPLIT_MIN_K:
+            s *= 2
+        return s
 
     def run_in(self, workspace_ptr: int, input_ptrs: list):
         """Queues the plan on the stream: inputs are device pointers in graph-input order."""

@@ -12,6 +12,8 @@
 // elementwise work after a dot into its stores.
 #pragma once
 
+#include <type_traits>
+
 #include "device_common.h"
 
 namespace nhipk {
@@ -23,6 +25,7 @@ struct GemmShape {
     int64_t a_batch[3], b_batch[3], d_batch[3];
     int64_t a_m, a_k, b_k, b_n, d_m, d_n;
     int32_t tiles_m, tiles_n;
+    int64_t d_split;  // split-k: element offset of split blockIdx.z's partial product in D (k is one split's)
 };
 
 // Element offsets of batch `z` in A, B and D.
@@ -312,5 +315,271 @@ constexpr int gemm_mfma_lds_bytes() {
     return 2 * (TileLayout<BM, BK, AT>::elems + TileLayout<BN, BK, BT>::elems) * 2;
 }
 
+// ---- MFMA, operands streamed HBM -> LDS (256 x 256 tiles) ------------------------------------------------
+//
+// gemm_stream: 2 x WN wavefronts, each a 128 x (256 / WN) block of D as 4 x FN MFMA 32x32x16 tiles (WN = 2:
+// 4 waves of 128 x 128, one a SIMD, 0.5 KiB of LDS reads per MFMA; WN = 4: 8 waves of 128 x 64). Operand
+// tiles go straight from HBM into LDS with global_load_lds_dwordx4 (no VGPR staging), STAGES deep, so loads of
+// later k tiles run under the MFMAs of the current one. A wave's 16-byte LDS writes are contiguous (lane i
+// at byte 16 i of a 1 KiB segment): lines are unpadded and the 16-byte chunks of each line are XOR-swizzled
+// so that the fragment reads (16 rows at one chunk for a k-contiguous tile; 4 k-lines of 64 bytes for an
+// mn-contiguous one read with ds_read_tr16_b64) fall on distinct banks. Fragments of k step kk + 16 are
+// read while the MFMAs of step kk run (their issue order pinned with sched_group_barrier).
+// The MFMA computes D^T blocks (B fragment as the A operand), so each lane ends with 4 consecutive columns
+// of one row; the epilogue stages the tile through LDS and writes rows with 16-byte stores.
+// Requires k % BK == 0 (a clamped k tail would add products of repeated columns).
+
+template <int BK>
+__device__ __forceinline__ int kmaj_swz(int r) {
+    if constexpr (BK == 64) return ((r >> 1) & 7) ^ ((r & 1) << 2);
+    else return (r >> 2) & 3;
+}
+__device__ __forceinline__ int mnmaj_swz(int k) { return (k & 3) << 2; }
+
+typedef __attribute__((address_space(3))) void glds_void_t;
+
+template <int BK, bool T>
+struct StreamTile {
+    static constexpr int line_bytes = T ? 256 * 2 : BK * 2;  // a k-line of 256 mn, or a row of BK k
+    static constexpr int chunks = line_bytes / 16;
+    static constexpr int lines_per_seg = 1024 / line_bytes;
+    static constexpr int bytes = 256 * BK * 2;
+    static constexpr int segs = bytes / 1024;
+};
+
+template <int BK>
+constexpr int gemm_stream_stages() { return (128 * 1024) / (2 * 256 * BK * 2); }
+// Epilogue staging: a wave's 64 rows at a time, 16 bytes of padding a row.
+template <int WN>
+constexpr int gemm_stream_stage_pitch() { return (256 / WN) * 4 + 16; }
+// LDS: the operand stages, or the epilogue's staging (float32 rows), whichever is larger.
+template <int BK, int WN>
+constexpr int gemm_stream_lds_bytes() {
+    return 128 * 1024 > 2 * WN * 64 * gemm_stream_stage_pitch<WN>() ? 128 * 1024 : 2 * WN * 64 * gemm_stream_stage_pitch<WN>();
+}
+
+// Scheduling constraint for one k step: M MFMAs with NR LDS reads spread evenly between them.
+template <int T, int M, int NR, int ID>
+__device__ __forceinline__ void mfma_ds_interleave() {
+    if constexpr (T < M) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, ID);
+        constexpr int r = NR * (T + 1) / M - NR * T / M;
+        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, ID);
+        mfma_ds_interleave<T + 1, M, NR, ID>();
+    }
+}
+
+template <bool F16, int BK, int WN, bool AT, bool BT>
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
+    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
+    constexpr int NW = 2 * WN;       // wavefronts
+    constexpr int FN = 8 / WN;       // 32-column MFMA tiles a wave
+    constexpr int WCOLS = 32 * FN;   // columns a wave
+    constexpr int STAGES = gemm_stream_stages<BK>();
+    using TA = StreamTile<BK, AT>;
+    using TB = StreamTile<BK, BT>;
+    constexpr int STAGE_BYTES = TA::bytes + TB::bytes;
+    constexpr int LPS = (TA::segs + TB::segs) / NW;  // load instructions a wave issues per stage
+    constexpr int NRD = (AT ? 8 : 4) + (BT ? 2 * FN : FN);  // LDS read instructions a k step
+    extern __shared__ __align__(1024) char smem[];
+
+    int tm, tn;
+    tile_of(blockIdx.x, s.tiles_m, s.tiles_n, tm, tn);
+    int64_t oa, ob, od;
+    batch_offsets(s, blockIdx.y, oa, ob, od);
+    const int64_t m0 = int64_t(tm) * 256, n0 = int64_t(tn) * 256;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int h = lane >> 5, l32 = lane & 31, g = lane >> 4, s16 = lane & 15;
+    const int64_t ks = int64_t(blockIdx.z) * s.k;  // split-k: this workgroup's first k
+    od += int64_t(blockIdx.z) * s.d_split;
+    const uint16_t *pa = a + oa + ks * s.a_k, *pb = b + ob + ks * s.b_k;
+    const int ktiles = int(s.k / BK);
+
+    auto issue = [&](int st, int kt) {
+        char *base = smem + st * STAGE_BYTES;
+        const int64_t k0 = int64_t(kt) * BK;
+#pragma unroll
+        for (int i = 0; i < TA::segs / NW; ++i) {
+            const int seg = wave + NW * i;
+            const int line = seg * TA::lines_per_seg + lane / TA::chunks, c = lane % TA::chunks;
+            const uint16_t *src;
+            if (AT) {
+                int64_t mm = m0 + ((c ^ mnmaj_swz(line)) << 3);
+                mm = mm < s.m ? mm : s.m - 8;
+                src = pa + (k0 + line) * s.a_k + mm;
+            } else {
+                int64_t mm = m0 + line;
+                mm = mm < s.m ? mm : s.m - 1;
+                src = pa + mm * s.a_m + k0 + ((c ^ kmaj_swz<BK>(line)) << 3);
+            }
+            __builtin_amdgcn_global_load_lds(src, (glds_void_t *)(base + seg * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < TB::segs / NW; ++i) {
+            const int seg = wave + NW * i;
+            const int line = seg * TB::lines_per_seg + lane / TB::chunks, c = lane % TB::chunks;
+            const uint16_t *src;
+            if (BT) {
+                int64_t nn = n0 + ((c ^ mnmaj_swz(line)) << 3);
+                nn = nn < s.n ? nn : s.n - 8;
+                src = pb + (k0 + line) * s.b_k + nn;
+            } else {
+                int64_t nn = n0 + line;
+                nn = nn < s.n ? nn : s.n - 1;
+                src = pb + nn * s.b_n + k0 + ((c ^ kmaj_swz<BK>(line)) << 3);
+            }
+            __builtin_amdgcn_global_load_lds(src, (glds_void_t *)(base + TA::bytes + seg * 1024), 16, 0, 0);
+        }
+    };
+    // fragment: 8 consecutive k (from kk + 8 h) at row `r0 + l32` of the tile
+    auto frag = [&](const char *tile, int r0, int kk, auto tr) -> uint4 {
+        if constexpr (decltype(tr)::value) {
+            const int kl = kk + 8 * h + s16 / 4;
+            const int mn = r0 + 16 * (g & 1) + 4 * (s16 & 3);
+            const char *p0 = tile + kl * 512 + (((mn >> 3) ^ mnmaj_swz(kl)) << 4) + ((mn & 7) << 1);
+            const char *p1 = tile + (kl + 4) * 512 + (((mn >> 3) ^ mnmaj_swz(kl + 4)) << 4) + ((mn & 7) << 1);
+            gv4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p0));
+            gv4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p1));
+            uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+            return make_uint4(xa.x, xa.y, ya.x, ya.y);
+        } else {
+            const int r = r0 + l32;
+            return *reinterpret_cast<const uint4 *>(tile + r * (BK * 2) + ((((kk >> 3) + h) ^ kmaj_swz<BK>(r)) << 4));
+        }
+    };
+
+    f32x16_t acc[4][FN];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < ktiles) issue(st, st);
+    for (int kt = 0; kt < ktiles; ++kt) {
+        // wait for this thread's loads of tile kt: later tiles' loads may stay in flight
+        const int later = min(STAGES - 2, ktiles - 1 - kt);
+        if (STAGES <= 2 || later <= 0) __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);
+        else if (later == 1) __builtin_amdgcn_s_waitcnt((LPS & 15) | ((LPS >> 4) << 14) | 0x0070 | 0x0f00);
+        else __builtin_amdgcn_s_waitcnt(((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | 0x0070 | 0x0f00);
+        __syncthreads();  // every thread's loads of tile kt landed; the stage of tile kt - 1 is free
+        if (kt + STAGES - 1 < ktiles) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+        const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+        const char *tb = ta + TA::bytes;
+        uint4 fa[2][4], fb[2][FN];
+        auto read = [&](int buf, int kk) {  // in the order the MFMAs (i-major) first use them
+            fa[buf][0] = frag(ta, wm * 128, kk, std::integral_constant<bool, AT>{});
+#pragma unroll
+            for (int j = 0; j < FN; ++j) fb[buf][j] = frag(tb, wn * WCOLS + 32 * j, kk, std::integral_constant<bool, BT>{});
+#pragma unroll
+            for (int i = 1; i < 4; ++i) fa[buf][i] = frag(ta, wm * 128 + 32 * i, kk, std::integral_constant<bool, AT>{});
+        };
+        read(0, 0);
+        auto step = [&](auto kkc) {
+            constexpr int kk = decltype(kkc)::value;
+            constexpr int cur = (kk / 16) & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kk + 16 < BK) read(cur ^ 1, kk + 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<F16>::run(fb[cur][j], fa[cur][i], acc[i][j]);
+            if constexpr (kk + 16 < BK) mfma_ds_interleave<0, 4 * FN, NRD, kk / 16 + 1>();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        step(std::integral_constant<int, 0>{});
+        step(std::integral_constant<int, 16>{});
+        if constexpr (BK > 32) {
+            step(std::integral_constant<int, 32>{});
+            step(std::integral_constant<int, 48>{});
+        }
+    }
+
+    // acc[i][j][e]: row m0 + wm*128 + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
+    // Staged through LDS as float32, 64 rows of the wave at a time, then written row-wise: 16-byte stores
+    // when D is row-contiguous and aligned, else element by element through the strided store.
+    const int64_t rbase = m0 + wm * 128, cbase = n0 + wn * WCOLS;
+    const int esize = out.dtype == 0 ? 4 : 2;
+    const bool vec = s.d_n == 1 && s.n % 8 == 0 && s.d_m % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(out.d) + od * esize) & 15) == 0;
+    constexpr int PITCH = gemm_stream_stage_pitch<WN>();
+    __syncthreads();  // operand stages are dead: reuse LDS for the output
+    char *stage = smem + wave * (64 * PITCH);
+    char *dbase = static_cast<char *>(out.d) + od * esize;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int i = 2 * half + ii;
+            const int r = 32 * ii + l32;
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4)
+                    *reinterpret_cast<float4 *>(stage + r * PITCH + (32 * j + 8 * e4 + 4 * h) * 4) =
+                        make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
+        }
+        __syncthreads();
+        if (vec) {
+            const int epc = 16 / esize;            // output elements a 16-byte chunk
+            const int cpr = WCOLS / epc;           // chunks a row
+            for (int idx = lane; idx < 64 * cpr; idx += 64) {
+                const int r = idx / cpr, ch = idx % cpr;
+                const int64_t gr = rbase + 64 * half + r, gc = cbase + ch * epc;
+                if (gr >= s.m || gc >= s.n) continue;
+                const float *src = reinterpret_cast<const float *>(stage + r * PITCH) + ch * epc;
+                uint4 v;
+                if (out.dtype == 0) {
+                    v = *reinterpret_cast<const uint4 *>(src);
+                } else {
+                    const float4 x = *reinterpret_cast<const float4 *>(src);
+                    const float4 y = *reinterpret_cast<const float4 *>(src + 4);
+                    if (out.dtype == 1)
+                        v = make_uint4(uint32_t(f32_to_bf16(x.x)) | (uint32_t(f32_to_bf16(x.y)) << 16),
+                                       uint32_t(f32_to_bf16(x.z)) | (uint32_t(f32_to_bf16(x.w)) << 16),
+                                       uint32_t(f32_to_bf16(y.x)) | (uint32_t(f32_to_bf16(y.y)) << 16),
+                                       uint32_t(f32_to_bf16(y.z)) | (uint32_t(f32_to_bf16(y.w)) << 16));
+                    else
+                        v = make_uint4(uint32_t(f32_to_f16(x.x)) | (uint32_t(f32_to_f16(x.y)) << 16),
+                                       uint32_t(f32_to_f16(x.z)) | (uint32_t(f32_to_f16(x.w)) << 16),
+                                       uint32_t(f32_to_f16(y.x)) | (uint32_t(f32_to_f16(y.y)) << 16),
+                                       uint32_t(f32_to_f16(y.z)) | (uint32_t(f32_to_f16(y.w)) << 16));
+                }
+                *reinterpret_cast<uint4 *>(dbase + (gr * s.d_m + gc) * esize) = v;
+            }
+        } else {
+            out.visit([&](auto stf) {
+                for (int idx = lane; idx < 64 * WCOLS; idx += 64) {
+                    const int r = idx / WCOLS, c = idx % WCOLS;
+                    const int64_t gr = rbase + 64 * half + r, gc = cbase + c;
+                    if (gr < s.m && gc < s.n)
+                        stf(s, od, gr, gc, *reinterpret_cast<const float *>(stage + r * PITCH + c * 4));
+                }
+            });
+        }
+        __syncthreads();
+    }
+}
+
+// Split-k reduction: D[z, r, c] = sum over splits of the float32 partials P[split][z][r][c] (contiguous,
+// `mn` = m * n elements a batch), in split order, rounded once to D's dtype.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmShape s, const float *__restrict__ part, int splits,
+                                                           int64_t total, AnyStore out) {
+    const int64_t mn = s.m * s.n;
+    out.visit([&](auto stf) {
+        for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+            float acc = part[i];
+            for (int sp = 1; sp < splits; ++sp) acc += part[int64_t(sp) * total + i];
+            const int64_t z = i / mn, rc = i % mn;
+            int64_t oa, ob, od;
+            batch_offsets(s, z, oa, ob, od);
+            stf(s, od, rc / s.n, rc % s.n, acc);
+        }
+    });
+}
 
 }  // namespace nhipk

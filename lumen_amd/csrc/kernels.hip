@@ -24,7 +24,11 @@ constexpr TileConfig kConfigs[] = {
     {128, 64, 64, 2, 2},
     {64, 64, 64, 2, 2},
 };
-constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
+// Configs past the tiled ones: gemm_stream (256 x 256, operands streamed into LDS): k tile 64 with 4 waves of
+// 128 x 128 (2 stages) and with 8 waves of 128 x 64 (2 stages); k tile 32 with 8 waves (4 stages).
+constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2;
+constexpr int kNumConfigs = kNumTiled + 3;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -54,14 +58,16 @@ int64_t batch_count(const nhip_gemm_desc *d) {
     return z;
 }
 
-// The default tile for a shape: the largest whose tile count fills the 256 CUs at least once.
+// The default tile for a shape: the streamed 256 x 256 kernel when k allows it and its tiles fill the 256 CUs,
+// else the largest tiled config whose tile count fills them at least once.
 int default_config(const nhip_gemm_desc *d) {
     int64_t z = batch_count(d);
-    for (int c = 0; c < kNumConfigs; ++c) {
+    if (d->k % 64 == 0 && ((d->m + 255) / 256) * ((d->n + 255) / 256) * z >= 256) return kStream8w;
+    for (int c = 0; c < kNumTiled; ++c) {
         int64_t tiles = ((d->m + kConfigs[c].bm - 1) / kConfigs[c].bm) * ((d->n + kConfigs[c].bn - 1) / kConfigs[c].bn) * z;
         if (tiles >= 256) return c;
     }
-    return kNumConfigs - 1;
+    return kNumTiled - 1;
 }
 
 template <typename TD>
@@ -101,9 +107,32 @@ int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const
     return check(hipGetLastError(), "gemm_mfma launch");
 }
 
+template <bool F16, int BK, int WN, bool AT, bool BT>
+int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
+                  int splits = 1) {
+    s.tiles_m = int((s.m + 255) / 256);
+    s.tiles_n = int((s.n + 255) / 256);
+    constexpr int lds = gemm_stream_lds_bytes<BK, WN>();
+    auto kern = gemm_stream<F16, BK, WN, AT, BT>;
+    static bool attr = false;
+    if (!attr) {
+        if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                  "hipFuncSetAttribute"))
+            return 1;
+        attr = true;
+    }
+    dim3 grid(s.tiles_m * s.tiles_n, unsigned(z), unsigned(splits));
+    hipLaunchKernelGGL(kern, grid, dim3(128 * WN), lds, st, s, static_cast<const uint16_t *>(a),
+                       static_cast<const uint16_t *>(b), AnyStore{out, dtype});
+    return check(hipGetLastError(), "gemm_stream launch");
+}
+
 template <bool F16, bool AT, bool BT>
 int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype) {
     switch (cfg) {
+        case kStream4w: return launch_stream<F16, 64, 2, AT, BT>(st, s, z, a, b, out, dtype);
+        case kStream8w: return launch_stream<F16, 64, 4, AT, BT>(st, s, z, a, b, out, dtype);
+        case kStream8w32: return launch_stream<F16, 32, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
         case 2: return launch_mfma_cfg<F16, 128, 256, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
@@ -142,6 +171,54 @@ bool mfma_ready(const nhip_gemm_desc *d, const void *a, const void *b, bool &at,
 
 }  // namespace
 
+size_t splitk_workspace_bytes(const nhip_gemm_desc *d) {
+    return d->splits > 1 ? size_t(d->splits) * size_t(batch_count(d)) * size_t(d->m) * size_t(d->n) * sizeof(float) : 0;
+}
+
+// Split-k through the streamed 8-wave kernel: partials into the workspace as [split][batch][m][n] float32, then
+// the ordered sum into D.
+int gemm_splitk_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *b, void *out, void *ws) {
+    if (d->splits <= 1) return gemm_on(st, d, a, b, out);
+    if (d->nbatch < 0 || d->nbatch > 3) return fail("nhip_gemm_splitk: at most 3 batch axes");
+    int64_t z = batch_count(d);
+    if (d->m == 0 || d->n == 0 || z == 0) return 0;
+    if (z > 65535 || d->splits > 64) return fail("nhip_gemm_splitk: more than 65535 batches or 64 splits");
+    bool at = false, bt = false;
+    if (!mfma_ready(d, a, b, at, bt) || d->k % (64 * int64_t(d->splits)))
+        return fail("nhip_gemm_splitk: needs 16-bit operands in an MFMA layout and k a multiple of 64 * splits");
+    if (!ws) return fail("nhip_gemm_splitk: no workspace");
+    // partial products: contiguous [split][batch...][m][n]
+    GemmShape p = shape_of(d);
+    p.k = d->k / d->splits;
+    p.d_m = d->n;
+    p.d_n = 1;
+    int64_t stride = d->m * d->n;
+    for (int i = d->nbatch - 1; i >= 0; --i) {
+        p.d_batch[i] = stride;
+        stride *= d->batch[i];
+    }
+    p.d_split = stride;
+    int rc;
+    bool f16 = d->a_dtype == NHIP_F16;
+#define NHIP_SPLIT(FF, AA, BB) rc = launch_stream<FF, 64, 4, AA, BB>(st, p, z, a, b, ws, NHIP_F32, d->splits)
+    if (f16) {
+        if (at) { if (bt) NHIP_SPLIT(true, true, true); else NHIP_SPLIT(true, true, false); }
+        else { if (bt) NHIP_SPLIT(true, false, true); else NHIP_SPLIT(true, false, false); }
+    } else {
+        if (at) { if (bt) NHIP_SPLIT(false, true, true); else NHIP_SPLIT(false, true, false); }
+        else { if (bt) NHIP_SPLIT(false, false, true); else NHIP_SPLIT(false, false, false); }
+    }
+#undef NHIP_SPLIT
+    if (rc) return rc;
+    GemmShape s = shape_of(d);
+    const int64_t total = z * d->m * d->n;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(unsigned(blocks)), dim3(256), 0, st, s, static_cast<const float *>(ws),
+                       d->splits, total, AnyStore{out, d->d_dtype});
+    return check(hipGetLastError(), "gemm split-k reduce launch");
+}
+
 int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *b, void *out) {
     if (d->nbatch < 0 || d->nbatch > 3) return fail("nhip_gemm: at most 3 batch axes");
     if ((d->a_dtype == NHIP_F32) != (d->b_dtype == NHIP_F32))
@@ -154,6 +231,8 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
+        if (((cfg == kStream4w || cfg == kStream8w) && d->k % 64) || (cfg == kStream8w32 && d->k % 32))
+            return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
         return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
     }
@@ -200,6 +279,17 @@ int nhip_gemm(const nhip_gemm_desc *desc, const void *a, const void *b, void *d)
 
 int nhip_gemm_config_count(int *count) {
     *count = kNumConfigs;
+    return 0;
+}
+
+int nhip_gemm_splitk(const nhip_gemm_desc *desc, const void *a, const void *b, void *d, void *workspace) {
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    return gemm_splitk_on(s, desc, a, b, d, workspace);
+}
+
+int nhip_gemm_workspace(const nhip_gemm_desc *desc, size_t *bytes) {
+    *bytes = splitk_workspace_bytes(desc);
     return 0;
 }
 

@@ -18,6 +18,7 @@ hipStream_t stream_of_current();
 
 // Built-in kernels queued on stream `s` (kernels.hip).
 int gemm_on(hipStream_t s, const nhip_gemm_desc *d, const void *a, const void *b, void *out);
+int gemm_splitk_on(hipStream_t s, const nhip_gemm_desc *d, const void *a, const void *b, void *out, void *ws);
 int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v, void *o,
                  float *lse);
 int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v,

@@ -522,7 +522,8 @@ int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninp
         int rc = 0;
         switch (st.kind) {
             case NHIP_STEP_GEMM:
-                rc = gemm_on(s, reinterpret_cast<const nhip_gemm_desc *>(st.args.data()), ptrs[0], ptrs[1], ptrs[2]);
+                rc = gemm_splitk_on(s, reinterpret_cast<const nhip_gemm_desc *>(st.args.data()), ptrs[0], ptrs[1],
+                                    ptrs[2], ptrs[3]);
                 break;
             case NHIP_STEP_FLASH_FWD:
                 rc = flash_fwd_on(s, reinterpret_cast<const nhip_attn_desc *>(st.args.data()), ptrs[0], ptrs[1],

@@ -54,7 +54,7 @@ class GemmDesc(C.Structure):
         ("d_m", C.c_int64),
         ("d_n", C.c_int64),
         ("config", C.c_int32),
-        ("reserved", C.c_int32),
+        ("splits", C.c_int32),
     ]
 
 
@@ -110,6 +110,8 @@ SIGNATURES = {
     ),
     "nhip_gemm": ([C.POINTER(GemmDesc), C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "nhip_gemm_config_count": ([C.POINTER(C.c_int)], C.c_int),
+    "nhip_gemm_splitk": ([C.POINTER(GemmDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "nhip_gemm_workspace": ([C.POINTER(GemmDesc), C.POINTER(C.c_size_t)], C.c_int),
     "nhip_flash_fwd": ([C.POINTER(AttnDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "nhip_flash_bwd": (
         [C.POINTER(AttnDesc)] + [C.c_void_p] * 10,

@@ -26,7 +26,10 @@ def _desc(m, n, k, a_m, a_k, b_k, b_n, dt=nv.NHIP_BF16, out=nv.NHIP_F32, cfg=-1,
 
 
 @pytest.mark.parametrize("at,bt", [(False, False), (False, True), (True, False), (True, True)])
-@pytest.mark.parametrize("m,n,k,cfg", [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0)])
+@pytest.mark.parametrize(
+    "m,n,k,cfg",
+    [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0), (520, 264, 192, 6), (264, 776, 128, 7), (264, 136, 96, 8)],
+)
 def test_gemm_layouts(hip, at, bt, m, n, k, cfg):
     """A as [m][k] or [k][m] in memory, B as [n][k] or [k][n]: float32 results within float32 rounding of
     the float64 product of the bf16 operands."""
@@ -54,6 +57,59 @@ def test_gemm_batched_bf16_output(hip):
     nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
     got = D.bf16_to_f32(dd.get((z, m, n), np.uint16))
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("cfg,out", [(6, nv.NHIP_BF16), (7, nv.NHIP_F16), (7, nv.NHIP_F32), (8, nv.NHIP_BF16)])
+def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
+    """The streamed 256 x 256 kernel's LDS-staged row stores: 16-bit and float32 outputs, m and n not
+    multiples of the tile, two batches."""
+    rng = np.random.default_rng(cfg + out)
+    z, m, n, k = 2, 300, 264, 128
+    a = D.bf16_bits(rng.standard_normal((z, m, k)).astype(np.float32))
+    b = D.bf16_bits(rng.standard_normal((z, n, k)).astype(np.float32))
+    want = np.einsum("zmk,znk->zmn", D.bf16_to_f32(a).astype(np.float64), D.bf16_to_f32(b).astype(np.float64))
+    es = 4 if out == nv.NHIP_F32 else 2
+    da, db, dd = Dev(a), Dev(b), Dev(nbytes=z * m * n * es)
+    desc = _desc(m, n, k, k, 1, 1, k, out=out, cfg=cfg, batch=(z,), sa=(m * k,), sb=(n * k,), sd=(m * n,))
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    if out == nv.NHIP_F32:
+        got = dd.get((z, m, n), np.float32)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
+    else:
+        raw = dd.get((z, m, n), np.uint16)
+        got = D.bf16_to_f32(raw) if out == nv.NHIP_BF16 else raw.view(np.float16).astype(np.float32)
+        np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("at,bt,splits,out", [(True, True, 4, nv.NHIP_BF16), (False, True, 2, nv.NHIP_F32),
+                                              (True, False, 8, nv.NHIP_F16)])
+def test_gemm_splitk(hip, at, bt, splits, out):
+    """Split-k (the weight-gradient shape: small output, deep k): partial products in the workspace, summed in
+    split order; two batches, ragged m and n."""
+    rng = np.random.default_rng(splits)
+    z, m, n, k = 2, 264, 200, 64 * splits * 3
+    a = D.bf16_bits(rng.standard_normal((z, m, k)).astype(np.float32))
+    b = D.bf16_bits(rng.standard_normal((z, k, n)).astype(np.float32))
+    want = np.einsum("zmk,zkn->zmn", D.bf16_to_f32(a).astype(np.float64), D.bf16_to_f32(b).astype(np.float64))
+    am = np.ascontiguousarray(a.transpose(0, 2, 1)) if at else a
+    bm = b if bt else np.ascontiguousarray(b.transpose(0, 2, 1))
+    es = 4 if out == nv.NHIP_F32 else 2
+    da, db, dd = Dev(am), Dev(bm), Dev(nbytes=z * m * n * es)
+    desc = _desc(m, n, k, 1 if at else k, m if at else 1, n if bt else 1, 1 if bt else k, out=out,
+                 batch=(z,), sa=(m * k,), sb=(n * k,), sd=(m * n,))
+    desc.splits = splits
+    ws = C.c_size_t()
+    nv.call("nhip_gemm_workspace", C.byref(desc), C.byref(ws))
+    assert ws.value == splits * z * m * n * 4
+    dw = Dev(nbytes=ws.value)
+    nv.call("nhip_gemm_splitk", C.byref(desc), da.ptr, db.ptr, dd.ptr, dw.ptr)
+    if out == nv.NHIP_F32:
+        got = dd.get((z, m, n), np.float32)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
+    else:
+        raw = dd.get((z, m, n), np.uint16)
+        got = D.bf16_to_f32(raw) if out == nv.NHIP_BF16 else raw.view(np.float16).astype(np.float32)
+        np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
 
 
 def test_gemm_f32_is_the_sequential_fold(hip):
