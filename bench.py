@@ -72,6 +72,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="5", choices=["4", "5", "tiny"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -142,6 +143,13 @@ def main():
             gbs = e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] else 0.0
             entry.update(gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
         breakdown[k] = entry
+    if args.top:
+        for si in sorted(per_step, key=per_step.get, reverse=True)[: args.top]:
+            f, b = plan.cost(si)
+            t = per_step[si]
+            rate = f"{f / (t * 1e-3) / 1e12:7.1f} TF/s" if f else f"{b / (t * 1e-3) / 1e9:7.1f} GB/s"
+            print(f"[top] step {si:4d} {t:8.3f} ms {rate}  {plan.steps[si].kind:9s} {plan.steps[si].name:18s} "
+                  f"{_describe(plan, si)[:110]}", file=sys.stderr)
     # dominant kernel: the step taking the most time
     dom = max(per_step, key=per_step.get)
     f, b = plan.cost(dom)

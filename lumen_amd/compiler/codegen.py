@@ -827,6 +827,44 @@ class LoopKernel:
         return "\n".join(src)
 
 
+class HorizontalKernel:
+    """Several loop kernels in one launch (``passes/horizontal.rs:394,566-605`` per-segment grid ranges): the
+    grid is the members' grids end to end, and each workgroup runs the member whose range holds it, with that
+    member's own block index and grid size."""
+
+    def __init__(self, parts):
+        self.parts = parts
+        self.name = "KNAME"
+        self.args = []
+
+    def source(self):
+        import re
+
+        params, bodies, begin = [], [], 0
+        self.args = []
+        for i, k in enumerate(self.parts):
+            src = k.source()
+            if k.block != (256, 1, 1) or k.lds:
+                raise Unfusable(k.step.outputs[0], "horizontal fusion of a kernel with another block shape")
+            head, _, rest = src.partition("{\n")
+            sig = re.search(r"void\s+\w+\((.*)\)\s*$", head.strip()).group(1)
+            body = rest[: rest.rstrip().rindex("}")]
+            ren = lambda t: re.sub(r"\b(in|out)(\d+)\b", lambda m_: f"m{i}_{m_.group(1)}{m_.group(2)}", t)
+            params.append(ren(sig))
+            body = ren(body).replace("blockIdx.x", "hb_").replace("gridDim.x", "hg_")
+            n = k.grid[0]
+            cond = f"if (b_ < {begin + n})" if i < len(self.parts) - 1 else ""
+            bodies.append(f"  {'else ' if i else ''}{cond} {{\n    const int64_t hb_ = b_ - {begin}, hg_ = {n};\n"
+                          + body + "  }")
+            begin += n
+            self.args += k.args
+        self.grid, self.block, self.lds = (begin, 1, 1), (256, 1, 1), 0
+        return "\n".join(
+            [f'extern "C" __global__ __launch_bounds__(256) void {self.name}({", ".join(params)}) {{',
+             "  const int64_t b_ = blockIdx.x;"] + bodies + ["}"]
+        )
+
+
 def _scatter_kernel(self):
     """``scatter_add``: the output already holds the operand (a fill or copy step before it); each update
     element is added atomically at the entry its index picks (float32; the order of the adds differs from the

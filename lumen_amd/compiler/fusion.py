@@ -331,6 +331,48 @@ def _rematerialize(graph, steps, prod):
     return kept
 
 
+# Horizontal fusion (``passes/horizontal.rs:40-49,79-393``): small independent loop kernels share one launch.
+HFUSE_MAX_ELEMENTS = 1 << 20      # a member's outputs are at most this many elements each
+HFUSE_MAX_MEMBERS = 32
+HFUSE_MAX_HELD_BYTES = 16 << 20   # operand bytes a group may keep alive past their first use
+
+
+def horizontal(graph, steps):
+    """Groups small loop steps that do not read each other's results into ``hloop`` steps. A member runs
+    late, at the group's launch, so the group is launched before the first later step that reads one of its
+    results (or at the end); steps in between keep their order."""
+    def small(st):
+        return st.kind == "loop" and all(graph.types[v].numel() <= HFUSE_MAX_ELEMENTS for v in st.outputs)
+
+    out, group, produced, held = [], [], set(), 0
+
+    def flush():
+        nonlocal group, produced, held
+        if len(group) == 1:
+            out.append(group[0])
+        elif group:
+            st = Step("hloop", [n for m in group for n in m.nodes], [v for m in group for v in m.outputs],
+                      [v for m in group for v in m.inputs])
+            st.members = group
+            out.append(st)
+        group, produced, held = [], set(), 0
+
+    for st in steps:
+        if group and any(u in produced for u in st.inputs):
+            flush()
+        if small(st):
+            nbytes = sum(graph.types[u].nbytes() for u in st.inputs)
+            if len(group) >= HFUSE_MAX_MEMBERS or held + nbytes > HFUSE_MAX_HELD_BYTES:
+                flush()
+            group.append(st)
+            produced.update(st.outputs)
+            held += nbytes
+            continue
+        out.append(st)
+    flush()
+    return out
+
+
 def _index_only(v, prod, done):
     n = prod.get(v)
     if n is None:

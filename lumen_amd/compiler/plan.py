@@ -146,7 +146,10 @@ class Plan:
 
     # ---- fusion with fallback: groups the generator rejects are split
     def _fuse(self):
-        return fusion.fuse(self.graph, fuse_loops=config.compiler.fuse)
+        steps = fusion.fuse(self.graph, fuse_loops=config.compiler.fuse)
+        if config.compiler.fuse and config.compiler.horizontal_fusion:
+            steps = fusion.horizontal(self.graph, steps)
+        return steps
 
     # ---- placement
     def _place(self):
@@ -251,8 +254,23 @@ class Plan:
 
     # ---- kernels
     def _gen_kernels(self):
+        import hashlib
+
         g = self.graph
         for si, st in enumerate(self.steps):
+            if st.kind == "hloop":
+                parts = []
+                for m in st.members:
+                    views = {v: self.loc[v].view() for v in m.inputs}
+                    outs = {v: self.loc[v].view() for v in m.outputs}
+                    parts.append(codegen.LoopKernel(g, m, "KNAME", views, outs))
+                k = codegen.HorizontalKernel(parts)
+                body = k.source()
+                name = f"hloop_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
+                k.name = st.name = name
+                self.kernels[si] = k
+                self.sources[si] = codegen.HEADER + body.replace("KNAME", name)
+                continue
             if st.kind not in ("loop", "row", "reduce", "scatter_add"):
                 continue
             if st.kind == "scatter_add":
@@ -265,8 +283,6 @@ class Plan:
             outs = {v: self.loc[v].view() for v in st.outputs}
             k = codegen.LoopKernel(g, st, "KNAME", views, outs)
             body = k.source()
-            import hashlib
-
             name = f"{st.kind}_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
             k.name = name
             st.name = name
@@ -334,7 +350,7 @@ class Plan:
                     desc = struct.pack("<Q", nbytes)
                     rr = (nv.Reloc * 2)(reloc(0, out), reloc(1, arg))
                     call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
-            if st.kind in ("loop", "row", "reduce", "scatter_add"):
+            if st.kind in ("loop", "row", "reduce", "scatter_add", "hloop"):
                 k = self.kernels[si]
                 fn = nv.module_function(self.objects[si], k.name)
                 if st.kind == "reduce" and getattr(k, "atomic", False):
@@ -352,6 +368,7 @@ class Plan:
                 call("nhip_plan_add_launch", plan, fn, grid, block, k.lds, args, len(args), rr, len(relocs))
             elif st.kind == "dot":
                 desc, ops = self._gemm_desc(st.nodes[0])
+                desc.config = getattr(st, "config", -1)
                 if getattr(st, "splits", 1) > 1:
                     desc.splits = st.splits
                     ops = ops + [self.scratch[id(st)]]
@@ -430,6 +447,52 @@ class Plan:
         d.config = -1
         return d, [lhs, rhs, out]
 
+    # ---- autotuning (lumen/autotune/mod.rs:20-150): bf16/f16 dots of at least 2^30 multiply-adds try every tile
+    # config the kernel accepts, timed with HIP events on the step's own operands (their values do not change
+    # MFMA timing), before the first run; the fastest is kept per (shape, layout, dtype) for the process.
+    AUTOTUNE_MACS = 1 << 30
+    _tuned: dict = {}
+
+    def _autotune(self, workspace_ptr, input_ptrs):
+        from lumen_amd import native as nv
+
+        n_cfg = C.c_int()
+        nv.call("nhip_gemm_config_count", C.byref(n_cfg))
+        ev0, ev1 = nv.Event(), nv.Event()
+        for st in self.steps:
+            if st.kind != "dot" or getattr(st, "splits", 1) > 1:
+                continue
+            try:
+                d, ops = self._gemm_desc(st.nodes[0])
+            except NotImplementedError:
+                continue
+            z = max(1, math.prod(d.batch[i] for i in range(d.nbatch)))
+            if d.a_dtype == nv.NHIP_F32 or d.m * d.n * d.k * z < self.AUTOTUNE_MACS:
+                continue
+            key = (d.m, d.n, d.k, tuple(d.batch[i] for i in range(d.nbatch)), d.a_dtype, d.d_dtype,
+                   d.a_m == 1, d.a_k == 1, d.b_k == 1, d.b_n == 1, d.d_n == 1)
+            if key not in Plan._tuned:
+                ptrs = []
+                for loc in ops:
+                    base = workspace_ptr if loc.base[0] == "ws" else input_ptrs[loc.base[1]]
+                    ptrs.append(base + loc.offset * D.size_of(loc.dtype))
+                best, best_ms = -1, float("inf")
+                for cfg in range(n_cfg.value):
+                    d.config = cfg
+                    try:
+                        nv.call("nhip_gemm", C.byref(d), *ptrs)  # warm-up; rejects configs the shape can't take
+                    except RuntimeError:
+                        continue
+                    ev0.record()
+                    for _ in range(3):
+                        nv.call("nhip_gemm", C.byref(d), *ptrs)
+                    ev1.record()
+                    ms = ev0.elapsed_ms(ev1) / 3
+                    if ms < best_ms:
+                        best, best_ms = cfg, ms
+                Plan._tuned[key] = best
+            st.config = Plan._tuned[key]
+
     # Split-k policy: a bf16/f16 dot whose 256 x 256 output tiles cannot fill the 256 CUs is cut along k (in
     # powers of two, each part at least 1024 deep) until they do; its float32 partials live in the step's
     # scratch (nhip_gemm_splitk).
@@ -453,9 +516,12 @@ class Plan:
         return s
 
     def run_in(self, workspace_ptr: int, input_ptrs: list):
-        """Queues the plan on the stream: inputs are device pointers in graph-input order."""
+        """Queues the plan on the stream: inputs are device pointers in graph-input order. The first run
+        autotunes the plan's large GEMMs on its own buffers (when ``config.compiler.autotune``)."""
         from lumen_amd import native as nv
 
+        if self._native is None and config.compiler.autotune:
+            self._autotune(workspace_ptr, input_ptrs)
         plan = self._native_plan()
         arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
         nv.call("nhip_plan_run", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs))

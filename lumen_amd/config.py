@@ -14,7 +14,7 @@ class CompilerFlags:
     merge_dots: bool = True           # one dot for dots sharing an operand (QKV)
     horizontal_fusion: bool = True    # merge small independent loop kernels into one launch
     epilogue_fusion: bool = True      # fuse elementwise consumers into GEMM stores
-    autotune: bool = False            # time GEMM tile candidates at plan compile
+    autotune: bool = True             # time GEMM tile candidates before a plan's first run
     deterministic: bool = True        # attention backward without atomics
     _version: int = 0
 

@@ -48,3 +48,23 @@ def test_config2_fused_chain_matches_oracle(hip, rows, cols):
     assert [s["kind"] for s in f.plan.describe()] == ["row"]
     (want,) = oracle.values(L.make_graph(_chain)(*args), [x, a, b])
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2)
+
+
+def test_horizontally_fused_loops_match_oracle_bit_for_bit(hip):
+    """Small independent elementwise results computed in one hloop launch equal the oracle exactly (float32
+    and bf16 elementwise ops are correctly rounded on both sides)."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((64, 64)).astype(np.float32)
+    b = _bf16(rng.standard_normal(128))
+    c = rng.standard_normal(1000).astype(np.float32)
+
+    def fn(a, b, c):
+        return a * 2.0 - 1.0, b + 1.0, c * c
+
+    args = [L.from_numpy(a), L.tensor(D.bf16_to_f32(b), "bfloat16"), L.from_numpy(c)]
+    f = L.compile(fn, device="hip")
+    got = [L.to_numpy(t) for t in f(*args)]
+    assert [s["kind"] for s in f.plan.describe()] == ["hloop"]
+    want = oracle.values(L.make_graph(fn)(*args), [a, b, c])
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(np.asarray(g_, np.float32), np.asarray(w_, np.float32))

@@ -144,3 +144,22 @@ def test_gemm_throughput(hip, at, bt):
     e1.record()
     ms = e0.elapsed_ms(e1) / 5
     print(f"gemm 8192^3 at={at} bt={bt}: {ms * 1e3:.1f} us {2 * m * n * k / ms / 1e9:.1f} TFLOP/s")
+
+
+def test_plan_autotunes_large_dots(hip):
+    """A compiled dot of 2^30 multiply-adds is timed over the tile configs before its first run; the chosen
+    config is kept per shape and the result matches the float64 product within bf16 rounding."""
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from lumen_amd.compiler.plan import Plan
+
+    rng = np.random.default_rng(5)
+    x = D.bf16_bits(rng.standard_normal((1024, 1024)).astype(np.float32))
+    w = D.bf16_bits(rng.standard_normal((1024, 1024)).astype(np.float32))
+    fn = L.compile(lambda a, b: F.matmul(a, b.t(), "float32", "bfloat16"), device="hip")
+    got = L.to_numpy(fn(L.tensor(D.bf16_to_f32(x), "bfloat16", "hip"), L.tensor(D.bf16_to_f32(w), "bfloat16", "hip")))
+    want = D.bf16_to_f32(x).astype(np.float64) @ D.bf16_to_f32(w).astype(np.float64).T
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+    dots = [st for st in fn.plan.steps if st.kind == "dot"]
+    assert dots and all(getattr(st, "config", -1) >= 0 for st in dots)
+    assert any(v >= 0 for v in Plan._tuned.values())

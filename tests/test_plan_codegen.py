@@ -60,3 +60,17 @@ def test_generated_kernels_compile_for_gfx950():
     ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
     p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=True)
     assert len(p.objects) == len(p.sources) > 10
+
+
+def test_small_independent_loops_share_one_launch():
+    """Horizontal fusion: three small elementwise results that do not read each other become one hloop step
+    whose grid is the members' grids end to end; large ones keep their own launches."""
+    p = _plan(lambda a, b, c: (a * 2.0, b + 1.0, F.exp(c)), ((64, 64), "float32"), ((128,), "bfloat16"),
+              ((1000,), "float32"), build=True)
+    kinds = [s.kind for s in p.steps]
+    assert kinds.count("hloop") == 1 and "loop" not in kinds
+    (si,) = [i for i, s in enumerate(p.steps) if s.kind == "hloop"]
+    k = p.kernels[si]
+    assert k.grid[0] == sum(m.grid[0] for m in k.parts) and len(k.args) == 6
+    big = _plan(lambda a, b: (a * 2.0, b + 1.0), ((2048, 1024), "float32"), ((2048, 1024), "float32"))
+    assert [s.kind for s in big.steps] == ["loop", "loop"]
