@@ -57,8 +57,9 @@ def _row_space(graph, n):
     return (math.prod(x.shape[: r - len(axes)]), c)
 
 
-def fuse(graph: Graph, fuse_loops=True) -> list:
-    """The steps computing ``graph``'s outputs, in an order respecting dependencies."""
+def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
+    """The steps computing ``graph``'s outputs, in an order respecting dependencies. ``packed`` holds
+    concatenations that are views (weights stored back to back)."""
     users = graph.users()
     prod = graph.producers()
     order = {n.output: i for i, n in enumerate(graph.nodes)}
@@ -73,12 +74,14 @@ def fuse(graph: Graph, fuse_loops=True) -> list:
             for j, u in enumerate(n.inputs):
                 if n.prim == "scatter_add" and j == 0 and u in prod and prod[u].prim == "full":
                     continue
-                while u in prod and prod[u].prim in VIEWABLE and u not in graph.outputs:
+                while u in prod and (prod[u].prim in VIEWABLE or u in packed) and u not in graph.outputs:
                     views.add(u)
                     u = prod[u].inputs[0]
                 must.add(u)
-    for v in views:
-        must.add(prod[v].inputs[0])
+    for v in views:  # a view's base is in memory (or is itself a view of memory)
+        for u in (prod[v].inputs if v in packed else prod[v].inputs[:1]):
+            if u not in views:
+                must.add(u)
     kernel_of: dict[int, int] = {}
     members: list[set] = []
     kinds: list[str] = []

@@ -17,7 +17,7 @@ from dataclasses import dataclass
 
 from lumen_amd import dtypes as D
 from lumen_amd.compiler import attention as attn_pass
-from lumen_amd.compiler import codegen, fusion, kcache, passes
+from lumen_amd.compiler import codegen, fusion, kcache, merge, passes
 from lumen_amd.config import config
 from lumen_amd.graph.ir import Graph
 
@@ -118,23 +118,36 @@ def _reshape_strides(shape, strides, new):
     return tuple(out)
 
 
-def compile_graph(graph: Graph) -> Graph:
+def compile_graph(graph: Graph, packable=()) -> tuple[Graph, list]:
     """The hip pipeline (``graph_compiler/pipeline.rs:162-320`` picks): frontend (cse, simplify), flash
-    attention forward and backward matching, simplify again."""
+    attention forward and backward matching, merge_dots over the weights at input positions ``packable``,
+    simplify again. Returns the graph and merge_dots' packs (weight input positions stored back to back)."""
     g = passes.frontend(graph)
     if config.compiler.flash_attention:
         g = attn_pass.match(g)
         g = passes.frontend(g)
-    return g
+    packs = []
+    if config.compiler.merge_dots and packable:
+        g, packs = merge.merge_dots(g, set(packable))
+        if packs:
+            g = passes.frontend(g)
+    return g, packs
 
 
 class Plan:
     """A graph compiled for ``device`` (``"hip:0"``): steps, workspace layout and native step list."""
 
-    def __init__(self, graph: Graph, device="hip:0", build_kernels=True):
+    def __init__(self, graph: Graph, device="hip:0", build_kernels=True, packable=()):
         self.device = device
         self.source_graph = graph
-        self.graph = compile_graph(graph)
+        self.graph, self.packs = compile_graph(graph, packable)
+        # concatenations of a pack's weights: views of the first weight's memory (the caller stores a pack's
+        # weights back to back, in order)
+        self.packed = set()
+        packed_inputs = {tuple(self.graph.inputs[i] for i in pk) for pk in self.packs}
+        for n in self.graph.nodes:
+            if n.prim == "concatenate" and n.params["dimension"] == 0 and tuple(n.inputs) in packed_inputs:
+                self.packed.add(n.output)
         self.steps = self._fuse()
         self._place()
         self.kernels = {}
@@ -146,7 +159,7 @@ class Plan:
 
     # ---- fusion with fallback: groups the generator rejects are split
     def _fuse(self):
-        steps = fusion.fuse(self.graph, fuse_loops=config.compiler.fuse)
+        steps = fusion.fuse(self.graph, fuse_loops=config.compiler.fuse, packed=self.packed)
         if config.compiler.fuse and config.compiler.horizontal_fusion:
             steps = fusion.horizontal(self.graph, steps)
         return steps
@@ -210,7 +223,11 @@ class Plan:
             if st.kind == "view":
                 n = st.nodes[0]
                 src = self.loc[n.inputs[0]]
-                loc = _view_of(n.prim, n.params, src, g.types[n.output])
+                if n.output in self.packed:
+                    t = g.types[n.output]
+                    loc = Loc(src.base, src.offset, _contig(t.shape), t.dtype, t.shape)
+                else:
+                    loc = _view_of(n.prim, n.params, src, g.types[n.output])
                 if loc is not None:
                     self.loc[n.output] = loc
                     base_of[n.output] = base_of.get(n.inputs[0], n.inputs[0])

@@ -56,10 +56,13 @@ class Compiled:
             if device_type(target) == "hip":
                 from lumen_amd.compiler.plan import Plan
 
-                plan = Plan(traced.graph, target)
+                weight_pos = [i for i, (kind, _) in enumerate(traced.layout) if kind == "weight"]
+                plan = Plan(traced.graph, target, packable=weight_pos)
                 workspace = DeviceBuffer(int(target.split(":")[1]), plan.workspace_bytes)
                 for w in traced.weights:
                     w._placed(target)
+                for pack in plan.packs:
+                    _pack([traced.weights[traced.layout[i][1]] for i in pack], target)
             entry = (traced, plan, workspace)
             self._plans[key] = entry
         self._latest = key
@@ -112,6 +115,29 @@ class Compiled:
             nn.assign(args[i], path, value)
         it = iter(outs)
         return _rebuild(traced.out, it)
+
+
+def _pack(weights, target):
+    """Stores ``weights`` back to back in one device block, in order (a merge_dots pack: the plan reads their
+    concatenation as a view of the first), moving their current data there; a no-op when they already are."""
+    placed = [w._placed(target) for w in weights]
+    first = placed[0]
+    if all(t._buffer is first._buffer for t in placed):
+        off = first._offset
+        for t in placed:
+            if t._offset != off:
+                break
+            off += t.nbytes
+        else:
+            return
+    dev = int(target.split(":")[1])
+    block = DeviceBuffer(dev, sum(t.nbytes for t in placed))
+    off = 0
+    for w, t in zip(weights, placed):
+        nt = Tensor(t.dtype, t.shape, target, buffer=block, offset=off)
+        nt.copy_(t)
+        w._placements[device_name(target)] = nt
+        off += t.nbytes
 
 
 def _size(dtype):

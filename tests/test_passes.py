@@ -111,3 +111,27 @@ def test_fusion_of_the_training_step_preserves_dependencies():
     assert set(g.outputs) <= have
     kinds = {st.kind for st in steps}
     assert {"dot", "row", "flash_fwd", "flash_bwd", "scatter_add"} <= kinds
+
+
+def test_merge_dots_packs_projections_and_their_gradients():
+    """merge_dots (passes/merge_dots): the three projections of one activation become one dot against the
+    packed weights, and their backward (the summed input gradient and the three weight gradients) one dot
+    each; values stay within float32 reassociation of the unmerged graph."""
+    from lumen_amd.compiler import merge
+
+    def f(x, wq, wk, wv):
+        q = F.matmul(x, wq.t(), "float32", "float32")
+        k = F.matmul(x, wk.t(), "float32", "float32")
+        v = F.matmul(x, wv.t(), "float32", "float32")
+        return ((q * k + v) * x.sum()).sum()
+
+    metas = [L.empty([16, 32], "float32", "meta")] + [L.empty([24, 32], "float32", "meta") for _ in range(3)]
+    g0 = passes.frontend(L.make_graph(L.value_and_grad(f, argnums=(0, 1, 2, 3)))(*metas))
+    g1, packs = merge.merge_dots(g0, {1, 2, 3})
+    assert packs == [(1, 2, 3)]
+    dots = lambda g: sum(n.prim == "dot_general" for n in g.nodes)
+    assert dots(g0) == 9 and dots(g1) == 3
+    xs = _inputs(g0)
+    for a, b in zip(oracle.run(g0, xs), oracle.run(g1, xs)):
+        np.testing.assert_allclose(np.asarray(a, np.float64), np.asarray(b, np.float64), rtol=1e-5,
+                                   atol=1e-5 * max(1.0, float(np.abs(a).max())))
