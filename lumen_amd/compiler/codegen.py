@@ -673,7 +673,14 @@ class LoopKernel:
         J = -(-chunks // T)
         exact = C % (T * V) == 0
         em = self._emitter(rows=(R, C))
-        em.vec = V if exact else 1
+        # C % V == 0, so a V-element chunk is wholly inside the row or wholly past it: past-the-end chunks load
+        # the row's last chunk (a clamped base keeps vector loads in bounds) and are masked out of reductions
+        # and stores
+        em.vec = V
+
+        def vbase(j):
+            b = f"(({j} * {T} + tid) * {V})"
+            return b if exact else f"({b} < {C - V} ? (int64_t){b} : {C - V}LL)"
         body = []
         red_identity = {"reduce_sum": "0", "reduce_max": "-INFINITY"}
         for red in reds:
@@ -688,7 +695,7 @@ class LoopKernel:
                     if cidx not in _declared(em):
                         em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
                         _declared(em).add(cidx)
-                    idx = ("rc", "r", cidx, f"(({j} * {T} + tid) * {V})", lane)
+                    idx = ("rc", "r", cidx, vbase(j), lane)
                     val = em.value(red.inputs[0], idx)
                     guard = "" if exact else f"if ({cexpr} < {C}LL) "
                     if red.prim == "reduce_sum":
@@ -723,7 +730,7 @@ class LoopKernel:
                 if cidx not in _declared(em):
                     em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
                     _declared(em).add(cidx)
-                idx = ("rc", "r", cidx, f"(({j} * {T} + tid) * {V})", lane)
+                idx = ("rc", "r", cidx, vbase(j), lane)
                 lanes.append([em.value(v, idx) for v in outs_elem])
             for k, v in enumerate(outs_elem):
                 oi = st.outputs.index(v)
