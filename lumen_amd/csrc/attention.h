@@ -13,6 +13,8 @@
 //  * P is rounded to the inputs' dtype before P V, as the reference does (kernel.py:99).
 #pragma once
 
+#include <type_traits>
+
 #include "device_common.h"
 #include "nhip_internal.h"
 
@@ -406,66 +408,112 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         const char *Qb = reinterpret_cast<const char *>(smem + (j & 1) * 2 * TILE);
         const char *Gb = Qb + TILE * 2;
         const float *Lt = Ls[j & 1], *Dt = Dl[j & 1];
-        // rows q with q > sq - 1 or (causal) kj > q + shift are masked
+        // rows q with q > sq - 1 or (causal) kj > q + shift are masked: tile row r is kept when rmin <= r < rmax
         const bool masked = q0 + BM > p.sq || (CAUSAL && q0 + shift < kb0 + 127);
+        const int rmin = CAUSAL ? int(min<int64_t>(max<int64_t>(kj - shift - q0, 0), BM)) : 0;
+        const int rmax = int(min<int64_t>(p.sq - q0, BM));
+
+        // phase 1: S and dP of both 32-query halves (4 independent MFMA chains), row fragments of Q and dO read
+        // one k step ahead
+        f32x16_t sv[2], dp[2];
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
-            if (CAUSAL && q0 + 32 * qs + 31 + shift < kb0 + 32 * wave) continue;  // all masked for this wave
-            f32x16_t sv, dp;
+        for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) sv[e] = dp[e] = 0.0f;
+            for (int e = 0; e < 16; ++e) sv[qs][e] = dp[qs][e] = 0.0f;
+        uint4 fq[2][2], fg[2][2];
+        auto rows = [&](int buf, int t) {
 #pragma unroll
-            for (int t = 0; t < DS; ++t) {
+            for (int qs = 0; qs < 2; ++qs) {
                 const int off = kv_off<D>(32 * qs + l32, 16 * t + 8 * h);
-                uint4 a = *reinterpret_cast<const uint4 *>(Qb + off);
-                uint4 c = *reinterpret_cast<const uint4 *>(Gb + off);
-                sv = mfma32<F16>(a, kf[t], sv);
-                dp = mfma32<F16>(c, vf[t], dp);
+                fq[buf][qs] = *reinterpret_cast<const uint4 *>(Qb + off);
+                fg[buf][qs] = *reinterpret_cast<const uint4 *>(Gb + off);
             }
-            uint4 pb[2], sb[2];
+        };
+        rows(0, 0);
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint32_t wp[4], ws[4];
+        for (int t = 0; t < DS; ++t) {
+            const int cur = t & 1;
+            if (t + 1 < DS) rows(cur ^ 1, t + 1);
 #pragma unroll
-                for (int jj = 0; jj < 8; jj += 2) {
-                    float pv[2], dv2[2];
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const int e = 8 * half + jj + u;
-                        const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
-                        float pe = fast_exp2(fmaf(sv[e], c2, -Lt[r]));
-                        if (masked) {
-                            const int64_t q = q0 + r;
-                            const bool ok = q < p.sq && (!CAUSAL || kj <= q + shift);
-                            pe = ok ? pe : 0.0f;
-                        }
-                        pv[u] = pe;
-                        dv2[u] = pe * (dp[e] - Dt[r]) * p.scale;
-                    }
-                    wp[jj / 2] = pack2<F16>(pv[0], pv[1]);
-                    ws[jj / 2] = pack2<F16>(dv2[0], dv2[1]);
-                }
-                pb[half] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
-                sb[half] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
-            }
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int r0 = 32 * qs + 16 * half + 4 * h + s16 / 4;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
-                    const int o0 = kv_off<D>(r0, col), o1 = kv_off<D>(r0 + 8, col);
-                    v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o0));
-                    v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o1));
-                    uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
-                    adv[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), pb[half], adv[dt]);
-                    x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o0));
-                    y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o1));
-                    xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
-                    adk[dt] = mfma32<F16>(make_uint4(xa.x, xa.y, ya.x, ya.y), sb[half], adk[dt]);
-                }
+            for (int qs = 0; qs < 2; ++qs) {
+                sv[qs] = mfma32<F16>(fq[cur][qs], kf[t], sv[qs]);
+                dp[qs] = mfma32<F16>(fg[cur][qs], vf[t], dp[qs]);
             }
         }
+        // issue order: two k steps of reads, then one read of k step t + 2 after each MFMA of step t
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+        mfma_then_ds<4 * DS - 8, 1, 1>();
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // phase 2: P = 2^(S scale log2 e - lse log2 e) and dS = P (dP - delta) scale, packed as B operands
+        uint4 pb[2][2], sb[2][2];
+        auto probs = [&](auto maskedc) {
+            constexpr bool MASKED = decltype(maskedc)::value;
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    uint32_t wp[4], ws[4];
+#pragma unroll
+                    for (int jj = 0; jj < 8; jj += 2) {
+                        float pv[2], dv2[2];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const int e = 8 * half + jj + u;
+                            const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
+                            float pe = fast_exp2(fmaf(sv[qs][e], c2, -Lt[r]));
+                            if constexpr (MASKED) pe = ((r >= rmin) & (r < rmax)) ? pe : 0.0f;
+                            pv[u] = pe;
+                            dv2[u] = pe * (dp[qs][e] - Dt[r]) * p.scale;
+                        }
+                        wp[jj / 2] = pack2<F16>(pv[0], pv[1]);
+                        ws[jj / 2] = pack2<F16>(dv2[0], dv2[1]);
+                    }
+                    pb[qs][half] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
+                    sb[qs][half] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
+                }
+        };
+        if (masked) probs(std::true_type{});
+        else probs(std::false_type{});
+        __builtin_amdgcn_sched_barrier(0);
+
+        // phase 3: dV^T += dO^T P and dK^T += Q^T dS (8 independent chains), transposed fragments read one step
+        // ahead
+        uint4 tg[2][DT], tq[2][DT];
+        auto trs = [&](int buf, int step) {
+            const int qs = step >> 1, half = step & 1;
+            const int r0 = 32 * qs + 16 * half + 4 * h + s16 / 4;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int col = 32 * dt + 16 * (g & 1) + 4 * (s16 & 3);
+                const int o0 = kv_off<D>(r0, col), o1 = kv_off<D>(r0 + 8, col);
+                v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o0));
+                v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Gb + o1));
+                uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                tg[buf][dt] = make_uint4(xa.x, xa.y, ya.x, ya.y);
+                x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o0));
+                y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(Qb + o1));
+                xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                tq[buf][dt] = make_uint4(xa.x, xa.y, ya.x, ya.y);
+            }
+        };
+        trs(0, 0);
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+            const int cur = step & 1, qs = step >> 1, half = step & 1;
+            if (step + 1 < 4) trs(cur ^ 1, step + 1);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                adv[dt] = mfma32<F16>(tg[cur][dt], pb[qs][half], adv[dt]);
+                adk[dt] = mfma32<F16>(tq[cur][dt], sb[qs][half], adk[dt]);
+            }
+        }
+        // issue order: the first step's reads, then two reads of the next step after each MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 * DT, 2);
+        mfma_then_ds<6 * DT, 2, 2>();
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * DT, 2);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (!kvalid) return;
     uint16_t *dkp = p.dk + b * p.dk_b + nkv * p.dk_n + kj * p.dk_s;

@@ -72,4 +72,26 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Scheduling constraint: M MFMAs with NR LDS reads spread evenly between them (sched_group_barrier groups
+// of sync id ID, in issue order).
+template <int T, int M, int NR, int ID>
+__device__ __forceinline__ void mfma_ds_interleave() {
+    if constexpr (T < M) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, ID);
+        constexpr int r = NR * (T + 1) / M - NR * T / M;
+        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, ID);
+        mfma_ds_interleave<T + 1, M, NR, ID>();
+    }
+}
+
+// Scheduling constraint: N times {one MFMA, then R LDS reads} (sync id ID).
+template <int N, int R, int ID>
+__device__ __forceinline__ void mfma_then_ds() {
+    if constexpr (N > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, ID);
+        if constexpr (R > 0) __builtin_amdgcn_sched_group_barrier(0x100, R, ID);
+        mfma_then_ds<N - 1, R, ID>();
+    }
+}
+
 }  // namespace nhipk

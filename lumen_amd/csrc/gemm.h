@@ -358,17 +358,6 @@ constexpr int gemm_stream_lds_bytes() {
     return 128 * 1024 > 2 * WN * 64 * gemm_stream_stage_pitch<WN>() ? 128 * 1024 : 2 * WN * 64 * gemm_stream_stage_pitch<WN>();
 }
 
-// Scheduling constraint for one k step: M MFMAs with NR LDS reads spread evenly between them.
-template <int T, int M, int NR, int ID>
-__device__ __forceinline__ void mfma_ds_interleave() {
-    if constexpr (T < M) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, ID);
-        constexpr int r = NR * (T + 1) / M - NR * T / M;
-        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, ID);
-        mfma_ds_interleave<T + 1, M, NR, ID>();
-    }
-}
-
 template <bool F16, int BK, int WN, bool AT, bool BT>
 __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
