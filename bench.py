@@ -73,6 +73,9 @@ def main():
     ap.add_argument("--config", default="5", choices=["4", "5", "tiny"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
+    ap.add_argument("--probe", action="store_true",
+                    help="after the measurement, replay the dominant step alone 3 times and a 1 GiB device copy 3 "
+                         "times (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -165,6 +168,16 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
     roof["kernel"] = f"{st.kind} step {dom}: {_describe(plan, dom)}"
     roof["per_launch"] = {"flops": f, "bytes": b, "ms": round(t_dom, 4)}
+    roof["traffic"] = _traffic(roof["kernel"], args.config)
+    if args.probe:
+        ws, ptrs = step.last_buffers()
+        for _ in range(3):
+            plan.run_steps(ws, ptrs, dom)
+        native.sync()
+        for _ in range(3):
+            native.d2d(ws, ws + (1 << 30), 1 << 30)
+        native.sync()
+        print(f"[probe] dominant step {dom} ({roof['kernel']}) x3, then a 1 GiB copy x3", file=sys.stderr, flush=True)
 
     out = {
         "metric": METRIC,
@@ -195,6 +208,21 @@ def main():
         out["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(out), flush=True)
     del np
+
+
+def _traffic(kernel, config):
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of
+    ``bench.py --probe`` and scaled by the same counters' reading for a 1 GiB copy (profiles/traffic.json);
+    None when no measurement for this kernel and config is recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    for r in rec:
+        if r.get("config") == config and r.get("kernel") == kernel:
+            return r["traffic"]
+    return None
 
 
 def _describe(plan, si):

@@ -200,6 +200,9 @@ int nhip_plan_add_builtin(void *plan, int kind, const void *desc, size_t desc_by
                           size_t nrelocs);
 /* Queues every step on the stream, in order (never waits). */
 int nhip_plan_run(void *plan, void *workspace, void *const *inputs, size_t ninputs);
+/* Queues steps [begin, end) only (profiling one step's kernels in isolation; the caller keeps their inputs
+ * valid, e.g. by a whole run first). Per-step profiling events are recorded by whole runs only. */
+int nhip_plan_run_steps(void *plan, void *workspace, void *const *inputs, size_t ninputs, size_t begin, size_t end);
 /* Number of steps (for tests). */
 int nhip_plan_steps(void *plan, size_t *count);
 /* Profiling: with `enable`, each run records a HIP event before every step and after the last, on the

@@ -543,6 +543,15 @@ class Plan:
         arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
         nv.call("nhip_plan_run", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs))
 
+    def run_steps(self, workspace_ptr: int, input_ptrs: list, si: int):
+        """Queues the native steps of python step ``si`` alone (after a whole run has produced its inputs)."""
+        from lumen_amd import native as nv
+
+        plan = self._native_plan()
+        idx = [i for i, s in enumerate(self.native_steps) if s == si]
+        arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
+        nv.call("nhip_plan_run_steps", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs), idx[0], idx[-1] + 1)
+
     def __del__(self):
         if getattr(self, "_native", None) is not None:
             try:

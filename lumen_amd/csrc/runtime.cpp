@@ -487,12 +487,21 @@ int nhip_plan_steps(void *plan, size_t *count) {
 
 int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninputs) {
     Plan *plan = static_cast<Plan *>(plan_);
+    return nhip_plan_run_steps(plan_, workspace, inputs, ninputs, 0, plan->steps.size());
+}
+
+int nhip_plan_run_steps(void *plan_, void *workspace, void *const *inputs, size_t ninputs, size_t begin, size_t end) {
+    Plan *plan = static_cast<Plan *>(plan_);
     hipStream_t s = stream_of_current();
     if (!s) return fail("no HIP stream: call nhip_set_device first");
+    if (begin > end || end > plan->steps.size())
+        return fail("nhip_plan_run_steps: steps [" + std::to_string(begin) + ", " + std::to_string(end) + ") of " +
+                    std::to_string(plan->steps.size()));
+    const bool whole = begin == 0 && end == plan->steps.size();
     char *ws = static_cast<char *>(workspace);
-    for (size_t i = 0; i < plan->steps.size(); ++i) {
+    for (size_t i = begin; i < end; ++i) {
         Step &st = plan->steps[i];
-        if (plan->profile && check(hipEventRecord(plan->events[i], s), "hipEventRecord")) return 1;
+        if (whole && plan->profile && check(hipEventRecord(plan->events[i], s), "hipEventRecord")) return 1;
         auto resolve = [&](const nhip_reloc &r, void **out) -> int {
             char *base;
             if (r.base == NHIP_BASE_WORKSPACE) {
@@ -551,7 +560,8 @@ int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninp
         }
         if (rc) return fail("plan step " + std::to_string(i) + ": " + g_error);
     }
-    if (plan->profile && check(hipEventRecord(plan->events[plan->steps.size()], s), "hipEventRecord")) return 1;
+    if (whole && plan->profile && check(hipEventRecord(plan->events[plan->steps.size()], s), "hipEventRecord"))
+        return 1;
     return 0;
 }
 

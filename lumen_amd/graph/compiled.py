@@ -72,6 +72,10 @@ class Compiled:
     def plan(self):
         return self._plans[self._latest][1]
 
+    def last_buffers(self):
+        """``(workspace pointer, input pointers)`` of the latest run (to replay some of its steps)."""
+        return self._last_buffers
+
     @property
     def graph(self):
         return self._plans[self._latest][0].graph
@@ -103,6 +107,7 @@ class Compiled:
                     keep.append(t)
                     ptrs.append(t.data_ptr())
             plan.run_in(workspace.ptr, ptrs)
+            self._last_buffers = (workspace.ptr, ptrs)
             outs = []
             for v, loc in zip(g.outputs, plan.output_locs):
                 t = Tensor(loc.dtype, loc.shape, target, buffer=workspace, offset=loc.offset * _size(loc.dtype))

@@ -136,6 +136,10 @@ SIGNATURES = {
     ),
     "nhip_plan_add_builtin": ([C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.POINTER(Reloc), C.c_size_t], C.c_int),
     "nhip_plan_run": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p), C.c_size_t], C.c_int),
+    "nhip_plan_run_steps": (
+        [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p), C.c_size_t, C.c_size_t, C.c_size_t],
+        C.c_int,
+    ),
     "nhip_plan_steps": ([C.c_void_p, C.POINTER(C.c_size_t)], C.c_int),
     "nhip_plan_profile": ([C.c_void_p, C.c_int], C.c_int),
     "nhip_plan_step_ms": ([C.c_void_p, C.POINTER(C.c_float), C.c_size_t], C.c_int),
