@@ -385,11 +385,13 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     const uint16_t *pa = a + oa + ks * s.a_k, *pb = b + ob + ks * s.b_k;
     const int ktiles = int(s.k / BK);
 
-    auto issue = [&](int st, int kt) {
+    // issues this wave's loads [lo, hi) of tile kt into stage st (A segments first, then B)
+    auto issue = [&](int st, int kt, int lo, int hi) {
         char *base = smem + st * STAGE_BYTES;
         const int64_t k0 = int64_t(kt) * BK;
 #pragma unroll
         for (int i = 0; i < TA::segs / NW; ++i) {
+            if (i < lo || i >= hi) continue;
             const int seg = wave + NW * i;
             const int line = seg * TA::lines_per_seg + lane / TA::chunks, c = lane % TA::chunks;
             const uint16_t *src;
@@ -406,6 +408,7 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
         }
 #pragma unroll
         for (int i = 0; i < TB::segs / NW; ++i) {
+            if (TA::segs / NW + i < lo || TA::segs / NW + i >= hi) continue;
             const int seg = wave + NW * i;
             const int line = seg * TB::lines_per_seg + lane / TB::chunks, c = lane % TB::chunks;
             const uint16_t *src;
@@ -448,7 +451,7 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
 
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
-        if (st < ktiles) issue(st, st);
+        if (st < ktiles) issue(st, st, 0, LPS);
     for (int kt = 0; kt < ktiles; ++kt) {
         // wait for this thread's loads of tile kt: later tiles' loads may stay in flight
         const int later = min(STAGES - 2, ktiles - 1 - kt);
@@ -456,7 +459,7 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
         else if (later == 1) __builtin_amdgcn_s_waitcnt((LPS & 15) | ((LPS >> 4) << 14) | 0x0070 | 0x0f00);
         else __builtin_amdgcn_s_waitcnt(((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | 0x0070 | 0x0f00);
         __syncthreads();  // every thread's loads of tile kt landed; the stage of tile kt - 1 is free
-        if (kt + STAGES - 1 < ktiles) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+        const bool more = kt + STAGES - 1 < ktiles;
         const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
         const char *tb = ta + TA::bytes;
         uint4 fa[2][4], fb[2][FN];
@@ -473,6 +476,9 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
             constexpr int cur = (kk / 16) & 1;
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (kk + 16 < BK) read(cur ^ 1, kk + 16);
+            // the next stage's loads, a quarter (a half for BK 32) each k step: spread among the MFMAs
+            // rather than issued in one burst after the barrier
+            if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
