@@ -83,6 +83,18 @@ def _view_of(prim, params, src: Loc, ty) -> Loc | None:
     return None
 
 
+def _operand_view(cat: Loc, start, operand, ty) -> Loc:
+    """Where an operand of a concatenation lives inside it: the slice ``start = (dim, offset)`` of shape
+    ``operand.shape``, reshaped to the producer's type ``ty``."""
+    dim, off = start
+    sl = Loc(cat.base, cat.offset + off * cat.strides[dim], cat.strides, operand.dtype, operand.shape)
+    if operand.shape == ty.shape:
+        return Loc(sl.base, sl.offset, sl.strides, ty.dtype, ty.shape)
+    st = _reshape_strides(sl.shape, sl.strides, ty.shape)
+    assert st is not None, "checked when the alias was chosen"
+    return Loc(sl.base, sl.offset, st, ty.dtype, ty.shape)
+
+
 def _reshape_strides(shape, strides, new):
     """torch's view rule: strides for ``new`` over memory laid out as ``shape``/``strides``, or None."""
     dims = [(n, s) for n, s in zip(shape, strides) if n != 1]
@@ -218,8 +230,17 @@ class Plan:
                     merged.append((o, s))
             free[:] = merged
 
+        # concatenations whose operands are written straight into the result by their producers
+        aliases = self._concat_aliases()
+        for si, st in enumerate(self.steps):
+            if st.kind == "alias":
+                c = st.outputs[0]
+                last_use[c] = max(last_use.get(c, si), si)
+
         converted = []
         for si, st in enumerate(self.steps):
+            if st.kind == "alias":
+                continue
             if st.kind == "view":
                 n = st.nodes[0]
                 src = self.loc[n.inputs[0]]
@@ -236,6 +257,15 @@ class Plan:
                 converted.append(si)
             for v in st.outputs:
                 t = g.types[v]
+                if v in aliases:
+                    c, start, _ = aliases[v]
+                    if c not in self.loc:  # the concatenation's memory is taken at its first producer
+                        ct = g.types[c]
+                        off, size = take(ct.nbytes())
+                        live[c] = (off, size)
+                        self.loc[c] = Loc(("ws", 0), off // D.size_of(ct.dtype), _contig(ct.shape), ct.dtype, ct.shape)
+                    self.loc[v] = _operand_view(self.loc[c], start, aliases[v][2], t)
+                    continue
                 off, size = take(t.nbytes())
                 live[v] = (off, size)
                 self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
@@ -268,6 +298,58 @@ class Plan:
                 self._copies[len(self.steps) - 1] = (loc, dst)
                 loc = dst
             self.output_locs.append(loc)
+
+    # the producers that may write an operand of a concatenation in place, through a strided view
+    ALIAS_PRODUCERS = ("flash_fwd", "flash_bwd", "dot", "loop")
+
+    def _concat_aliases(self):
+        """``{value: (concatenation, start, operand type)}`` for loop steps that only concatenate (through
+        reshapes) values produced by earlier kernels that read nothing else of them: each such value is
+        placed as a strided view into the concatenation at ``start`` along its dimension, and the step
+        becomes an ``alias`` (no launch). A step qualifies only if every operand does."""
+        g = self.graph
+        users: dict[int, list] = {}
+        producer: dict[int, object] = {}
+        for st in self.steps:
+            for u in st.inputs:
+                users.setdefault(u, []).append(st)
+            for v in st.outputs:
+                producer[v] = st
+        outputs = set(g.outputs)
+        aliases = {}
+        for st in self.steps:
+            if st.kind != "loop" or len(st.outputs) != 1 or st.nodes[-1].prim != "concatenate":
+                continue
+            cat = st.nodes[-1]
+            if cat.output != st.outputs[0] or any(n.prim != "reshape" for n in st.nodes[:-1]):
+                continue
+            made = {n.output: n.inputs[0] for n in st.nodes[:-1]}
+            dim = cat.params["dimension"]
+            found, start, ok = {}, 0, True
+            for u in cat.inputs:
+                v = u
+                while v in made:
+                    v = made[v]
+                p_ = producer.get(v)
+                if (p_ is None or p_.kind not in self.ALIAS_PRODUCERS or v in outputs or v in found
+                        or v in aliases or any(x is not st for x in users.get(v, []))):
+                    ok = False
+                    break
+                # the operand's place in the concatenation, as the producer's shape; kernels need a
+                # unit-stride innermost dimension
+                ct = g.types[cat.output]
+                view = _operand_view(Loc(("ws", 0), 0, _contig(ct.shape), ct.dtype, ct.shape), (dim, start),
+                                     g.types[u], g.types[v]) if _reshape_strides(
+                    g.types[u].shape, _contig(ct.shape), g.types[v].shape) is not None else None
+                if view is None or (view.strides and view.strides[-1] != 1):
+                    ok = False
+                    break
+                found[v] = (cat.output, (dim, start), g.types[u])
+                start += g.types[u].shape[dim]
+            if ok and found:
+                aliases.update(found)
+                st.kind = "alias"
+        return aliases
 
     # ---- kernels
     def _gen_kernels(self):
@@ -400,7 +482,7 @@ class Plan:
                 desc = struct.pack("<Q", g.types[st.outputs[0]].nbytes())
                 rr = (nv.Reloc * 2)(reloc(0, dst), reloc(1, src))
                 call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
-            elif st.kind == "view":
+            elif st.kind in ("view", "alias"):
                 continue
             else:
                 raise NotImplementedError(f"{st.kind}: the hip backend has no kernel for it yet")

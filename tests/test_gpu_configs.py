@@ -68,3 +68,23 @@ def test_horizontally_fused_loops_match_oracle_bit_for_bit(hip):
     want = oracle.values(L.make_graph(fn)(*args), [a, b, c])
     for g_, w_ in zip(got, want):
         assert np.array_equal(np.asarray(g_, np.float32), np.asarray(w_, np.float32))
+
+
+def test_concatenated_dot_results_written_in_place_match_oracle(hip):
+    """Two dots writing straight into their concatenation (strided GEMM stores, no copy launch), then a dot
+    reading it, against the oracle (bf16 tolerance: the reference's bf16 bounds)."""
+    rng = np.random.default_rng(3)
+
+    def fn(x, w1, w2, w3):
+        a = F.matmul(x, w1, "float32", "bfloat16")
+        b = F.matmul(x, w2, "float32", "bfloat16")
+        return F.matmul(F.cat([a, b], 1), w3, "float32", "bfloat16")
+
+    shapes = [(2048, 256), (256, 512), (256, 512), (1024, 128)]
+    xs = [_bf16(rng.standard_normal(s) * 0.5) for s in shapes]
+    args = [L.tensor(D.bf16_to_f32(x), "bfloat16") for x in xs]
+    f = L.compile(fn, device="hip")
+    got = np.asarray(L.to_numpy(f(*args)), np.float32)
+    assert "alias" in [s["kind"] for s in f.plan.describe()]
+    (want,) = oracle.values(L.make_graph(fn)(*args), xs)
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())

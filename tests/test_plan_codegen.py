@@ -49,6 +49,27 @@ def test_transposed_weight_feeds_the_dot_as_a_view():
     assert (desc.m, desc.n, desc.k, desc.b_k, desc.b_n) == (64, 48, 32, 1, 32)
 
 
+def test_concatenated_dot_results_are_written_in_place():
+    """Two dot results only read by a concatenation are placed inside it as strided views: the
+    concatenation launches nothing, and the consuming dot reads the one buffer."""
+    def fn(x, w1, w2, w3):
+        a = F.matmul(x, w1, "float32", "bfloat16")
+        b = F.matmul(x, w2, "float32", "bfloat16")
+        return F.matmul(F.cat([a, b], 1), w3, "float32", "bfloat16")
+
+    p = _plan(fn, ((2048, 256), "bfloat16"), ((256, 512), "bfloat16"), ((256, 512), "bfloat16"),
+              ((1024, 128), "bfloat16"))
+    kinds = [s.kind for s in p.steps]
+    assert kinds == ["dot", "dot", "alias", "dot"], kinds
+    a, b = p.steps[0].outputs[0], p.steps[1].outputs[0]
+    c = p.steps[2].outputs[0]
+    la, lb, lc = p.loc[a], p.loc[b], p.loc[c]
+    assert la.strides == lb.strides == (1024, 1) and lc.strides == (1024, 1)
+    assert {la.offset, lb.offset} == {lc.offset, lc.offset + 512}
+    desc, _ = p._gemm_desc(p.steps[1].nodes[0])
+    assert (desc.d_m, desc.d_n) == (1024, 1)
+
+
 def test_one_row_kernel_for_a_normalization_chain():
     p = _plan(lambda x, w: F.softmax(F.rms_norm(x, 256, w) * 3.0, -1), ((32, 256), "float32"), ((256,), "float32"))
     assert [s.kind for s in p.steps] == ["row"]
