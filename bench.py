@@ -153,8 +153,11 @@ def main():
             rate = f"{f / (t * 1e-3) / 1e12:7.1f} TF/s" if f else f"{b / (t * 1e-3) / 1e9:7.1f} GB/s"
             print(f"[top] step {si:4d} {t:8.3f} ms {rate}  {plan.steps[si].kind:9s} {plan.steps[si].name:18s} "
                   f"{_describe(plan, si)[:110]}", file=sys.stderr)
-    # dominant kernel: the step taking the most time
-    dom = max(per_step, key=per_step.get)
+    # dominant kernel: the step taking the most time; steps within 10% of it count as tied (the three
+    # vocabulary-head GEMMs take the same time) and the earliest of them is reported, so that the choice does
+    # not flip with timing noise
+    t_max = max(per_step.values())
+    dom = min(si for si, t in per_step.items() if t >= 0.9 * t_max)
     f, b = plan.cost(dom)
     st = plan.steps[dom]
     t_dom = per_step[dom]

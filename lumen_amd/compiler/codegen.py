@@ -157,6 +157,7 @@ class Emitter:
         self.row_scalars: dict = {}   # reduction var -> C name of its per-row value
         self.flat_loads: dict = {}    # (arg, fbase) -> element names (vectorized loads)
         self.vec = 1
+        self.given: dict = {}         # var -> fn(idx) -> C name: values the caller computes (a GEMM's sums)
 
     def tmp(self, prefix="t"):
         self.count += 1
@@ -265,6 +266,8 @@ class Emitter:
         return f"(({COMP_T[dtype]})({STORE_T[dtype]})({expr}))"
 
     def _compute(self, var, idx, ty):
+        if var in self.given:
+            return self.given[var](idx)
         if var in self.inputs:
             return self.load(var, idx, ty)
         n = self.prod.get(var)
@@ -618,10 +621,13 @@ class LoopKernel:
             terms.append(f"{e} * {view.strides[d]}LL")
         return "(" + (" + ".join(terms) if terms else "0") + ")"
 
-    def _vec_prologue(self, em, V):
+    def _vec_prologue(self, em, V, inputs=None):
+        """Vector loads of the inputs (``inputs``, by default the step's, in argument order) that ``em`` read
+        at flat ``base + lane`` indices."""
+        inputs = self.step.inputs if inputs is None else inputs
         lines = []
         for (arg, base), names in em.flat_loads.items():
-            dt = self.graph.types[self.step.inputs[arg]].dtype
+            dt = self.graph.types[inputs[arg]].dtype
             esz = D.size_of(dt)
             vt = {2: "u16v", 4: "u32v", 8: "u64v"}.get(esz)
             if vt is None or V * esz not in (4, 8, 16) or esz == 1:
@@ -921,3 +927,98 @@ def _declared(em):
 
 
 _ = (struct, TensorType, VEC_T)
+
+
+class GemmEpilogueKernel:
+    """A streamed GEMM (``gemm_stream_tile`` in gemm.h, 256 x 256 tiles, 8 wavefronts, k steps of 64) whose
+    store is a fused loop step: the loop's elementwise body runs on the dot's sums rounded to the dot's output
+    dtype, at the flat index of each [m, n] element, and writes the loop's outputs (plus the dot's own result
+    when anything else reads it). The dot's lhs/rhs locations give ``a``/``b`` with the layout flags ``at``/``bt``
+    (mn-contiguous operands), as nhip_gemm takes them."""
+
+
+    def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views):
+        self.graph, self.dot, self.loop = graph, dot_step, loop_step
+        self.desc, self.at, self.bt, self.f16, self.store_dot = desc, at, bt, f16, store_dot
+        self.views, self.out_views = views, out_views
+        self.name = "KNAME"
+        d = desc
+        self.grid = (-(-d.m // 256) * -(-d.n // 256), 1, 1)
+        self.block = (512, 1, 1)
+        self.lds = 0
+        self.args = []
+
+    def source(self):
+        g, dot, loop = self.graph, self.dot, self.loop
+        dv = dot.nodes[0].output
+        d = self.desc
+        n = d.n
+        if n % 4:
+            raise Unfusable(dv, "GEMM epilogue over a row length that is not a multiple of 4")
+        ddt = g.types[dv].dtype
+        lin = [v for v in loop.inputs if v != dv]
+        # the loop's body, evaluated 4 columns at a time at flat index base + lane of the [m, n] result
+        lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views)
+        em = Emitter(g, loop.nodes, {v: (k, self.views[v]) for k, v in enumerate(lin)})
+        em.vec = 4
+        accs = [f"acc.{c}" for c in "xyzw"]
+        dnames = []
+        for lane in range(4):
+            nm = em.tmp("d")
+            em.emit(f"const float {nm} = {em.round(accs[lane], ddt) if ddt != 'float32' else accs[lane]};")
+            dnames.append(nm)
+
+        def given(idx):
+            if idx[0] == "flat" and len(idx) == 4 and idx[2] == "base":
+                return dnames[idx[3]]
+            raise Unfusable(dv, "the fused loop reads the dot's result at another index")
+
+        em.given[dv] = given
+        per_lane = []
+        for lane in range(4):
+            idx = ("flat", f"(base + {lane})", "base", lane)
+            per_lane.append([em.value(v, idx) for v in loop.outputs])
+        body = em.lines
+        pro = lk._vec_prologue(em, 4, lin)
+        stores = []
+        outs = ([dv] if self.store_dot else []) + list(loop.outputs)
+        for k, v in enumerate(outs):
+            dt = g.types[v].dtype
+            names = dnames if (self.store_dot and k == 0) else [per_lane[l][k - (1 if self.store_dot else 0)] for l in range(4)]
+            view = self.out_views[v]
+            if view.contiguous():
+                stores.append(lk._vec_store(f"out{k}", "base", names, dt, 4))
+            else:
+                for lane in range(4):
+                    addr = lk._out_addr(view, g.types[v].shape, f"(base + {lane})")
+                    stores.append(f"out{k}[{addr}] = {_store(names[lane], dt)};")
+        self.args = [("in", dot.nodes[0].inputs[0]), ("in", dot.nodes[0].inputs[1])]
+        self.args += [("in", v) for v in lin] + [("out", v) for v in outs]
+        fields = [f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k};" for k, v in enumerate(lin)]
+        fields += [f"{STORE_T[g.types[v].dtype]}* __restrict__ out{k};" for k, v in enumerate(outs)]
+        params = ["const uint16_t* __restrict__ a", "const uint16_t* __restrict__ b"]
+        params += [f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k}" for k, v in enumerate(lin)]
+        params += [f"{STORE_T[g.types[v].dtype]}* __restrict__ out{k}" for k, v in enumerate(outs)]
+        init = ", ".join([f"in{k}" for k in range(len(lin))] + [f"out{k}" for k in range(len(outs))])
+        shape = (f"s.m = {d.m}LL; s.n = {d.n}LL; s.k = {d.k}LL; s.nbatch = 0; s.a_m = {d.a_m}LL; "
+                 f"s.a_k = {d.a_k}LL; s.b_k = {d.b_k}LL; s.b_n = {d.b_n}LL; s.d_m = {d.n}LL; s.d_n = 1; "
+                 f"s.tiles_m = {-(-d.m // 256)}; s.tiles_n = {-(-d.n // 256)}; s.d_split = 0;")
+        lines = [
+            '#include "gemm.h"',
+            "struct EpiKNAME {",
+            *["  " + f for f in fields],
+            "  __device__ __forceinline__ void operator()(int64_t r, int64_t c, float4 acc) const {",
+            f"    const int64_t base = r * {n}LL + c;",
+            *["    " + l for l in pro + body + stores],
+            "  }",
+            "};",
+            f'extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) '
+            f'void KNAME({", ".join(params)}) {{',
+            "  __shared__ __align__(1024) char smem[nhipk::gemm_stream_lds_bytes<64, 4>()];",
+            "  nhipk::GemmShape s;",
+            f"  {shape}",
+            f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, 64, 4, {'true' if self.at else 'false'}, "
+            f"{'true' if self.bt else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
+            "}",
+        ]
+        return "\n".join(lines)

@@ -162,6 +162,8 @@ class Plan:
                 self.packed.add(n.output)
         self.steps = self._fuse()
         self._place()
+        if config.compiler.fuse and config.compiler.epilogue_fusion and self._fuse_epilogues():
+            self._place()
         self.kernels = {}
         self.sources = {}
         self._native = None
@@ -179,6 +181,12 @@ class Plan:
     # ---- placement
     def _place(self):
         g = self.graph
+        # placement may run again after a pass merges steps: start from the graph's own steps
+        self.steps = [st for st in self.steps if st.kind != "copy"]
+        self._copies = {}
+        for st in self.steps:
+            if st.kind == "alias":
+                st.kind = "loop"
         self.loc: dict[int, Loc] = {}
         self.scratch: dict[int, Loc] = {}
         for i, v in enumerate(g.inputs):
@@ -270,7 +278,7 @@ class Plan:
                 live[v] = (off, size)
                 self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
             if st.kind == "dot":
-                st.splits = self._split_count(st.nodes[0])
+                st.splits = 1 if getattr(st, "epi", None) is not None else self._split_count(st.nodes[0])
                 if st.splits > 1:
                     d, _ = self._gemm_desc(st.nodes[0])
                     st.scratch = st.splits * max(1, math.prod(d.batch[i] for i in range(d.nbatch))) * d.m * d.n * 4
@@ -294,10 +302,93 @@ class Plan:
                 self.workspace_bytes += -(-t.nbytes() // ALIGNMENT) * ALIGNMENT
                 dst = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
                 self.steps.append(fusion.Step("copy", [], [v], [v]))
-                self._copies = getattr(self, "_copies", {})
                 self._copies[len(self.steps) - 1] = (loc, dst)
                 loc = dst
             self.output_locs.append(loc)
+
+    # ---- GEMM epilogues (lumen/graph_compiler/passes/fusion/mod.rs:20-112, the CUDA backend's `epilogue`):
+    # a loop step that reads a dot's [m, n] result element for element runs inside the dot's store
+    def _epilogue_layout(self, st):
+        """``(desc, at, bt, f16)`` when dot step ``st`` can run as a streamed GEMM with a generated epilogue
+        (2-D bf16/f16 operands, k a multiple of 64, one k split, operand rows 16-byte aligned), else None."""
+        from lumen_amd import native as nv
+
+        n = st.nodes[0]
+        p = n.params
+        if p["lhs_batch"] or p["rhs_batch"] or getattr(st, "splits", 1) > 1:
+            return None
+        if len(self.graph.types[n.output].shape) != 2 or self.loc[n.output].strides != _contig(self.graph.types[n.output].shape):
+            return None
+        try:
+            d, ops = self._gemm_desc(n)
+        except NotImplementedError:
+            return None
+        if d.a_dtype != d.b_dtype or d.a_dtype not in (nv.NHIP_BF16, nv.NHIP_F16) or d.k % 64 or d.n % 4:
+            return None
+        if d.a_k == 1 and d.a_m % 8 == 0:
+            at = False
+        elif d.a_m == 1 and d.m % 8 == 0 and d.a_k % 8 == 0:
+            at = True
+        else:
+            return None
+        if d.b_k == 1 and d.b_n % 8 == 0:
+            bt = False
+        elif d.b_n == 1 and d.n % 8 == 0 and d.b_k % 8 == 0:
+            bt = True
+        else:
+            return None
+        if any((loc.offset * D.size_of(loc.dtype)) % 16 for loc in ops[:2]):
+            return None
+        return d, at, bt, d.a_dtype == nv.NHIP_F16
+
+    def _fuse_epilogues(self):
+        """Merges each loop step that is the elementwise consumer of a dot's [m, n] result into the dot's step
+        (``st.epi``); returns whether any was merged. The loop's other inputs must exist before the dot runs;
+        the dot's result is still stored when other steps or the graph's outputs read it."""
+        from lumen_amd.graph.ir import ELEMENTWISE
+
+        g = self.graph
+        pos = {}
+        users: dict[int, list] = {}
+        for si, st in enumerate(self.steps):
+            for v in st.outputs:
+                pos[v] = si
+            for u in st.inputs:
+                users.setdefault(u, []).append(si)
+        outputs = set(g.outputs)
+        merged = set()
+        for si, st in enumerate(self.steps):
+            if st.kind != "dot" or getattr(st, "epi", None) is not None:
+                continue
+            dv = st.nodes[0].output
+            lay = self._epilogue_layout(st)
+            if lay is None:
+                continue
+            shape = g.types[dv].shape
+            for li in users.get(dv, []):
+                lt = self.steps[li]
+                if li in merged or lt.kind != "loop" or li <= si:
+                    continue
+                if any(g.types[v].shape != shape or not self.loc[v].view().contiguous() for v in lt.outputs):
+                    continue
+                readers = [n for n in lt.nodes if dv in n.inputs]
+                if any(n.prim not in ELEMENTWISE or g.types[n.output].shape != shape for n in readers):
+                    continue
+                if any(u != dv and pos.get(u, -1) >= si for u in lt.inputs):
+                    continue  # an operand the loop reads is made after the dot
+                keep = dv in outputs or any(x != li for x in users.get(dv, []))
+                st.epi = lt
+                st.epi_layout = lay
+                st.store_dot = keep
+                st.outputs = ([dv] if keep else []) + list(lt.outputs)
+                st.inputs = list(st.inputs) + [u for u in lt.inputs if u != dv and u not in st.inputs]
+                st.nodes = list(st.nodes) + list(lt.nodes)
+                merged.add(li)
+                break
+        if not merged:
+            return False
+        self.steps = [st for i, st in enumerate(self.steps) if i not in merged]
+        return True
 
     # the producers that may write an operand of a concatenation in place, through a strided view
     ALIAS_PRODUCERS = ("flash_fwd", "flash_bwd", "dot", "loop")
@@ -366,6 +457,19 @@ class Plan:
                 k = codegen.HorizontalKernel(parts)
                 body = k.source()
                 name = f"hloop_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
+                k.name = st.name = name
+                self.kernels[si] = k
+                self.sources[si] = codegen.HEADER + body.replace("KNAME", name)
+                continue
+            if st.kind == "dot" and getattr(st, "epi", None) is not None:
+                d, at, bt, f16 = st.epi_layout
+                d, _ = self._gemm_desc(st.nodes[0])
+                lin = [v for v in st.epi.inputs if v != st.nodes[0].output]
+                views = {v: self.loc[v].view() for v in lin}
+                outs = {v: self.loc[v].view() for v in st.outputs}
+                k = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs)
+                body = k.source()
+                name = f"gemm_epi_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
                 k.name = st.name = name
                 self.kernels[si] = k
                 self.sources[si] = codegen.HEADER + body.replace("KNAME", name)
@@ -449,7 +553,8 @@ class Plan:
                     desc = struct.pack("<Q", nbytes)
                     rr = (nv.Reloc * 2)(reloc(0, out), reloc(1, arg))
                     call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_COPY, desc, len(desc), rr, 2)
-            if st.kind in ("loop", "row", "reduce", "scatter_add", "hloop"):
+            if st.kind in ("loop", "row", "reduce", "scatter_add", "hloop") or (
+                    st.kind == "dot" and getattr(st, "epi", None) is not None):
                 k = self.kernels[si]
                 fn = nv.module_function(self.objects[si], k.name)
                 if st.kind == "reduce" and getattr(k, "atomic", False):
@@ -496,7 +601,9 @@ class Plan:
         g = self.graph
         p = n.params
         lhs, rhs = self.loc[n.inputs[0]], self.loc[n.inputs[1]]
-        out = self.loc[n.output]
+        ot = g.types[n.output]
+        # a dot whose result only feeds its fused epilogue has no location of its own: rows are n apart
+        out = self.loc.get(n.output) or Loc(("ws", 0), 0, _contig(ot.shape), ot.dtype, ot.shape)
         lt, rt = g.types[n.inputs[0]], g.types[n.inputs[1]]
         lc, rc, lb, rb = p["lhs_contracting"], p["rhs_contracting"], p["lhs_batch"], p["rhs_batch"]
         lf = [d for d in range(len(lt.shape)) if d not in lc and d not in lb]
@@ -559,7 +666,7 @@ class Plan:
         nv.call("nhip_gemm_config_count", C.byref(n_cfg))
         ev0, ev1 = nv.Event(), nv.Event()
         for st in self.steps:
-            if st.kind != "dot" or getattr(st, "splits", 1) > 1:
+            if st.kind != "dot" or getattr(st, "splits", 1) > 1 or getattr(st, "epi", None) is not None:
                 continue
             try:
                 d, ops = self._gemm_desc(st.nodes[0])

@@ -358,9 +358,60 @@ constexpr int gemm_stream_lds_bytes() {
     return 128 * 1024 > 2 * WN * 64 * gemm_stream_stage_pitch<WN>() ? 128 * 1024 : 2 * WN * 64 * gemm_stream_stage_pitch<WN>();
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT>
-__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
-    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
+// Writes rows [rbase, rbase + 64) x columns [cbase, cbase + WCOLS) of D from a wave's float32 staging rows
+// (`PITCH` bytes apart): 16-byte stores when D is row-contiguous and aligned, else element by element through
+// the strided store.
+template <int WCOLS, int PITCH>
+__device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyStore &out, int64_t od, const char *stage,
+                                                  int64_t rbase, int64_t cbase, int lane) {
+    const int esize = out.dtype == 0 ? 4 : 2;
+    const bool vec = s.d_n == 1 && s.n % 8 == 0 && s.d_m % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(out.d) + od * esize) & 15) == 0;
+    char *dbase = static_cast<char *>(out.d) + od * esize;
+    if (vec) {
+        const int epc = 16 / esize;            // output elements a 16-byte chunk
+        const int cpr = WCOLS / epc;           // chunks a row
+        for (int idx = lane; idx < 64 * cpr; idx += 64) {
+            const int r = idx / cpr, ch = idx % cpr;
+            const int64_t gr = rbase + r, gc = cbase + ch * epc;
+            if (gr >= s.m || gc >= s.n) continue;
+            const float *src = reinterpret_cast<const float *>(stage + r * PITCH) + ch * epc;
+            uint4 v;
+            if (out.dtype == 0) {
+                v = *reinterpret_cast<const uint4 *>(src);
+            } else {
+                const float4 x = *reinterpret_cast<const float4 *>(src);
+                const float4 y = *reinterpret_cast<const float4 *>(src + 4);
+                if (out.dtype == 1)
+                    v = make_uint4(uint32_t(f32_to_bf16(x.x)) | (uint32_t(f32_to_bf16(x.y)) << 16),
+                                   uint32_t(f32_to_bf16(x.z)) | (uint32_t(f32_to_bf16(x.w)) << 16),
+                                   uint32_t(f32_to_bf16(y.x)) | (uint32_t(f32_to_bf16(y.y)) << 16),
+                                   uint32_t(f32_to_bf16(y.z)) | (uint32_t(f32_to_bf16(y.w)) << 16));
+                else
+                    v = make_uint4(uint32_t(f32_to_f16(x.x)) | (uint32_t(f32_to_f16(x.y)) << 16),
+                                   uint32_t(f32_to_f16(x.z)) | (uint32_t(f32_to_f16(x.w)) << 16),
+                                   uint32_t(f32_to_f16(y.x)) | (uint32_t(f32_to_f16(y.y)) << 16),
+                                   uint32_t(f32_to_f16(y.z)) | (uint32_t(f32_to_f16(y.w)) << 16));
+            }
+            *reinterpret_cast<uint4 *>(dbase + (gr * s.d_m + gc) * esize) = v;
+        }
+    } else {
+        out.visit([&](auto stf) {
+            for (int idx = lane; idx < 64 * WCOLS; idx += 64) {
+                const int r = idx / WCOLS, c = idx % WCOLS;
+                const int64_t gr = rbase + r, gc = cbase + c;
+                if (gr < s.m && gc < s.n) stf(s, od, gr, gc, *reinterpret_cast<const float *>(stage + r * PITCH + c * 4));
+            }
+        });
+    }
+}
+
+// One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
+// functor called as out(row, col, float4) with the float32 sums of four consecutive columns (col a multiple
+// of 4; columns at or past n are the functor's to skip). `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
+template <bool F16, int BK, int WN, bool AT, bool BT, class Out>
+__device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
+                                                 const uint16_t *__restrict__ b, const Out &out, char *smem) {
     constexpr int NW = 2 * WN;       // wavefronts
     constexpr int FN = 8 / WN;       // 32-column MFMA tiles a wave
     constexpr int WCOLS = 32 * FN;   // columns a wave
@@ -370,7 +421,6 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     constexpr int STAGE_BYTES = TA::bytes + TB::bytes;
     constexpr int LPS = (TA::segs + TB::segs) / NW;  // load instructions a wave issues per stage
     constexpr int NRD = (AT ? 8 : 4) + (BT ? 2 * FN : FN);  // LDS read instructions a k step
-    extern __shared__ __align__(1024) char smem[];
 
     int tm, tn;
     tile_of(blockIdx.x, s.tiles_m, s.tiles_n, tm, tn);
@@ -495,16 +545,11 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     }
 
     // acc[i][j][e]: row m0 + wm*128 + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
-    // Staged through LDS as float32, 64 rows of the wave at a time, then written row-wise: 16-byte stores
-    // when D is row-contiguous and aligned, else element by element through the strided store.
+    // Staged through LDS as float32, 64 rows of the wave at a time, then written row-wise.
     const int64_t rbase = m0 + wm * 128, cbase = n0 + wn * WCOLS;
-    const int esize = out.dtype == 0 ? 4 : 2;
-    const bool vec = s.d_n == 1 && s.n % 8 == 0 && s.d_m % 8 == 0 &&
-                     ((reinterpret_cast<uintptr_t>(out.d) + od * esize) & 15) == 0;
     constexpr int PITCH = gemm_stream_stage_pitch<WN>();
     __syncthreads();  // operand stages are dead: reuse LDS for the output
     char *stage = smem + wave * (64 * PITCH);
-    char *dbase = static_cast<char *>(out.d) + od * esize;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
 #pragma unroll
@@ -519,45 +564,25 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
                         make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
         }
         __syncthreads();
-        if (vec) {
-            const int epc = 16 / esize;            // output elements a 16-byte chunk
-            const int cpr = WCOLS / epc;           // chunks a row
-            for (int idx = lane; idx < 64 * cpr; idx += 64) {
-                const int r = idx / cpr, ch = idx % cpr;
-                const int64_t gr = rbase + 64 * half + r, gc = cbase + ch * epc;
-                if (gr >= s.m || gc >= s.n) continue;
-                const float *src = reinterpret_cast<const float *>(stage + r * PITCH) + ch * epc;
-                uint4 v;
-                if (out.dtype == 0) {
-                    v = *reinterpret_cast<const uint4 *>(src);
-                } else {
-                    const float4 x = *reinterpret_cast<const float4 *>(src);
-                    const float4 y = *reinterpret_cast<const float4 *>(src + 4);
-                    if (out.dtype == 1)
-                        v = make_uint4(uint32_t(f32_to_bf16(x.x)) | (uint32_t(f32_to_bf16(x.y)) << 16),
-                                       uint32_t(f32_to_bf16(x.z)) | (uint32_t(f32_to_bf16(x.w)) << 16),
-                                       uint32_t(f32_to_bf16(y.x)) | (uint32_t(f32_to_bf16(y.y)) << 16),
-                                       uint32_t(f32_to_bf16(y.z)) | (uint32_t(f32_to_bf16(y.w)) << 16));
-                    else
-                        v = make_uint4(uint32_t(f32_to_f16(x.x)) | (uint32_t(f32_to_f16(x.y)) << 16),
-                                       uint32_t(f32_to_f16(x.z)) | (uint32_t(f32_to_f16(x.w)) << 16),
-                                       uint32_t(f32_to_f16(y.x)) | (uint32_t(f32_to_f16(y.y)) << 16),
-                                       uint32_t(f32_to_f16(y.z)) | (uint32_t(f32_to_f16(y.w)) << 16));
-                }
-                *reinterpret_cast<uint4 *>(dbase + (gr * s.d_m + gc) * esize) = v;
-            }
+        if constexpr (std::is_same<Out, AnyStore>::value) {
+            stream_store_rows<WCOLS, PITCH>(s, out, od, stage, rbase + 64 * half, cbase, lane);
         } else {
-            out.visit([&](auto stf) {
-                for (int idx = lane; idx < 64 * WCOLS; idx += 64) {
-                    const int r = idx / WCOLS, c = idx % WCOLS;
-                    const int64_t gr = rbase + 64 * half + r, gc = cbase + c;
-                    if (gr < s.m && gc < s.n)
-                        stf(s, od, gr, gc, *reinterpret_cast<const float *>(stage + r * PITCH + c * 4));
-                }
-            });
+            // four consecutive columns a lane, WCOLS / 4 lanes a row
+            for (int idx = lane; idx < 64 * (WCOLS / 4); idx += 64) {
+                const int r = idx / (WCOLS / 4), ch = idx % (WCOLS / 4);
+                const int64_t gr = rbase + 64 * half + r, gc = cbase + 4 * ch;
+                if (gr < s.m && gc < s.n) out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16));
+            }
         }
         __syncthreads();
     }
+}
+
+template <bool F16, int BK, int WN, bool AT, bool BT>
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
+    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
+    extern __shared__ __align__(1024) char smem[];
+    gemm_stream_tile<F16, BK, WN, AT, BT>(s, a, b, out, smem);
 }
 
 // Split-k reduction: D[z, r, c] = sum over splits of the float32 partials P[split][z][r][c] (contiguous,

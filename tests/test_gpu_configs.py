@@ -88,3 +88,43 @@ def test_concatenated_dot_results_written_in_place_match_oracle(hip):
     assert "alias" in [s["kind"] for s in f.plan.describe()]
     (want,) = oracle.values(L.make_graph(fn)(*args), xs)
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+def _epi_fn(x, w, h, b):
+    y = F.matmul(x, w, "float32", "float32")
+    return F.gelu(y) * b + y * h
+
+
+def _epi_fn_keep(x, w, h, b):
+    y = F.matmul(x, w, "float32", "float32")
+    return F.gelu(y) * b + y * h, y
+
+
+@pytest.mark.parametrize("fn", [_epi_fn, _epi_fn_keep])
+@pytest.mark.parametrize("m,n,k", [(512, 512, 256), (1000, 776, 320)])
+def test_gemm_epilogue_matches_oracle_and_unfused_plan(hip, fn, m, n, k):
+    """The dot with its elementwise consumer fused into the GEMM's store (gemm_epi kernel, ragged m and n
+    included) against the oracle (float32: rtol 1e-4 of the largest value, the tolerance for float32
+    results), and bit for bit against the same plan without epilogue fusion (same sums, same body)."""
+    rng = np.random.default_rng(11)
+    x = _bf16(rng.standard_normal((m, k)) * 0.25)
+    w = _bf16(rng.standard_normal((k, n)) * 0.25)
+    h = rng.standard_normal((m, n)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    args = [L.tensor(D.bf16_to_f32(x), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(h),
+            L.from_numpy(b)]
+    with L.config.compiler.patch(horizontal_fusion=False):
+        f = L.compile(fn, device="hip")
+        got = f(*args)
+        got = [np.asarray(L.to_numpy(t), np.float32) for t in (got if isinstance(got, tuple) else (got,))]
+        assert [s["name"][:9] for s in f.plan.describe()] == ["gemm_epi_"]
+    with L.config.compiler.patch(horizontal_fusion=False, epilogue_fusion=False, autotune=False):
+        u = L.compile(fn, device="hip")
+        ref = u(*args)
+        ref = [np.asarray(L.to_numpy(t), np.float32) for t in (ref if isinstance(ref, tuple) else (ref,))]
+        assert "loop" in [s["kind"] for s in u.plan.describe()]
+    want = oracle.values(L.make_graph(fn)(*args), [x, w, h, b])
+    for g_, r_, w_ in zip(got, ref, want):
+        w_ = np.asarray(w_, np.float32)
+        np.testing.assert_allclose(g_, w_, rtol=1e-4, atol=1e-4 * np.abs(w_).max())
+        assert np.array_equal(g_, r_)

@@ -70,6 +70,34 @@ def test_concatenated_dot_results_are_written_in_place():
     assert (desc.d_m, desc.d_n) == (1024, 1)
 
 
+def _epilogue_fn(x, w, h, b):
+    y = F.matmul(x, w, "float32", "float32")
+    return F.gelu(y) * b + y * h
+
+
+def _epilogue_fn_keep(x, w, h, b):
+    y = F.matmul(x, w, "float32", "float32")
+    return F.gelu(y) * b + y * h, y
+
+
+EPI_SHAPES = [((512, 256), "bfloat16"), ((256, 512), "bfloat16"), ((512, 512), "float32"), ((512,), "float32")]
+
+
+@pytest.mark.parametrize("fn,keep", [(_epilogue_fn, False), (_epilogue_fn_keep, True)])
+def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep):
+    """A loop reading a dot's [m, n] result element for element (with other operands: a broadcast row, a
+    same-shape tensor) is merged into the dot: one launch of a generated gemm_epi kernel, which also stores
+    the dot's own result when something else (here a graph output) reads it."""
+    with L.config.compiler.patch(horizontal_fusion=False):
+        p = _plan(fn, *EPI_SHAPES, build=True)
+    assert [s.kind for s in p.steps] == ["dot"]
+    st = p.steps[0]
+    assert st.epi is not None and st.name.startswith("gemm_epi_") and st.store_dot == keep
+    with L.config.compiler.patch(epilogue_fusion=False, horizontal_fusion=False):
+        q = _plan(fn, *EPI_SHAPES)
+    assert [s.kind for s in q.steps] == ["dot", "loop"]
+
+
 def test_one_row_kernel_for_a_normalization_chain():
     p = _plan(lambda x, w: F.softmax(F.rms_norm(x, 256, w) * 3.0, -1), ((32, 256), "float32"), ((256,), "float32"))
     assert [s.kind for s in p.steps] == ["row"]
