@@ -302,7 +302,8 @@ __device__ __forceinline__ float half_to_f32(uint16_t v) {
 // base-2 LSE written once by the delta kernel; masks only on tiles that cross the diagonal or the end of the
 // queries.
 
-// delta = rowsum(dO * O) and lse2 = lse * log2(e), float32 [B, N, Sq] each; one wavefront a query row.
+// delta = rowsum(dO * O) * scale and lse2 = lse * log2(e), float32 [B, N, Sq] each; one wavefront a query
+// row.
 template <int D, bool F16>
 __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *lse2) {
     const int lane = threadIdx.x & 63;
@@ -317,10 +318,13 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *ls
     acc = wave_sum(acc);
     const int64_t i = (b * p.heads + n) * p.sq + q;
     if (lane == 0) {
-        p.delta[i] = acc;
+        p.delta[i] = acc * p.scale;  // delta times the softmax scale: dS = P (dP scale - delta scale)
         lse2[i] = p.lse_in[i] * 1.4426950408889634f;
     }
 }
+
+// Component i (a constant) of a float4.
+__device__ __forceinline__ float f4_at(const float4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // 64 floats [k0, k0 + 64) of `src` (clamped to `rows`) into LDS by one wavefront.
 __device__ __forceinline__ void load_row64_async(const float *src, int64_t k0, int64_t rows, float *dst, int lane) {
@@ -337,7 +341,8 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
     constexpr int DS = D / 16, DT = D / 32;
     constexpr int TILE = BM * D;
     __shared__ __align__(1024) uint16_t smem[4 * TILE];  // Q0 dO0 Q1 dO1
-    __shared__ float Ls[2][BM], Dl[2][BM];
+    __shared__ __align__(16) float Ls[2][BM];
+    __shared__ __align__(16) float Dl[2][BM];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
@@ -454,6 +459,14 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
             for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
+                    // the rows' base-2 LSE and scaled delta, four consecutive rows a 16-byte LDS read
+                    float4 l4[2], d4[2];
+#pragma unroll
+                    for (int j4 = 0; j4 < 2; ++j4) {
+                        const int r4 = 32 * qs + 8 * (2 * half + j4) + 4 * h;
+                        l4[j4] = *reinterpret_cast<const float4 *>(Lt + r4);
+                        d4[j4] = *reinterpret_cast<const float4 *>(Dt + r4);
+                    }
                     uint32_t wp[4], ws[4];
 #pragma unroll
                     for (int jj = 0; jj < 8; jj += 2) {
@@ -462,10 +475,12 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                         for (int u = 0; u < 2; ++u) {
                             const int e = 8 * half + jj + u;
                             const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
-                            float pe = fast_exp2(fmaf(sv[qs][e], c2, -Lt[r]));
+                            const float lr = f4_at(l4[(jj + u) / 4], (jj + u) % 4);
+                            const float dr = f4_at(d4[(jj + u) / 4], (jj + u) % 4);
+                            float pe = fast_exp2(fmaf(sv[qs][e], c2, -lr));
                             if constexpr (MASKED) pe = ((r >= rmin) & (r < rmax)) ? pe : 0.0f;
                             pv[u] = pe;
-                            dv2[u] = pe * (dp[qs][e] - Dt[r]) * p.scale;
+                            dv2[u] = pe * fmaf(dp[qs][e], p.scale, -dr);
                         }
                         wp[jj / 2] = pack2<F16>(pv[0], pv[1]);
                         ws[jj / 2] = pack2<F16>(dv2[0], dv2[1]);
@@ -626,7 +641,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
                             const int kk = 32 * ks + 8 * (e / 4) + (e % 4);
                             pe = (qvalid && kk <= lim) ? pe : 0.0f;
                         }
-                        ds2[u] = pe * (dp[e] - dl) * p.scale;
+                        ds2[u] = pe * fmaf(dp[e], p.scale, -dl);
                     }
                     w[jj / 2] = pack2<F16>(ds2[0], ds2[1]);
                 }
