@@ -14,6 +14,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libnhip.so")
 SOURCES = ["runtime.cpp", "kernels.hip", "attention.hip"]
+# Per-source flags. The flash backward's dK/dV kernel holds ~330 registers (one wave a SIMD); with MFMA
+# results in VGPRs the allocator keeps the K/V operands in AGPRs instead of shuttling the dK/dV accumulators
+# between AGPRs and VGPRs on every tile.
+EXTRA = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -40,7 +44,7 @@ def build(verbose=False):
     for src in SOURCES:  # one translation unit a process, in parallel
         obj = os.path.join(objdir, src + ".o")
         objs.append(obj)
-        cmd = [hipcc()] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [hipcc()] + FLAGS + EXTRA.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj]
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
     errors = []
     for src, p in procs:
