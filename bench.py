@@ -70,7 +70,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="5", choices=["4", "5", "tiny"])
+    ap.add_argument("--config", default="5", choices=["1", "2", "3", "4", "5", "tiny"],
+                    help="4, 5, tiny: the training step; 1, 2, 3: the single-op configurations (relu(matmul) f32, "
+                         "the fused elementwise/norm/softmax chain, flash attention forward + backward)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     ap.add_argument("--probe", action="store_true",
@@ -91,6 +93,11 @@ def main():
     from lumen_amd import native
     from lumen_amd import workloads as W
 
+    if args.config in ("1", "2", "3"):
+        native.set_device(0)
+        out = OP_CONFIGS[args.config](args)
+        print(json.dumps(out), flush=True)
+        return
     cfg = {"4": W.CONFIG4, "5": W.CONFIG5, "tiny": W.TINY}[args.config]
     native.set_device(0)
     model, opt = W.build(cfg, lr=1e-2)
@@ -213,6 +220,245 @@ def main():
     del np
 
 
+# ---- single-op configurations (SURVEY-style configs 1-3): one compiled call (or C-ABI call) is a step
+
+
+def _op_line(args, metric, ms, unit_value, unit, config, roof, cpu, dtype, extra=None):
+    out = {
+        "metric": metric, "value": round(unit_value, 3), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": unit != "ms/step",
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic (numpy default_rng, seeded)",
+        "config": config, "roofline": roof,
+    }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    out.update(extra or {})
+    return out
+
+
+def _time_calls(fn, steps, warmup):
+    from lumen_amd import native
+    for _ in range(warmup):
+        fn()
+    native.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    native.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def _plan_kernel_ms(f, call, reps=5):
+    """Average HIP-event time of each plan step over ``reps`` profiled calls: {step index: ms}."""
+    plan = f.plan
+    plan.profile(True)
+    per = {}
+    for _ in range(reps):
+        call()
+        for si, t in plan.step_ms():
+            per[si] = per.get(si, 0.0) + t / reps
+    plan.profile(False)
+    return per
+
+
+def _config1(args):
+    """relu(matmul(x, w)) in float32, x [256, 512], w [512, 1024]: the reference's bit-exact float32 fold
+    (gemm_exact, VALU)."""
+    import numpy as np
+
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((256, 512)).astype(np.float32)
+    w = rng.standard_normal((512, 1024)).astype(np.float32)
+    fn = lambda x, w: F.relu(F.matmul(x, w, "float32", "float32"))  # noqa: E731
+    xd, wd = L.from_numpy(x).to("hip"), L.from_numpy(w).to("hip")
+    f = L.compile(fn, device="hip")
+    f(xd, wd)
+    ms = _time_calls(lambda: f(xd, wd), args.steps, args.warmup)
+    per = _plan_kernel_ms(f, lambda: f(xd, wd))
+    dom = max(per, key=per.get)
+    flops = 2 * 256 * 512 * 1024
+    k_ms = per[dom]
+    roof = {"bound": "valu", "achieved": round(flops / (k_ms * 1e-3) / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
+            "frac": round(flops / (k_ms * 1e-3) / 1e12 / 157.3, 4), "traffic": None,
+            "kernel": f"{f.plan.steps[dom].kind} step {dom}: gemm_exact relu(matmul) f32 (sequential-k fold)",
+            "per_launch": {"flops": flops, "bytes": 3670016, "ms": round(k_ms, 4)}}
+    cpu = None
+    if not args.no_cpu:
+        g = L.make_graph(fn)(L.from_numpy(x), L.from_numpy(w))
+        t = time.perf_counter()
+        oracle.run(g, [x, w])
+        c = time.perf_counter() - t
+        cpu = {"value": round(c * 1e3, 1), "unit": "ms/call", "cores": 1, "kind": "port",
+               "sample": "the whole config-1 call in the C oracle (1 thread)"}
+    return _op_line(args, "config1 relu(matmul) f32 call time", ms, ms, "ms/step",
+                    {"workload": "config1: relu(x[256,512] @ w[512,1024]) float32, bit-exact fold"}, roof, cpu, "f32",
+                    {"kernel_ms": round(k_ms, 4)})
+
+
+def _config2(args):
+    """The fused chain t = x*a+b (bf16) -> f32 -> gelu_tanh -> layernorm -> softmax -> bf16 over x [8192, 4096]:
+    one row kernel, HBM-bound (134.2 MB algorithmic a call)."""
+    import numpy as np
+
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from lumen_amd import dtypes as D
+    from oracle import oracle
+
+    def chain(x, a, b):
+        t = (x * a + b).float()
+        t = F.gelu(t)
+        t = F.layer_norm(t, x.shape[-1])
+        return F.softmax(t, -1).bfloat16()
+
+    rows, cols = 8192, 4096
+    rng = np.random.default_rng(0)
+    x = D.bf16_bits(rng.standard_normal((rows, cols)).astype(np.float32))
+    a = D.bf16_bits((1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32))
+    b = D.bf16_bits((0.1 * rng.standard_normal(cols)).astype(np.float32))
+    # rotate 4 copies of x so that consecutive calls do not hit in L2/MALL (32 MiB of L2 + 256 MiB MALL)
+    xs = [L.tensor(D.bf16_to_f32(np.roll(x, i, axis=0)), "bfloat16").to("hip") for i in range(4)]
+    ad = L.tensor(D.bf16_to_f32(a), "bfloat16").to("hip")
+    bd = L.tensor(D.bf16_to_f32(b), "bfloat16").to("hip")
+    f = L.compile(chain, device="hip")
+    f(xs[0], ad, bd)
+    it = [0]
+
+    def call():
+        it[0] += 1
+        return f(xs[it[0] % 4], ad, bd)
+
+    ms = _time_calls(call, args.steps, args.warmup)
+    per = _plan_kernel_ms(f, call)
+    dom = max(per, key=per.get)
+    nbytes = 2 * rows * cols * 2 + 2 * cols * 2
+    k_ms = sum(per.values())
+    gbs = nbytes / (per[dom] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
+            "traffic": None, "kernel": f"{f.plan.steps[dom].kind} step {dom}: {f.plan.steps[dom].label()}",
+            "per_launch": {"flops": 0, "bytes": nbytes, "ms": round(per[dom], 4)}}
+    cpu = None
+    if not args.no_cpu:
+        r = 64
+        g = L.make_graph(chain)(*[L.empty(s, "bfloat16", "meta") for s in ([r, cols], [cols], [cols])])
+        t = time.perf_counter()
+        oracle.run(g, [x[:r], a, b])
+        c = (time.perf_counter() - t) * rows / r
+        cpu = {"value": round(c * 1e3, 1), "unit": "ms/call", "cores": 1, "kind": "port",
+               "sample": f"{r} of the {rows} rows in the C oracle (1 thread), scaled by rows"}
+    return _op_line(args, "config2 fused chain GB/s", ms, nbytes / (ms * 1e-3) / 1e9, "GB/s",
+                    {"workload": "config2: gelu_tanh -> layernorm -> softmax over x*a+b, x [8192,4096] bf16"},
+                    roof, cpu, "f32", {"kernel_ms": round(k_ms, 4), "launches": len(per)})
+
+
+def _config3(args):
+    """Flash attention forward + backward, causal, Q/K/V/dO [8, 2048, 16, 128] bf16 through the C ABI
+    (nhip_flash_fwd, nhip_flash_bwd): 137.4 GFLOP forward + 343.6 GFLOP backward (2.5x) a step."""
+    import ctypes as C
+    import math
+
+    import numpy as np
+
+    from lumen_amd import native as nv
+
+    b, s, n, d = 8, 2048, 16, 128
+    rng = np.random.default_rng(0)
+    from lumen_amd.tensor import DeviceBuffer
+
+    nbytes = b * s * n * d * 2
+
+    def mk():
+        h = (rng.standard_normal((b, s, n, d)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        buf = DeviceBuffer(0, nbytes)
+        nv.h2d(buf.ptr, h.ctypes.data, nbytes)
+        return buf
+
+    q, k, v, do = mk(), mk(), mk(), mk()
+    o, dq, dk, dv = (DeviceBuffer(0, nbytes) for _ in range(4))
+    lse = DeviceBuffer(0, b * n * s * 4)
+    desc = nv.AttnDesc()
+    desc.batch, desc.heads, desc.kv_heads, desc.sq, desc.sk, desc.head_dim = b, n, n, s, s, d
+    desc.dtype, desc.causal, desc.scale, desc.config = 1, 1, 1.0 / math.sqrt(d), -1
+    desc.q_b, desc.q_s, desc.q_n = s * n * d, n * d, d
+    for nm in ("k", "v", "o", "do", "dq", "dk", "dv"):
+        setattr(desc, f"{nm}_b", s * n * d)
+        setattr(desc, f"{nm}_s", n * d)
+        setattr(desc, f"{nm}_n", d)
+    wsz = C.c_size_t()
+    nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(wsz))
+    ws = DeviceBuffer(0, wsz.value)
+
+    def fwd():
+        nv.call("nhip_flash_fwd", C.byref(desc), q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr)
+
+    def bwd():
+        nv.call("nhip_flash_bwd", C.byref(desc), q.ptr, k.ptr, v.ptr, o.ptr, do.ptr, lse.ptr, dq.ptr, dk.ptr,
+                dv.ptr, ws.ptr)
+
+    ev = [nv.Event() for _ in range(3)]
+    fwd()
+    bwd()
+    nv.sync()
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    ev[0].record()
+    for _ in range(args.steps):
+        fwd()
+    ev[1].record()
+    for _ in range(args.steps):
+        bwd()
+    ev[2].record()
+    nv.sync()
+    f_ms = ev[0].elapsed_ms(ev[1]) / args.steps
+    b_ms = ev[1].elapsed_ms(ev[2]) / args.steps
+    ff = 2.0 * b * n * s * s * d
+    bf = 2.5 * ff
+    tf = (ff + bf) / ((f_ms + b_ms) * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4),
+            "traffic": None, "kernel": "flash attention forward + backward (flash_fwd, flash_prep, flash_dkdv, flash_dq)",
+            "per_launch": {"flops": ff + bf, "bytes": 6 * nbytes + 2 * b * n * s * 4, "ms": round(f_ms + b_ms, 4)}}
+    cpu = None
+    if not args.no_cpu:
+        cpu = _attn_cpu(b, s, n, d)
+    return _op_line(args, "config3 flash attention fwd+bwd TFLOP/s", f_ms + b_ms, tf, "TFLOP/s",
+                    {"workload": "config3: causal flash attention fwd+bwd, [8,2048,16,128] bf16"}, roof, cpu, "bf16",
+                    {"fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+                     "fwd_tflops": round(ff / (f_ms * 1e-3) / 1e12, 1),
+                     "bwd_tflops": round(bf / (b_ms * 1e-3) / 1e12, 1)})
+
+
+def _attn_cpu(b, s, n, d, sl=256):
+    """The oracle on one (batch, head) slice of ``sl`` queries and keys of the traced causal attention
+    forward (the unfused primitives F.flash_attention lowers to), scaled by (s / sl)^2 x b x n and by 3.5
+    for forward + backward (the backward is 2.5x the forward's work)."""
+    import numpy as np
+
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from lumen_amd import dtypes as D
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    xs = [D.bf16_bits(rng.standard_normal((1, sl, 1, d)).astype(np.float32)) for _ in range(3)]
+    g = L.make_graph(lambda q, k, v: F.flash_attention(q, k, v, is_causal=True))(
+        *[L.empty([1, sl, 1, d], "bfloat16", "meta") for _ in range(3)])
+    t = time.perf_counter()
+    oracle.run(g, xs)
+    c = time.perf_counter() - t
+    scale = (s / sl) ** 2 * b * n * 3.5
+    return {"value": round(c * scale * 1e3, 1), "unit": "ms/call", "cores": 1, "kind": "port",
+            "sample": f"one head, {sl} queries x {sl} keys of the causal attention forward (unfused primitives) "
+                      f"in the C oracle (1 thread), scaled by (S/{sl})^2 x B x N and x3.5 for forward + backward"}
+
+
+OP_CONFIGS = {"1": _config1, "2": _config2, "3": _config3}
+
+
 def _traffic(kernel, config):
     """HBM bytes per launch of the dominant kernel, measured by rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of
     ``bench.py --probe`` and scaled by the same counters' reading for a 1 GiB copy (profiles/traffic.json);
@@ -222,8 +468,9 @@ def _traffic(kernel, config):
         return None
     with open(path) as f:
         rec = json.load(f)
+    key = kernel.split(": ", 1)[-1]  # the step index moves when the plan changes; the kernel does not
     for r in rec:
-        if r.get("config") == config and r.get("kernel") == kernel:
+        if r.get("config") == config and r.get("kernel", "").split(": ", 1)[-1] == key:
             return r["traffic"]
     return None
 

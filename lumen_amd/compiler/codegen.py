@@ -409,6 +409,18 @@ class Emitter:
             dims = n.params["broadcast_dimensions"]
             if idx[0] in ("rc",) and self._row_broadcast(src, ty, dims):
                 return self.value(n.inputs[0], ("r", idx[1]))
+            lead = len(ty.shape) - len(src.shape)
+            if src.shape and tuple(dims) == tuple(range(lead, len(ty.shape))) and tuple(src.shape) == tuple(ty.shape[lead:]):
+                # only leading axes are added: the operand's flat index is the trailing part of the output's, and
+                # a vector of consecutive output elements reads consecutive operand elements
+                sn = math.prod(src.shape)
+                if idx[0] == "rc" and self.rows and sn == self.rows[1]:
+                    if len(idx) == 5:
+                        return self.value(n.inputs[0], ("flat", f"({idx[3]} + {idx[4]})", idx[3], idx[4]))
+                    return self.value(n.inputs[0], ("flat", idx[2]))
+                if idx[0] == "flat" and len(idx) == 4 and sn % max(1, self.vec) == 0:
+                    sb = f"(({idx[2]}) % {sn}LL)"
+                    return self.value(n.inputs[0], ("flat", f"({sb} + {idx[3]})", sb, idx[3]))
             m = self.multi(idx, ty.shape)
             sm = [("0" if src.shape[i] == 1 else m[d]) for i, d in enumerate(dims)]
             return self.value(n.inputs[0], ("multi", tuple(sm)))
