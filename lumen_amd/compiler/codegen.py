@@ -960,6 +960,14 @@ class GemmEpilogueKernel:
         self.lds = 0
         self.args = []
 
+    def buffer_ok(self):
+        """gemm.h's stream_buffer_ok: the operand bytes a 256 x 256 tile spans fit 32-bit buffer offsets."""
+        d = self.desc
+        lim = 1 << 31
+        ab = ((d.k - 1) * d.a_k + 256) * 2 if self.at else (255 * d.a_m + d.k) * 2
+        bb = ((d.k - 1) * d.b_k + 256) * 2 if self.bt else (255 * d.b_n + d.k) * 2
+        return ab < lim and bb < lim
+
     def source(self):
         g, dot, loop = self.graph, self.dot, self.loop
         dv = dot.nodes[0].output
@@ -1030,7 +1038,7 @@ class GemmEpilogueKernel:
             "  nhipk::GemmShape s;",
             f"  {shape}",
             f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, 64, 4, {'true' if self.at else 'false'}, "
-            f"{'true' if self.bt else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
+            f"{'true' if self.bt else 'false'}, {'true' if self.buffer_ok() else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
             "}",
         ]
         return "\n".join(lines)

@@ -409,7 +409,7 @@ __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyS
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
 // functor called as out(row, col, float4) with the float32 sums of four consecutive columns (col a multiple
 // of 4; columns at or past n are the functor's to skip). `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
-template <bool F16, int BK, int WN, bool AT, bool BT, class Out>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
     constexpr int NW = 2 * WN;       // wavefronts
@@ -436,6 +436,18 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     const int ktiles = int(s.k / BK);
 
     // issues this wave's loads [lo, hi) of tile kt into stage st (A segments first, then B)
+    // Buffer resources over this tile's rows of A and B (columns when mn-contiguous): the loads then take a
+    // per-lane 32-bit offset fixed for the whole k loop plus a uniform k offset, with no per-load address
+    // arithmetic, and rows past m / n read zeros. Operands whose tile span exceeds 2^31 bytes use 64-bit
+    // global addresses instead.
+    const int64_t mrem = s.m - m0 < 256 ? s.m - m0 : 256, nrem = s.n - n0 < 256 ? s.n - n0 : 256;
+    const int64_t abytes = AT ? ((s.k - 1) * s.a_k + mrem) * 2 : ((mrem - 1) * s.a_m + s.k) * 2;
+    const int64_t bbytes = BT ? ((s.k - 1) * s.b_k + nrem) * 2 : ((nrem - 1) * s.b_n + s.k) * 2;
+    constexpr bool buf = BUF;  // the launcher checked stream_buffer_ok()
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(AT ? pa + m0 : pa + m0 * s.a_m), (short)0, int(abytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(BT ? pb + n0 : pb + n0 * s.b_n), (short)0, int(bbytes), 0x00020000);
     auto issue = [&](int st, int kt, int lo, int hi) {
         char *base = smem + st * STAGE_BYTES;
         const int64_t k0 = int64_t(kt) * BK;
@@ -444,6 +456,13 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             if (i < lo || i >= hi) continue;
             const int seg = wave + NW * i;
             const int line = seg * TA::lines_per_seg + lane / TA::chunks, c = lane % TA::chunks;
+            if constexpr (buf) {
+                const uint32_t vo = AT ? uint32_t((line * s.a_k + ((c ^ mnmaj_swz(line)) << 3)) * 2)
+                                       : uint32_t((line * s.a_m + ((c ^ kmaj_swz<BK>(line)) << 3)) * 2);
+                const uint32_t so = AT ? uint32_t(k0 * s.a_k * 2) : uint32_t(k0 * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (glds_void_t *)(base + seg * 1024), 16, vo, so, 0, 0);
+                continue;
+            }
             const uint16_t *src;
             if (AT) {
                 int64_t mm = m0 + ((c ^ mnmaj_swz(line)) << 3);
@@ -461,6 +480,13 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             if (TA::segs / NW + i < lo || TA::segs / NW + i >= hi) continue;
             const int seg = wave + NW * i;
             const int line = seg * TB::lines_per_seg + lane / TB::chunks, c = lane % TB::chunks;
+            if constexpr (buf) {
+                const uint32_t vo = BT ? uint32_t((line * s.b_k + ((c ^ mnmaj_swz(line)) << 3)) * 2)
+                                       : uint32_t((line * s.b_n + ((c ^ kmaj_swz<BK>(line)) << 3)) * 2);
+                const uint32_t so = BT ? uint32_t(k0 * s.b_k * 2) : uint32_t(k0 * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, (glds_void_t *)(base + TA::bytes + seg * 1024), 16, vo, so, 0, 0);
+                continue;
+            }
             const uint16_t *src;
             if (BT) {
                 int64_t nn = n0 + ((c ^ mnmaj_swz(line)) << 3);
@@ -578,11 +604,22 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     }
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
 __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
     extern __shared__ __align__(1024) char smem[];
-    gemm_stream_tile<F16, BK, WN, AT, BT>(s, a, b, out, smem);
+    gemm_stream_tile<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
+}
+
+// Whether every operand byte a 256 x 256 tile of `s` reads lies within 2^31 bytes of the tile's first
+// element (the buffer-load path's 32-bit offsets); the launch picks the 64-bit global-address path otherwise.
+__host__ __device__ inline bool stream_buffer_ok(int64_t m, int64_t n, int64_t k, bool at, bool bt, int64_t a_m,
+                                                 int64_t a_k, int64_t b_k, int64_t b_n) {
+    const int64_t lim = int64_t(1) << 31;
+    const int64_t abytes = at ? ((k - 1) * a_k + 256) * 2 : (255 * a_m + k) * 2;
+    const int64_t bbytes = bt ? ((k - 1) * b_k + 256) * 2 : (255 * b_n + k) * 2;
+    (void)m, (void)n;
+    return abytes < lim && bbytes < lim;
 }
 
 // Split-k reduction: D[z, r, c] = sum over splits of the float32 partials P[split][z][r][c] (contiguous,

@@ -107,13 +107,11 @@ int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const
     return check(hipGetLastError(), "gemm_mfma launch");
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT>
-int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
-                  int splits = 1) {
-    s.tiles_m = int((s.m + 255) / 256);
-    s.tiles_n = int((s.n + 255) / 256);
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
+int launch_stream_kernel(hipStream_t st, const GemmShape &s, int64_t z, const void *a, const void *b, void *out,
+                         int dtype, int splits) {
     constexpr int lds = gemm_stream_lds_bytes<BK, WN>();
-    auto kern = gemm_stream<F16, BK, WN, AT, BT>;
+    auto kern = gemm_stream<F16, BK, WN, AT, BT, BUF>;
     static bool attr = false;
     if (!attr) {
         if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
@@ -125,6 +123,16 @@ int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const v
     hipLaunchKernelGGL(kern, grid, dim3(128 * WN), lds, st, s, static_cast<const uint16_t *>(a),
                        static_cast<const uint16_t *>(b), AnyStore{out, dtype});
     return check(hipGetLastError(), "gemm_stream launch");
+}
+
+template <bool F16, int BK, int WN, bool AT, bool BT>
+int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
+                  int splits = 1) {
+    s.tiles_m = int((s.m + 255) / 256);
+    s.tiles_n = int((s.n + 255) / 256);
+    if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
+        return launch_stream_kernel<F16, BK, WN, AT, BT, true>(st, s, z, a, b, out, dtype, splits);
+    return launch_stream_kernel<F16, BK, WN, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
 }
 
 template <bool F16, bool AT, bool BT>
