@@ -123,13 +123,28 @@ __device__ __forceinline__ int kv_off(int r, int col) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Issues the loads of rows [k0, k0 + 64) of a [*, D] operand (row stride `rs` elements) into the swizzled
-// tile `dst`; rows past `rows` are clamped to the last row (their scores are masked).
+// Issues the loads of rows [k0, k0 + 64) of a [*, D] operand (row stride `rs` elements, `rows` rows) into
+// the swizzled tile `dst`. When the operand spans less than 2^31 bytes the loads are buffer loads (the row
+// offset a uniform operand, the lane's offset fixed) and rows past `rows` read zeros; otherwise 64-bit global
+// loads with rows past `rows` clamped to the last row. Either way those rows' scores are masked.
 template <int D>
 __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs, int64_t k0, int64_t rows,
                                                 uint16_t *dst, int wave, int lane) {
     constexpr int RPS = 1024 / (D * 2);  // rows a wave instruction covers
     constexpr int SEGS = 64 / RPS;       // 1 KiB segments in the tile
+    const int64_t bytes = ((rows - 1) * rs + D) * 2;
+    if (bytes < (int64_t(1) << 31) && (k0 + 64) * rs * 2 < (int64_t(1) << 31)) {
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, int(bytes), 0x00020000);
+        const uint32_t so = uint32_t(k0 * rs * 2);
+#pragma unroll
+        for (int seg = wave; seg < SEGS; seg += 4) {
+            const int r = seg * RPS + lane / (D / 8);
+            const int c = lane % (D / 8);
+            const uint32_t vo = uint32_t((r * rs + ((c ^ kv_swz<D>(r)) << 3)) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(dst + seg * 512), 16, vo, so, 0, 0);
+        }
+        return;
+    }
 #pragma unroll
     for (int seg = wave; seg < SEGS; seg += 4) {
         const int r = seg * RPS + lane / (D / 8);
