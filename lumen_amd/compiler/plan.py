@@ -308,6 +308,8 @@ class Plan:
 
     # ---- GEMM epilogues (lumen/graph_compiler/passes/fusion/mod.rs:20-112, the CUDA backend's `epilogue`):
     # a loop step that reads a dot's [m, n] result element for element runs inside the dot's store
+    EPI_MIN_TILES = 256  # the streamed GEMM's own default threshold (kernels.hip: default_config)
+
     def _epilogue_layout(self, st):
         """``(desc, at, bt, f16)`` when dot step ``st`` can run as a streamed GEMM with a generated epilogue
         (2-D bf16/f16 operands, k a multiple of 64, one k split, operand rows 16-byte aligned), else None."""
@@ -325,6 +327,8 @@ class Plan:
             return None
         if d.a_dtype != d.b_dtype or d.a_dtype not in (nv.NHIP_BF16, nv.NHIP_F16) or d.k % 64 or d.n % 4:
             return None
+        if -(-d.m // 256) * -(-d.n // 256) < self.EPI_MIN_TILES:
+            return None  # too few 256 x 256 tiles to fill the CUs: a smaller tiled kernel (autotuned) is faster
         if d.a_k == 1 and d.a_m % 8 == 0:
             at = False
         elif d.a_m == 1 and d.m % 8 == 0 and d.a_k % 8 == 0:

@@ -102,10 +102,14 @@ def _epi_fn_keep(x, w, h, b):
 
 @pytest.mark.parametrize("fn", [_epi_fn, _epi_fn_keep])
 @pytest.mark.parametrize("m,n,k", [(512, 512, 256), (1000, 776, 320)])
-def test_gemm_epilogue_matches_oracle_and_unfused_plan(hip, fn, m, n, k):
+def test_gemm_epilogue_matches_oracle_and_unfused_plan(hip, fn, m, n, k, monkeypatch):
     """The dot with its elementwise consumer fused into the GEMM's store (gemm_epi kernel, ragged m and n
     included) against the oracle (float32: rtol 1e-4 of the largest value, the tolerance for float32
-    results), and bit for bit against the same plan without epilogue fusion (same sums, same body)."""
+    results), and bit for bit against the same plan without epilogue fusion (same sums, same body). The
+    fusion threshold (256 tiles) is lowered so that these small shapes take the fused path."""
+    from lumen_amd.compiler.plan import Plan
+
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
     rng = np.random.default_rng(11)
     x = _bf16(rng.standard_normal((m, k)) * 0.25)
     w = _bf16(rng.standard_normal((k, n)) * 0.25)

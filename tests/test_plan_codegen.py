@@ -84,10 +84,12 @@ EPI_SHAPES = [((512, 256), "bfloat16"), ((256, 512), "bfloat16"), ((512, 512), "
 
 
 @pytest.mark.parametrize("fn,keep", [(_epilogue_fn, False), (_epilogue_fn_keep, True)])
-def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep):
+def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep, monkeypatch):
     """A loop reading a dot's [m, n] result element for element (with other operands: a broadcast row, a
     same-shape tensor) is merged into the dot: one launch of a generated gemm_epi kernel, which also stores
-    the dot's own result when something else (here a graph output) reads it."""
+    the dot's own result when something else (here a graph output) reads it. (The plan fuses only dots with
+    enough 256 x 256 tiles to fill the GPU; the threshold is lowered to exercise small shapes.)"""
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
     with L.config.compiler.patch(horizontal_fusion=False):
         p = _plan(fn, *EPI_SHAPES, build=True)
     assert [s.kind for s in p.steps] == ["dot"]
@@ -96,6 +98,10 @@ def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep):
     with L.config.compiler.patch(epilogue_fusion=False, horizontal_fusion=False):
         q = _plan(fn, *EPI_SHAPES)
     assert [s.kind for s in q.steps] == ["dot", "loop"]
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 256)
+    with L.config.compiler.patch(horizontal_fusion=False):
+        r = _plan(fn, *EPI_SHAPES)
+    assert [s.kind for s in r.steps] == ["dot", "loop"]  # 4 tiles: left to the autotuned tiled kernels
 
 
 def test_one_row_kernel_for_a_normalization_chain():
