@@ -338,24 +338,28 @@ __device__ __forceinline__ int mnmaj_swz(int k) { return (k & 3) << 2; }
 
 typedef __attribute__((address_space(3))) void glds_void_t;
 
-template <int BK, bool T>
+template <int BK, bool T, int TM = 256>
 struct StreamTile {
-    static constexpr int line_bytes = T ? 256 * 2 : BK * 2;  // a k-line of 256 mn, or a row of BK k
+    static constexpr int line_bytes = T ? TM * 2 : BK * 2;  // a k-line of TM mn, or a row of BK k
     static constexpr int chunks = line_bytes / 16;
     static constexpr int lines_per_seg = 1024 / line_bytes;
-    static constexpr int bytes = 256 * BK * 2;
+    static constexpr int bytes = TM * BK * 2;
     static constexpr int segs = bytes / 1024;
 };
 
-template <int BK>
-constexpr int gemm_stream_stages() { return (128 * 1024) / (2 * 256 * BK * 2); }
+// Stages: 128 KiB of operand tiles for the 256 x 256 tile (one workgroup a CU); two stages (64 KiB, two
+// workgroups a CU) for the 128 x 128 tile.
+template <int BK, int TM = 256>
+constexpr int gemm_stream_stages() { return TM == 256 ? (128 * 1024) / (2 * 256 * BK * 2) : 2; }
 // Epilogue staging: a wave's 64 rows at a time, 16 bytes of padding a row.
-template <int WN>
-constexpr int gemm_stream_stage_pitch() { return (256 / WN) * 4 + 16; }
+template <int WN, int TM = 256>
+constexpr int gemm_stream_stage_pitch() { return (TM / WN) * 4 + 16; }
 // LDS: the operand stages, or the epilogue's staging (float32 rows), whichever is larger.
-template <int BK, int WN>
+template <int BK, int WN, int TM = 256>
 constexpr int gemm_stream_lds_bytes() {
-    return 128 * 1024 > 2 * WN * 64 * gemm_stream_stage_pitch<WN>() ? 128 * 1024 : 2 * WN * 64 * gemm_stream_stage_pitch<WN>();
+    constexpr int ops = gemm_stream_stages<BK, TM>() * 2 * TM * BK * 2;
+    constexpr int epi = 2 * WN * 64 * gemm_stream_stage_pitch<WN, TM>();
+    return ops > epi ? ops : epi;
 }
 
 // Writes rows [rbase, rbase + 64) x columns [cbase, cbase + WCOLS) of D from a wave's float32 staging rows
@@ -409,24 +413,26 @@ __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyS
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
 // functor called as out(row, col, float4) with the float32 sums of four consecutive columns (col a multiple
 // of 4; columns at or past n are the functor's to skip). `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
-    constexpr int NW = 2 * WN;       // wavefronts
-    constexpr int FN = 8 / WN;       // 32-column MFMA tiles a wave
-    constexpr int WCOLS = 32 * FN;   // columns a wave
-    constexpr int STAGES = gemm_stream_stages<BK>();
-    using TA = StreamTile<BK, AT>;
-    using TB = StreamTile<BK, BT>;
+    constexpr int NW = 2 * WN;       // wavefronts (2 x WN)
+    constexpr int WR = TM / 2;       // rows a wave
+    constexpr int FM = WR / 32;      // 32-row MFMA tiles a wave
+    constexpr int WCOLS = TM / WN;   // columns a wave
+    constexpr int FN = WCOLS / 32;   // 32-column MFMA tiles a wave
+    constexpr int STAGES = gemm_stream_stages<BK, TM>();
+    using TA = StreamTile<BK, AT, TM>;
+    using TB = StreamTile<BK, BT, TM>;
     constexpr int STAGE_BYTES = TA::bytes + TB::bytes;
     constexpr int LPS = (TA::segs + TB::segs) / NW;  // load instructions a wave issues per stage
-    constexpr int NRD = (AT ? 8 : 4) + (BT ? 2 * FN : FN);  // LDS read instructions a k step
+    constexpr int NRD = (AT ? 2 * FM : FM) + (BT ? 2 * FN : FN);  // LDS read instructions a k step
 
     int tm, tn;
     tile_of(blockIdx.x, s.tiles_m, s.tiles_n, tm, tn);
     int64_t oa, ob, od;
     batch_offsets(s, blockIdx.y, oa, ob, od);
-    const int64_t m0 = int64_t(tm) * 256, n0 = int64_t(tn) * 256;
+    const int64_t m0 = int64_t(tm) * TM, n0 = int64_t(tn) * TM;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int h = lane >> 5, l32 = lane & 31, g = lane >> 4, s16 = lane & 15;
@@ -440,7 +446,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     // per-lane 32-bit offset fixed for the whole k loop plus a uniform k offset, with no per-load address
     // arithmetic, and rows past m / n read zeros. Operands whose tile span exceeds 2^31 bytes use 64-bit
     // global addresses instead.
-    const int64_t mrem = s.m - m0 < 256 ? s.m - m0 : 256, nrem = s.n - n0 < 256 ? s.n - n0 : 256;
+    const int64_t mrem = s.m - m0 < TM ? s.m - m0 : TM, nrem = s.n - n0 < TM ? s.n - n0 : TM;
     const int64_t abytes = AT ? ((s.k - 1) * s.a_k + mrem) * 2 : ((mrem - 1) * s.a_m + s.k) * 2;
     const int64_t bbytes = BT ? ((s.k - 1) * s.b_k + nrem) * 2 : ((nrem - 1) * s.b_n + s.k) * 2;
     constexpr bool buf = BUF;  // the launcher checked stream_buffer_ok()
@@ -505,8 +511,8 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         if constexpr (decltype(tr)::value) {
             const int kl = kk + 8 * h + s16 / 4;
             const int mn = r0 + 16 * (g & 1) + 4 * (s16 & 3);
-            const char *p0 = tile + kl * 512 + (((mn >> 3) ^ mnmaj_swz(kl)) << 4) + ((mn & 7) << 1);
-            const char *p1 = tile + (kl + 4) * 512 + (((mn >> 3) ^ mnmaj_swz(kl + 4)) << 4) + ((mn & 7) << 1);
+            const char *p0 = tile + kl * (TM * 2) + (((mn >> 3) ^ mnmaj_swz(kl)) << 4) + ((mn & 7) << 1);
+            const char *p1 = tile + (kl + 4) * (TM * 2) + (((mn >> 3) ^ mnmaj_swz(kl + 4)) << 4) + ((mn & 7) << 1);
             gv4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p0));
             gv4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p1));
             uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
@@ -517,9 +523,9 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         }
     };
 
-    f32x16_t acc[4][FN];
+    f32x16_t acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -538,13 +544,13 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         const bool more = kt + STAGES - 1 < ktiles;
         const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
         const char *tb = ta + TA::bytes;
-        uint4 fa[2][4], fb[2][FN];
+        uint4 fa[2][FM], fb[2][FN];
         auto read = [&](int buf, int kk) {  // in the order the MFMAs (i-major) first use them
-            fa[buf][0] = frag(ta, wm * 128, kk, std::integral_constant<bool, AT>{});
+            fa[buf][0] = frag(ta, wm * WR, kk, std::integral_constant<bool, AT>{});
 #pragma unroll
             for (int j = 0; j < FN; ++j) fb[buf][j] = frag(tb, wn * WCOLS + 32 * j, kk, std::integral_constant<bool, BT>{});
 #pragma unroll
-            for (int i = 1; i < 4; ++i) fa[buf][i] = frag(ta, wm * 128 + 32 * i, kk, std::integral_constant<bool, AT>{});
+            for (int i = 1; i < FM; ++i) fa[buf][i] = frag(ta, wm * WR + 32 * i, kk, std::integral_constant<bool, AT>{});
         };
         read(0, 0);
         auto step = [&](auto kkc) {
@@ -556,10 +562,10 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             // rather than issued in one burst after the barrier
             if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<F16>::run(fb[cur][j], fa[cur][i], acc[i][j]);
-            if constexpr (kk + 16 < BK) mfma_ds_interleave<0, 4 * FN, NRD, kk / 16 + 1>();
+            if constexpr (kk + 16 < BK) mfma_ds_interleave<0, FM * FN, NRD, kk / 16 + 1>();
             __builtin_amdgcn_sched_barrier(0);
         };
         step(std::integral_constant<int, 0>{});
@@ -570,14 +576,14 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         }
     }
 
-    // acc[i][j][e]: row m0 + wm*128 + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
+    // acc[i][j][e]: row m0 + wm*WR + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
     // Staged through LDS as float32, 64 rows of the wave at a time, then written row-wise.
-    const int64_t rbase = m0 + wm * 128, cbase = n0 + wn * WCOLS;
-    constexpr int PITCH = gemm_stream_stage_pitch<WN>();
+    const int64_t rbase = m0 + wm * WR, cbase = n0 + wn * WCOLS;
+    constexpr int PITCH = gemm_stream_stage_pitch<WN, TM>();
     __syncthreads();  // operand stages are dead: reuse LDS for the output
     char *stage = smem + wave * (64 * PITCH);
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < FM / 2; ++half) {
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) {
             const int i = 2 * half + ii;
@@ -609,6 +615,15 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
     extern __shared__ __align__(1024) char smem[];
     gemm_stream_tile<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
+}
+
+// The 128 x 128 tile: 4 wavefronts of 64 x 64, two 32 KiB stages, two workgroups a CU (dots with too few
+// 256 x 256 tiles to fill the chip).
+template <bool F16, bool AT, bool BT, bool BUF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stream128(
+    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
+    extern __shared__ __align__(1024) char smem[];
+    gemm_stream_tile<F16, 64, 2, AT, BT, BUF, AnyStore, 128>(s, a, b, out, smem);
 }
 
 // Whether every operand byte a 256 x 256 tile of `s` reads lies within 2^31 bytes of the tile's first

@@ -26,9 +26,11 @@ constexpr TileConfig kConfigs[] = {
 };
 constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // Configs past the tiled ones: gemm_stream (256 x 256, operands streamed into LDS): k tile 64 with 4 waves of
-// 128 x 128 (2 stages) and with 8 waves of 128 x 64 (2 stages); k tile 32 with 8 waves (4 stages).
-constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2;
-constexpr int kNumConfigs = kNumTiled + 3;
+// 128 x 128 (2 stages) and with 8 waves of 128 x 64 (2 stages); k tile 32 with 8 waves (4 stages); and
+// gemm_stream128 (128 x 128 tiles, 4 waves of 64 x 64, 2 stages, two workgroups a CU).
+constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
+              kStream128 = kNumTiled + 3;
+constexpr int kNumConfigs = kNumTiled + 4;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -59,10 +61,12 @@ int64_t batch_count(const nhip_gemm_desc *d) {
 }
 
 // The default tile for a shape: the streamed 256 x 256 kernel when k allows it and its tiles fill the 256 CUs,
-// else the largest tiled config whose tile count fills them at least once.
+// else the streamed 128 x 128 kernel (two workgroups a CU) when its tiles fill half of them, else the largest
+// tiled config whose tile count fills them at least once.
 int default_config(const nhip_gemm_desc *d) {
     int64_t z = batch_count(d);
     if (d->k % 64 == 0 && ((d->m + 255) / 256) * ((d->n + 255) / 256) * z >= 256) return kStream8w;
+    if (d->k % 64 == 0 && ((d->m + 127) / 128) * ((d->n + 127) / 128) * z >= 128) return kStream128;
     for (int c = 0; c < kNumTiled; ++c) {
         int64_t tiles = ((d->m + kConfigs[c].bm - 1) / kConfigs[c].bm) * ((d->n + kConfigs[c].bn - 1) / kConfigs[c].bn) * z;
         if (tiles >= 256) return c;
@@ -125,6 +129,34 @@ int launch_stream_kernel(hipStream_t st, const GemmShape &s, int64_t z, const vo
     return check(hipGetLastError(), "gemm_stream launch");
 }
 
+template <bool F16, bool AT, bool BT, bool BUF>
+int launch_stream128_kernel(hipStream_t st, const GemmShape &s, int64_t z, const void *a, const void *b, void *out,
+                            int dtype, int splits) {
+    constexpr int lds = gemm_stream_lds_bytes<64, 2, 128>();
+    auto kern = gemm_stream128<F16, AT, BT, BUF>;
+    static bool attr = false;
+    if (!attr) {
+        if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                  "hipFuncSetAttribute"))
+            return 1;
+        attr = true;
+    }
+    dim3 grid(s.tiles_m * s.tiles_n, unsigned(z), unsigned(splits));
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, s, static_cast<const uint16_t *>(a),
+                       static_cast<const uint16_t *>(b), AnyStore{out, dtype});
+    return check(hipGetLastError(), "gemm_stream128 launch");
+}
+
+template <bool F16, bool AT, bool BT>
+int launch_stream128(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
+                     int splits = 1) {
+    s.tiles_m = int((s.m + 127) / 128);
+    s.tiles_n = int((s.n + 127) / 128);
+    if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
+        return launch_stream128_kernel<F16, AT, BT, true>(st, s, z, a, b, out, dtype, splits);
+    return launch_stream128_kernel<F16, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
+}
+
 template <bool F16, int BK, int WN, bool AT, bool BT>
 int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
                   int splits = 1) {
@@ -141,6 +173,7 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream4w: return launch_stream<F16, 64, 2, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8w: return launch_stream<F16, 64, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8w32: return launch_stream<F16, 32, 4, AT, BT>(st, s, z, a, b, out, dtype);
+        case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
         case 2: return launch_mfma_cfg<F16, 128, 256, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
@@ -239,7 +272,7 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
-        if (((cfg == kStream4w || cfg == kStream8w) && d->k % 64) || (cfg == kStream8w32 && d->k % 32))
+        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128) && d->k % 64) || (cfg == kStream8w32 && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
         return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);

@@ -28,7 +28,8 @@ def _desc(m, n, k, a_m, a_k, b_k, b_n, dt=nv.NHIP_BF16, out=nv.NHIP_F32, cfg=-1,
 @pytest.mark.parametrize("at,bt", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize(
     "m,n,k,cfg",
-    [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0), (520, 264, 192, 6), (264, 776, 128, 7), (264, 136, 96, 8)],
+    [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0), (520, 264, 192, 6), (264, 776, 128, 7),
+     (264, 136, 96, 8), (200, 392, 192, 9)],
 )
 def test_gemm_layouts(hip, at, bt, m, n, k, cfg):
     """A as [m][k] or [k][m] in memory, B as [n][k] or [k][n]: float32 results within float32 rounding of
@@ -59,10 +60,11 @@ def test_gemm_batched_bf16_output(hip):
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
 
 
-@pytest.mark.parametrize("cfg,out", [(6, nv.NHIP_BF16), (7, nv.NHIP_F16), (7, nv.NHIP_F32), (8, nv.NHIP_BF16)])
+@pytest.mark.parametrize("cfg,out", [(6, nv.NHIP_BF16), (7, nv.NHIP_F16), (7, nv.NHIP_F32), (8, nv.NHIP_BF16),
+                                     (9, nv.NHIP_BF16), (9, nv.NHIP_F32)])
 def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
-    """The streamed 256 x 256 kernel's LDS-staged row stores: 16-bit and float32 outputs, m and n not
-    multiples of the tile, two batches."""
+    """The streamed kernels' LDS-staged row stores (256 x 256 tiles, configs 6-8; 128 x 128, config 9):
+    16-bit and float32 outputs, m and n not multiples of the tile, two batches."""
     rng = np.random.default_rng(cfg + out)
     z, m, n, k = 2, 300, 264, 128
     a = D.bf16_bits(rng.standard_normal((z, m, k)).astype(np.float32))
