@@ -252,6 +252,7 @@ def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
 
 REMAT = ELEMENTWISE | INDEX_ONLY | VIEWABLE
 REMAT_BUDGET = 32  # nodes a kernel may recompute in place of one value it reads
+REMAT_SMALL = 1 << 20  # operand bytes a recomputation may add regardless (per-row statistics)
 
 
 def _inputs_of(nodes):
@@ -267,9 +268,10 @@ def _inputs_of(nodes):
 def _rematerialize(graph, steps, prod):
     """Recomputes values instead of storing them (``passes/fusion/mod.rs`` duplicates cheap producers the
     same way). A loop or row kernel that reads a value computed elementwise from values already in memory
-    computes it itself, when that adds at most one new operand read: the training graph's backward kernels
-    then recompute an activation's intermediates (GELU's tanh argument and friends) from its input instead
-    of reading them back, and the forward kernels stop writing them."""
+    computes it itself, when that adds at most one new operand read (or new operands of at most the replaced
+    value's bytes, or at most 1 MiB): the training graph's backward kernels then recompute an activation's
+    intermediates (GELU's tanh argument and friends) from its input instead of reading them back, and the
+    forward kernels stop writing them."""
     in_memory = set(graph.inputs)
     for st in steps:
         in_memory.update(st.outputs)
@@ -302,8 +304,8 @@ def _rematerialize(graph, steps, prod):
                 if not ok:
                     continue
                 new = [v for v in leaves if v not in st.inputs]
-                if len(new) > 1:
-                    continue
+                if len(new) > 1 and sum(graph.types[v].nbytes() for v in new) > max(graph.types[u].nbytes(), REMAT_SMALL):
+                    continue  # more bytes to read than the value it replaces (small per-row vectors are free)
                 have = {m.output for m in st.nodes}
                 st.nodes.extend(m for v, m in expr.items() if v not in have)
                 st.nodes.sort(key=lambda m: m.output)
@@ -332,6 +334,44 @@ def _rematerialize(graph, steps, prod):
                 st.inputs = _inputs_of(st.nodes)
         kept.append(st)
     return kept
+
+
+def absorb_rows(graph, steps):
+    """Merges a loop kernel into an earlier row kernel over the same row space when everything the loop
+    reads is the row kernel's input, its output, or already in memory when the row kernel runs: the row
+    kernel writes the loop's outputs in its writing pass, and the operands both read (a softmax's logits,
+    say) are read once. Cross entropy's backward (softmax minus one-hot) joins the forward's max/sum-exp
+    kernel this way."""
+    pos = {}
+    for si, st in enumerate(steps):
+        for v in st.outputs:
+            pos[v] = si
+    merged = set()
+    for li, lt in enumerate(steps):
+        if lt.kind != "loop" or len(lt.outputs) == 0:
+            continue
+        numel = graph.types[lt.outputs[0]].numel()
+        cands = {pos[u] for u in lt.inputs if u in pos and steps[pos[u]].kind == "row"}
+        for ri in sorted(cands):
+            rt = steps[ri]
+            if ri in merged or ri >= li or rt.rows is None or rt.rows[0] * rt.rows[1] != numel:
+                continue
+            elem = [v for v in rt.outputs if graph.types[v].numel() == numel]
+            shape = graph.types[(elem or rt.inputs)[0]].shape if (elem or rt.inputs) else None
+            if any(graph.types[v].shape != shape for v in lt.outputs):
+                continue
+            ok = all(u in rt.inputs or u in rt.outputs or pos.get(u, -1) < ri for u in lt.inputs)
+            if not ok:
+                continue
+            have = {m.output for m in rt.nodes}
+            rt.nodes = sorted(rt.nodes + [m for m in lt.nodes if m.output not in have], key=lambda m: m.output)
+            rt.outputs = list(rt.outputs) + [v for v in lt.outputs if v not in rt.outputs]
+            rt.inputs = _inputs_of(rt.nodes)
+            for v in lt.outputs:
+                pos[v] = ri
+            merged.add(li)
+            break
+    return [st for i, st in enumerate(steps) if i not in merged]
 
 
 # Horizontal fusion (``passes/horizontal.rs:40-49,79-393``): small independent loop kernels share one launch.

@@ -174,6 +174,8 @@ class Plan:
     # ---- fusion with fallback: groups the generator rejects are split
     def _fuse(self):
         steps = fusion.fuse(self.graph, fuse_loops=config.compiler.fuse, packed=self.packed)
+        if config.compiler.fuse:
+            steps = fusion.absorb_rows(self.graph, steps)
         if config.compiler.fuse and config.compiler.horizontal_fusion:
             steps = fusion.horizontal(self.graph, steps)
         return steps
