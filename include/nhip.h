@@ -211,6 +211,15 @@ int nhip_plan_profile(void *plan, int enable);
 /* Milliseconds of each of the first `n` steps of the last profiled run (waits for it to finish). */
 int nhip_plan_step_ms(void *plan, float *ms, size_t n);
 
+/* HIP graphs of a plan (the analogue of the reference's CUDA graphs: lumen/graph/tracer.py:958-1049,
+ * lumen/runtime/stream/cuda.rs:119-294). nhip_plan_capture records every step of one run, bound to
+ * `workspace` and `inputs` (whose addresses the graph keeps; the caller stages new argument values into
+ * the same memory before each launch), into an executable graph; profiling events are not recorded.
+ * nhip_graph_launch queues it on the current device's stream; nhip_graph_destroy frees it. */
+int nhip_plan_capture(void *plan, void *workspace, void *const *inputs, size_t ninputs, void **graph);
+int nhip_graph_launch(void *graph);
+int nhip_graph_destroy(void *graph);
+
 #ifdef __cplusplus
 }
 #endif

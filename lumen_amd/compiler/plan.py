@@ -83,6 +83,28 @@ def _view_of(prim, params, src: Loc, ty) -> Loc | None:
     return None
 
 
+class _Graph:
+    """An executable HIP graph of a plan run (``Plan.capture``), destroyed with the object."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def launch(self):
+        from lumen_amd import native as nv
+
+        nv.call("nhip_graph_launch", C.c_void_p(self.handle))
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            try:
+                from lumen_amd import native as nv
+
+                nv.lib().nhip_graph_destroy(C.c_void_p(self.handle))
+            except Exception:
+                pass
+            self.handle = None
+
+
 def _operand_view(cat: Loc, start, operand, ty) -> Loc:
     """Where an operand of a concatenation lives inside it: the slice ``start = (dim, offset)`` of shape
     ``operand.shape``, reshaped to the producer's type ``ty``."""
@@ -738,6 +760,17 @@ class Plan:
         arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
         nv.call("nhip_plan_run", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs))
 
+    def capture(self, workspace_ptr: int, input_ptrs: list):
+        """A HIP graph of one whole run bound to these pointers (``nhip_plan_capture``); launch it with
+        ``launch_graph``. The plan must have run once (its kernels built and autotuned)."""
+        from lumen_amd import native as nv
+
+        plan = self._native_plan()
+        arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
+        handle = C.c_void_p()
+        nv.call("nhip_plan_capture", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs), C.byref(handle))
+        return _Graph(handle.value)
+
     def run_steps(self, workspace_ptr: int, input_ptrs: list, si: int):
         """Queues the native steps of python step ``si`` alone (after a whole run has produced its inputs)."""
         from lumen_amd import native as nv
@@ -758,10 +791,12 @@ class Plan:
 
     # ---- measurement
     def profile(self, enable=True):
-        """Records a HIP event around every native step of each run (per-kernel times)."""
+        """Records a HIP event around every native step of each run (per-kernel times); profiled runs are
+        never replayed from a captured graph."""
         from lumen_amd import native as nv
 
         nv.call("nhip_plan_profile", self._native_plan(), int(enable))
+        self._profiling = bool(enable)
 
     def step_ms(self):
         """Milliseconds of each native step of the last profiled run, as ``(python step index, ms)``."""

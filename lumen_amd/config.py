@@ -16,6 +16,7 @@ class CompilerFlags:
     epilogue_fusion: bool = True      # fuse elementwise consumers into GEMM stores
     autotune: bool = True             # time GEMM tile candidates before a plan's first run
     deterministic: bool = True        # attention backward without atomics
+    hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
     _version: int = 0
 
     def __setattr__(self, name, value):

@@ -490,14 +490,71 @@ int nhip_plan_run(void *plan_, void *workspace, void *const *inputs, size_t ninp
     return nhip_plan_run_steps(plan_, workspace, inputs, ninputs, 0, plan->steps.size());
 }
 
+static int run_steps(Plan *plan, void *workspace, void *const *inputs, size_t ninputs, size_t begin, size_t end,
+                     bool events);
+
 int nhip_plan_run_steps(void *plan_, void *workspace, void *const *inputs, size_t ninputs, size_t begin, size_t end) {
+    return run_steps(static_cast<Plan *>(plan_), workspace, inputs, ninputs, begin, end, true);
+}
+
+struct Graph {
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
+};
+
+int nhip_plan_capture(void *plan_, void *workspace, void *const *inputs, size_t ninputs, void **graph) {
     Plan *plan = static_cast<Plan *>(plan_);
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return 1;
+    if (check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) return 1;
+    const int rc = run_steps(plan, workspace, inputs, ninputs, 0, plan->steps.size(), false);
+    const std::string err = rc ? g_error : std::string();
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(s, &g);  // ends the capture even when a step failed
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail("nhip_plan_capture: " + err);
+    }
+    if (check(end, "hipStreamEndCapture")) return 1;
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (check(inst, "hipGraphInstantiate")) return 1;
+    Graph *out = new Graph;
+    out->exec = exec;
+    out->device = dev;
+    *graph = out;
+    return 0;
+}
+
+int nhip_graph_launch(void *graph_) {
+    Graph *graph = static_cast<Graph *>(graph_);
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return 1;
+    if (dev != graph->device) return fail("nhip_graph_launch: the graph was captured on another device");
+    return check(hipGraphLaunch(graph->exec, s), "hipGraphLaunch");
+}
+
+int nhip_graph_destroy(void *graph_) {
+    Graph *graph = static_cast<Graph *>(graph_);
+    if (!graph) return 0;
+    const int rc = graph->exec ? check(hipGraphExecDestroy(graph->exec), "hipGraphExecDestroy") : 0;
+    delete graph;
+    return rc;
+}
+
+static int run_steps(Plan *plan, void *workspace, void *const *inputs, size_t ninputs, size_t begin, size_t end,
+                     bool events) {
     hipStream_t s = stream_of_current();
     if (!s) return fail("no HIP stream: call nhip_set_device first");
     if (begin > end || end > plan->steps.size())
         return fail("nhip_plan_run_steps: steps [" + std::to_string(begin) + ", " + std::to_string(end) + ") of " +
                     std::to_string(plan->steps.size()));
-    const bool whole = begin == 0 && end == plan->steps.size();
+    const bool whole = events && begin == 0 && end == plan->steps.size();
     char *ws = static_cast<char *>(workspace);
     for (size_t i = begin; i < end; ++i) {
         Step &st = plan->steps[i];

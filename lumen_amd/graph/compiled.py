@@ -16,6 +16,7 @@ import numpy as np
 from lumen_amd import nn
 from lumen_amd.config import config
 from lumen_amd.graph.trace import trace, tree_leaves
+from lumen_amd import native
 from lumen_amd.tensor import DeviceBuffer, Tensor, device_name, device_type, empty
 
 
@@ -31,6 +32,7 @@ class Compiled:
         self._device = None if device is None else device_name(device)
         self._plans = {}
         self._latest = None
+        self._graphs = {}  # id(plan) -> "warm" after its first call, then (graph, staging buffers, fixed, ptrs)
 
     def _target(self, args):
         if self._device is not None:
@@ -72,6 +74,42 @@ class Compiled:
     def plan(self):
         return self._plans[self._latest][1]
 
+    def _run(self, plan, workspace, traced, ptrs, keep):
+        """``plan.run_in``; with ``config.compiler.hip_graphs`` (the reference's CUDA graphs,
+        ``lumen/graph/tracer.py:958-1049``) a plan runs as usual on its first call (which builds and autotunes
+        its kernels), is captured on its second into a HIP graph over device buffers of its own for the
+        call's arguments and runtime scalars, and from then on each call copies those in (stream-ordered)
+        and launches the graph. Weights and the workspace are read where they were captured; when one moves,
+        the plan is captured again. Profiled runs (``plan.profile``) are never captured. Returns the input
+        pointers the run read."""
+        if not config.compiler.hip_graphs or getattr(plan, "_profiling", False):
+            plan.run_in(workspace.ptr, ptrs)
+            return ptrs
+        state = self._graphs.get(id(plan))
+        staged = [i for i, (kind, _) in enumerate(traced.layout) if kind in ("arg", "scalar")]
+        fixed = [workspace.ptr] + [p for i, p in enumerate(ptrs) if i not in staged]
+        if state is None:
+            self._graphs[id(plan)] = "warm"
+            plan.run_in(workspace.ptr, ptrs)
+            return ptrs
+        if state == "warm" or state[2] != fixed:
+            dev = int(plan.device.split(":")[1])
+            buffers = {i: DeviceBuffer(dev, max(1, keep[i].nbytes)) for i in staged}
+            gptrs = [buffers[i].ptr if i in buffers else p for i, p in enumerate(ptrs)]
+            graph = None
+            self._graphs[id(plan)] = None
+            for i, b in buffers.items():
+                native.d2d(b.ptr, ptrs[i], keep[i].nbytes)
+            graph = plan.capture(workspace.ptr, gptrs)
+            state = (graph, buffers, fixed, gptrs)
+            self._graphs[id(plan)] = state
+        else:
+            graph, buffers, _, gptrs = state
+            for i, b in buffers.items():
+                native.d2d(b.ptr, ptrs[i], keep[i].nbytes)
+        graph.launch()
+        return gptrs
+
     def last_buffers(self):
         """``(workspace pointer, input pointers)`` of the latest run (to replay some of its steps)."""
         return self._last_buffers
@@ -106,7 +144,7 @@ class Compiled:
                     t = traced.weights[k]._placed(target)
                     keep.append(t)
                     ptrs.append(t.data_ptr())
-            plan.run_in(workspace.ptr, ptrs)
+            ptrs = self._run(plan, workspace, traced, ptrs, keep)
             self._last_buffers = (workspace.ptr, ptrs)
             outs = []
             for v, loc in zip(g.outputs, plan.output_locs):

@@ -143,6 +143,9 @@ SIGNATURES = {
     "nhip_plan_steps": ([C.c_void_p, C.POINTER(C.c_size_t)], C.c_int),
     "nhip_plan_profile": ([C.c_void_p, C.c_int], C.c_int),
     "nhip_plan_step_ms": ([C.c_void_p, C.POINTER(C.c_float), C.c_size_t], C.c_int),
+    "nhip_plan_capture": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p), C.c_size_t, C.POINTER(C.c_void_p)], C.c_int),
+    "nhip_graph_launch": ([C.c_void_p], C.c_int),
+    "nhip_graph_destroy": ([C.c_void_p], C.c_int),
 }
 
 

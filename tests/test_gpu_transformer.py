@@ -82,3 +82,42 @@ def test_transformer_train_step_updates_weights(hip):
         w = want[1 + j]
         tol = 2e-2 * np.abs(w) + 1e-2 * np.abs(w).max()
         assert (np.abs(got - w) <= tol).mean() > 0.999, names[id(p)]
+
+
+def test_hip_graph_replays_match_uncaptured_runs(hip):
+    """With hip_graphs the third and later calls of a compiled function replay one captured HIP graph whose
+    arguments and runtime scalars are staged into its own buffers: several calls with new inputs, new
+    scalars and eager device work in between, each equal bit for bit to the same call run uncaptured; then
+    the training step (weights written back every call) for three steps, equal to the uncaptured steps."""
+    import lumen_amd.functional as F
+
+    def fn(x, w, s):
+        return F.relu(F.matmul(x, w, "float32", "float32")) * s + x.float().sum()
+
+    rng = np.random.default_rng(5)
+    w = L.tensor(D.bf16_to_f32(D.bf16_bits(rng.standard_normal((256, 320)) * 0.1)), "bfloat16")
+    xs = [L.tensor(D.bf16_to_f32(D.bf16_bits(rng.standard_normal((512, 256)))), "bfloat16") for _ in range(5)]
+    with L.config.compiler.patch(hip_graphs=True):
+        f = L.compile(fn, device="hip")
+        got = []
+        for i, x in enumerate(xs):
+            got.append(np.asarray(L.to_numpy(f(x, w, 0.5 + i)), np.float32))
+            L.from_numpy(np.full(1 << 20, float(i), np.float32)).to("hip")  # eager work between calls
+        assert f._graphs[id(f.plan)] not in (None, "warm")  # captured
+    with L.config.compiler.patch(hip_graphs=False):
+        u = L.compile(fn, device="hip")
+        want = [np.asarray(L.to_numpy(u(x, w, 0.5 + i)), np.float32) for i, x in enumerate(xs)]
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(g_, w_)
+
+    losses = {}
+    for graphs in (True, False):
+        cfg = W.TINY
+        model, opt, weights, ids, targets, args = _setup(cfg, W.train_step)
+        args = (model, opt) + args[1:]
+        with L.config.compiler.patch(hip_graphs=graphs):
+            step = L.compile(W.train_step, device="hip")
+            losses[graphs] = [float(L.to_numpy(step(*args))) for _ in range(4)]
+            losses[graphs].append(D.bf16_to_f32(model.head._placed("hip:0").raw()).copy())
+    assert losses[True][:4] == losses[False][:4]
+    assert np.array_equal(losses[True][4], losses[False][4])
