@@ -10,6 +10,7 @@ from __future__ import annotations
 import functools
 
 from lumen_amd import dtypes as D
+from lumen_amd.autograd import cross_entropy
 from lumen_amd.autograd.function import FUNCTION, gradients
 from lumen_amd.autograd.rules import NON_DIFFERENTIABLE, RULES
 from lumen_amd.graph import prims as P
@@ -30,6 +31,7 @@ def backward(out, ct, tape, leaves):
     if (ct.dtype, tuple(ct.shape)) != (out.dtype, tuple(out.shape)):
         raise TypeError(f"backward: a gradient must have its value's type, got {ct.dtype}{list(ct.shape)} for {out!r}")
     graph = tracer.current_graph()
+    tape = cross_entropy.substitute(tape)
     # Values that depend on a float leaf: only their nodes are differentiated.
     live = {p.var for p in leaves if D.is_float(p.dtype)}
     linear = []

@@ -17,6 +17,8 @@ class CompilerFlags:
     autotune: bool = True             # time GEMM tile candidates before a plan's first run
     deterministic: bool = True        # attention backward without atomics
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
+    # rows a chunk of the fused linear cross entropy backward (None: off, the reference's default)
+    fused_linear_cross_entropy_chunk_size: int | None = None
     _version: int = 0
 
     def __setattr__(self, name, value):

@@ -88,3 +88,38 @@ def test_function_backward_is_used():
 
     (g,) = oracle.run(L.make_graph(f)(L.empty([2], "float64", "meta")), [np.array([1.0, 2.0])])
     np.testing.assert_allclose(g, [10.0, 10.0])
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_fused_linear_cross_entropy_backward_matches_the_plain_gradient(transposed):
+    """With fused_linear_cross_entropy_chunk_size, the gradient of mean(cross_entropy(h @ w')) is taken a row
+    chunk at a time from the saved log-sum-exp (the logits recomputed per chunk): the graph has the chunk
+    dots, and the oracle's gradients equal the plain graph's within the bf16 rounding of the logits gradient
+    (rtol 2e-2 / atol 1e-2 of the largest, the bf16 bound) — bit for bit for the loss."""
+    import lumen_amd.functional as F
+    from lumen_amd import dtypes as D
+
+    rows, feat, classes = 96, 32, 80
+    rng = np.random.default_rng(2)
+    h = D.bf16_bits(rng.standard_normal((rows, feat)).astype(np.float32))
+    w = D.bf16_bits((0.3 * rng.standard_normal((feat, classes) if transposed else (classes, feat))).astype(np.float32))
+    t = rng.integers(0, classes, rows).astype(np.int64)
+
+    def loss(h, w, t):
+        logits = F.matmul(h, w if transposed else w.t(), "float32", "float32")
+        return F.mean(F.cross_entropy(logits, t))
+
+    metas = [L.empty(list(h.shape), "bfloat16", "meta"), L.empty(list(w.shape), "bfloat16", "meta"),
+             L.empty([rows], "int64", "meta")]
+    outs = {}
+    for chunk in (None, 40):
+        with L.config.compiler.patch(fused_linear_cross_entropy_chunk_size=chunk):
+            g = L.make_graph(lambda a, b, c: L.value_and_grad(loss, (0, 1))(a, b, c))(*metas)
+        dots = sum(1 for n in g.nodes if n.prim == "dot_general")
+        outs[chunk] = (dots, oracle.run(g, [h, w, t]))
+    assert outs[40][0] == 1 + 3 * 3 and outs[None][0] == 3  # forward + 3 chunks x (logits, dh, dw)
+    assert np.array_equal(np.asarray(outs[None][1][0]), np.asarray(outs[40][1][0]))  # the loss
+    for a, b in zip(outs[None][1][1:], outs[40][1][1:]):
+        a = D.bf16_to_f32(a) if a.dtype == np.uint16 else np.asarray(a, np.float32)
+        b = D.bf16_to_f32(b) if b.dtype == np.uint16 else np.asarray(b, np.float32)
+        np.testing.assert_allclose(b, a, rtol=2e-2, atol=1e-2 * np.abs(a).max())

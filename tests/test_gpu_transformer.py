@@ -65,15 +65,19 @@ def test_transformer_gradients_match_oracle(hip, hfuse):
         assert err <= 5e-2, (name, err)
 
 
-def test_transformer_train_step_updates_weights(hip):
-    """One SGD step (lr 1.0): the loss, and the written-back weights within bf16 rounding of the oracle's."""
+@pytest.mark.parametrize("lce_chunk", [None, 128])
+def test_transformer_train_step_updates_weights(hip, lce_chunk):
+    """One SGD step (lr 1.0): the loss, and the written-back weights within bf16 rounding of the oracle's;
+    also with the fused linear cross entropy backward (two row chunks), against the oracle on the same
+    (substituted) traced graph."""
     cfg = W.TINY
     model, opt, weights, ids, targets, args = _setup(cfg, W.train_step)
     args = (model, opt) + args[1:]
     names = {id(p): n for n, p in model.named_parameters()}
-    f = L.compile(W.train_step, device="hip")
-    loss = float(L.to_numpy(f(*args)))
-    traced = trace(W.train_step, args)
+    with L.config.compiler.patch(fused_linear_cross_entropy_chunk_size=lce_chunk):
+        f = L.compile(W.train_step, device="hip")
+        loss = float(L.to_numpy(f(*args)))
+        traced = trace(W.train_step, args)
     want = oracle.values(traced.graph, _oracle_inputs(traced, ids, targets, weights, names, scalars=[1.0]))
     assert abs(loss - want[0]) <= 1e-2 * abs(want[0])
     for j, k in enumerate(traced.written):
