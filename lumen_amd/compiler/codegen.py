@@ -814,6 +814,8 @@ class LoopKernel:
         atomic = red.prim == "reduce_sum" and out_dt == "float32" and Q >= 64
         chunk = max(1, min(Q, 64)) if atomic else Q
         nchunks = -(-Q // chunk)
+        if atomic and tuple(axes) == tuple(range(len(axes))) and O % 4 == 0 and O >= 1024:
+            return self._reduce_leading(red, Q, O, chunk, nchunks)
         em = self._emitter()
         om = em.multi(("flat", "o"), oshape)
         qm = em.multi(("flat", "q"), rshape)
@@ -849,6 +851,40 @@ class LoopKernel:
         ]
         src += ["    " + l for l in body]
         src += ["    " + upd, "  }", "  " + store, "}"]
+        return "\n".join(src)
+
+
+    def _reduce_leading(self, red, Q, O, chunk, nchunks):
+        """float32 sum over the leading axes of a [Q, O] row-major value (a bias or norm-weight gradient):
+        each thread sums 4 consecutive columns over ``chunk`` rows with 16-byte loads (four rows in flight),
+        then adds them atomically into the zero-filled output."""
+        g = self.graph
+        em = self._emitter()
+        em.vec = 4
+        vals = []
+        for lane in range(4):
+            vals.append(em.value(red.inputs[0], ("flat", f"(qb + {lane})", "qb", lane)))
+        body = self._vec_prologue(em, 4) + em.lines
+        self.atomic = True
+        threads = 256
+        self.grid, self.block, self.lds = (-(-(O // 4) // threads), nchunks, 1), (threads, 1, 1), 0
+        view = self.out_views[red.output]
+        oshape = g.types[red.output].shape
+        adds = [f"atomicAdd(&out0[{self._out_addr(view, oshape, f'(o + {l})')}], acc{l});" for l in range(4)]
+        src = [
+            f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{',
+            f"  const int64_t o = ((int64_t)blockIdx.x * {threads} + threadIdx.x) * 4;",
+            f"  if (o >= {O}LL) return;",
+            f"  const int64_t q0 = (int64_t)blockIdx.y * {chunk}LL;",
+            f"  const int64_t q1 = min(q0 + {chunk}LL, {Q}LL);",
+            "  float acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;",
+            "#pragma unroll 4",
+            "  for (int64_t q = q0; q < q1; ++q) {",
+            f"    const int64_t qb = q * {O}LL + o;",
+        ]
+        src += ["    " + l for l in body]
+        src += [f"    acc{l} = ((float)(acc{l} + {vals[l]}));" for l in range(4)]
+        src += ["  }"] + ["  " + a for a in adds] + ["}"]
         return "\n".join(src)
 
 
