@@ -132,3 +132,43 @@ def test_gemm_epilogue_matches_oracle_and_unfused_plan(hip, fn, m, n, k, monkeyp
         w_ = np.asarray(w_, np.float32)
         np.testing.assert_allclose(g_, w_, rtol=1e-4, atol=1e-4 * np.abs(w_).max())
         assert np.array_equal(g_, r_)
+
+
+@pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,))])
+def test_leading_axis_sums_match_oracle(hip, shape, axes):
+    """float32 sums over leading axes (the vectorized reduce kernel: four columns a thread, 64-row chunks
+    added atomically; 4100 columns is not a multiple of 4 x 256 threads) against the oracle's sequential sum
+    (float32 reassociation: rtol 1e-4 of the sum of magnitudes)."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(shape).astype(np.float32)
+
+    def fn(x):
+        return F.sum(x * 2.0, dim=axes)
+
+    f = L.compile(fn, device="hip")
+    got = np.asarray(L.to_numpy(f(L.from_numpy(x))), np.float32)
+    assert "reduce" in [s["kind"] for s in f.plan.describe()]
+    (want,) = oracle.values(L.make_graph(fn)(L.from_numpy(x)), [x])
+    scale = np.abs(x * 2.0).sum(axis=axes)
+    assert np.all(np.abs(got - want) <= 1e-4 * scale + 1e-6)
+
+
+def test_softmax_gradient_joins_its_statistics_row_kernel(hip):
+    """Cross entropy forward + backward over [rows, classes] logits: the backward's softmax-minus-one-hot
+    loop is absorbed into the forward's max/sum-exp row kernel (one launch reads the logits once), and the
+    loss and logits gradient match the oracle (float32: rtol 1e-4)."""
+    rng = np.random.default_rng(4)
+    rows, classes = 512, 3000
+    x = rng.standard_normal((rows, classes)).astype(np.float32)
+    t = rng.integers(0, classes, rows).astype(np.int64)
+
+    def fn(x, t):
+        return L.value_and_grad(lambda x: F.mean(F.cross_entropy(x, t)))(x)
+
+    f = L.compile(fn, device="hip")
+    loss, dx = f(L.from_numpy(x), L.from_numpy(t))
+    writers = [s.kind for s in f.plan.steps if any(f.plan.graph.types[v].shape == (rows, classes) for v in s.outputs)]
+    assert writers == ["row"], writers
+    want = oracle.values(L.make_graph(fn)(L.from_numpy(x), L.from_numpy(t)), [x, t])
+    np.testing.assert_allclose(float(L.to_numpy(loss)), float(want[0]), rtol=1e-4)
+    np.testing.assert_allclose(np.asarray(L.to_numpy(dx), np.float32), want[1], rtol=1e-4, atol=1e-4 * np.abs(want[1]).max())

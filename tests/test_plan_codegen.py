@@ -129,3 +129,15 @@ def test_small_independent_loops_share_one_launch():
     assert k.grid[0] == sum(m.grid[0] for m in k.parts) and len(k.args) == 6
     big = _plan(lambda a, b: (a * 2.0, b + 1.0), ((2048, 1024), "float32"), ((2048, 1024), "float32"))
     assert [s.kind for s in big.steps] == ["loop", "loop"]
+
+
+def test_loop_over_a_row_space_joins_the_row_kernel():
+    """Softmax statistics (a row kernel) and an elementwise consumer of the same rows reading only the
+    row kernel's input, its per-row results and values already in memory: one row kernel writing both."""
+    def fn(x, t):
+        return L.value_and_grad(lambda x: F.mean(F.cross_entropy(x, t)))(x)
+
+    p = _plan(fn, ((512, 3000), "float32"), ((512,), "int64"))
+    big = [s for s in p.steps if s.outputs and p.graph.types[s.outputs[0]].numel() == 512 * 3000
+           or any(p.graph.types[v].numel() == 512 * 3000 for v in s.outputs)]
+    assert [s.kind for s in big] == ["row"], [(s.kind, s.label()) for s in p.steps]
