@@ -302,7 +302,9 @@ class Plan:
                 live[v] = (off, size)
                 self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
             if st.kind == "dot":
-                st.splits = 1 if getattr(st, "epi", None) is not None else self._split_count(st.nodes[0])
+                st.splits, split_cfg = (1, None) if getattr(st, "epi", None) is not None else self._split_count(st.nodes[0])
+                if split_cfg is not None:
+                    st.config = split_cfg
                 if st.splits > 1:
                     d, _ = self._gemm_desc(st.nodes[0])
                     st.scratch = st.splits * max(1, math.prod(d.batch[i] for i in range(d.nbatch))) * d.m * d.n * 4
@@ -731,23 +733,30 @@ class Plan:
     # powers of two, each part at least 1024 deep) until they do; its float32 partials live in the step's
     # scratch (nhip_gemm_splitk).
     SPLIT_MIN_K = 1024
+    SPLIT_MAX = 8
+    STREAM128 = 9  # kernels.hip's kStream128
 
     def _split_count(self, n):
         lhs, rhs, out = self.loc[n.inputs[0]], self.loc[n.inputs[1]], self.loc[n.output]
         if lhs.dtype not in ("bfloat16", "float16") or rhs.dtype != lhs.dtype:
-            return 1
+            return 1, None
         try:
             d, _ = self._gemm_desc(n)
         except NotImplementedError:
-            return 1
+            return 1, None
         if not _mfma_layout(d) or any((loc.offset * D.size_of(loc.dtype)) % 16 for loc in (lhs, rhs)):
-            return 1
+            return 1, None
         z = max(1, math.prod(d.batch[i] for i in range(d.nbatch)))
         tiles = -(-d.m // 256) * -(-d.n // 256) * z
+        if tiles >= 256:
+            return 1, None
+        # the 128 x 128 kernel runs two workgroups a CU: split until its tiles fill 2 x 256 of them
+        tiles = -(-d.m // 128) * -(-d.n // 128) * z
         s = 1
-        while tiles * s * 2 <= 256 and d.k % (64 * s * 2) == 0 and d.k // (s * 2) >= self.SPLIT_MIN_K:
+        while (tiles * s * 2 <= 512 and s < self.SPLIT_MAX and d.k % (64 * s * 2) == 0
+               and d.k // (s * 2) >= self.SPLIT_MIN_K):
             s *= 2
-        return s
+        return s, (self.STREAM128 if s > 1 else None)
 
     def run_in(self, workspace_ptr: int, input_ptrs: list):
         """Queues the plan on the stream: inputs are device pointers in graph-input order. The first run

@@ -241,7 +241,11 @@ int gemm_splitk_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const
     p.d_split = stride;
     int rc;
     bool f16 = d->a_dtype == NHIP_F16;
-#define NHIP_SPLIT(FF, AA, BB) rc = launch_stream<FF, 64, 4, AA, BB>(st, p, z, a, b, ws, NHIP_F32, d->splits)
+    // the partial products come from the 128 x 128 streamed kernel when the caller picked it (config 9), else
+    // from the 256 x 256 one
+#define NHIP_SPLIT(FF, AA, BB)                                                                      \
+    rc = d->config == kStream128 ? launch_stream128<FF, AA, BB>(st, p, z, a, b, ws, NHIP_F32, d->splits) \
+                                 : launch_stream<FF, 64, 4, AA, BB>(st, p, z, a, b, ws, NHIP_F32, d->splits)
     if (f16) {
         if (at) { if (bt) NHIP_SPLIT(true, true, true); else NHIP_SPLIT(true, true, false); }
         else { if (bt) NHIP_SPLIT(true, false, true); else NHIP_SPLIT(true, false, false); }

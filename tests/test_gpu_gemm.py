@@ -85,9 +85,11 @@ def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
 
 @pytest.mark.parametrize("at,bt,splits,out", [(True, True, 4, nv.NHIP_BF16), (False, True, 2, nv.NHIP_F32),
                                               (True, False, 8, nv.NHIP_F16)])
-def test_gemm_splitk(hip, at, bt, splits, out):
+@pytest.mark.parametrize("config", [-1, 9])
+def test_gemm_splitk(hip, at, bt, splits, out, config):
     """Split-k (the weight-gradient shape: small output, deep k): partial products in the workspace, summed in
-    split order; two batches, ragged m and n."""
+    split order; two batches, ragged m and n; partials from the 256 x 256 streamed kernel (default) and from
+    the 128 x 128 one (config 9)."""
     rng = np.random.default_rng(splits)
     z, m, n, k = 2, 264, 200, 64 * splits * 3
     a = D.bf16_bits(rng.standard_normal((z, m, k)).astype(np.float32))
@@ -100,6 +102,7 @@ def test_gemm_splitk(hip, at, bt, splits, out):
     desc = _desc(m, n, k, 1 if at else k, m if at else 1, n if bt else 1, 1 if bt else k, out=out,
                  batch=(z,), sa=(m * k,), sb=(n * k,), sd=(m * n,))
     desc.splits = splits
+    desc.config = config
     ws = C.c_size_t()
     nv.call("nhip_gemm_workspace", C.byref(desc), C.byref(ws))
     assert ws.value == splits * z * m * n * 4
