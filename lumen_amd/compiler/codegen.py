@@ -20,6 +20,7 @@ Kernels:
 from __future__ import annotations
 
 import math
+import re
 import struct
 
 from lumen_amd import dtypes as D
@@ -58,6 +59,27 @@ DEV float ro_f32(double x) {
   if (!isfinite(f) || (double)f == x || (b & 1u)) return f;
   bool outward = ((double)f < x) != (f < 0.0f || (f == 0.0f && signbit(f)));
   return __uint_as_float(outward ? b + 1u : b - 1u);
+}
+// tanh in float32: below 0.55 in magnitude the odd Taylor series of tanh through x^19 (Horner in x^2; the
+// first omitted term is under 2^-27 of the value), above it sign(x) (1 - 2 / (2^(2|x| log2 e) + 1)) on the
+// hardware exp2 and reciprocal (2^... overflows to inf past |x| = 44, giving +-1; NaN propagates). Within 2 ulp
+// of the exact value with correctly rounded exp2 and division (checked over [2^-31, 12] on the host).
+DEV float tanh_f32(float x) {
+  const float ax = fabsf(x);
+  if (ax < 0.55f) {
+    const float x2 = x * x;
+    float p = fmaf(x2, -2.3912911e-4f, 5.9002744e-4f);
+    p = fmaf(x2, p, -1.4558344e-3f);
+    p = fmaf(x2, p, 3.5921280e-3f);
+    p = fmaf(x2, p, -8.8632355e-3f);
+    p = fmaf(x2, p, 2.1869488e-2f);
+    p = fmaf(x2, p, -5.3968254e-2f);
+    p = fmaf(x2, p, 1.3333334e-1f);
+    p = fmaf(x2, p, -3.3333334e-1f);
+    return copysignf(fmaf(x * x2, p, x), x);  // keeps the sign of -0
+  }
+  const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * ax);
+  return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), x);
 }
 DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
@@ -325,7 +347,9 @@ class Emitter:
             }.get(p)
             s = "f" if f32 else ""
             one = "1.0f" if f32 else "1.0"
-            if p == "logistic":
+            if p == "tanh" and f32:
+                expr = f"tanh_f32({a})"
+            elif p == "logistic":
                 expr = f"{one} / ({one} + exp{s}(-{a}))"
             elif p == "rsqrt":
                 expr = f"{one} / sqrt{s}({a})"
@@ -1065,13 +1089,33 @@ class GemmEpilogueKernel:
         shape = (f"s.m = {d.m}LL; s.n = {d.n}LL; s.k = {d.k}LL; s.nbatch = 0; s.a_m = {d.a_m}LL; "
                  f"s.a_k = {d.a_k}LL; s.b_k = {d.b_k}LL; s.b_n = {d.b_n}LL; s.d_m = {d.n}LL; s.d_n = 1; "
                  f"s.tiles_m = {-(-d.m // 256)}; s.tiles_n = {-(-d.n // 256)}; s.d_split = 0;")
+        # the vector loads of the other operands move into load(): gemm.h issues them ahead of the sums' staging
+        pre_fields, pre_loads, pre_uses, rest = [], [], [], []
+        for l in pro:
+            m = re.match(r"const ((?:u16v|u32v|u64v)<\d+>) (\w+) = (.*);$", l)
+            if m:
+                pre_fields.append(f"{m.group(1)} {m.group(2)};")
+                pre_loads.append(f"p.{m.group(2)} = {m.group(3)};")
+                pre_uses.append(f"const {m.group(1)} {m.group(2)} = pre.{m.group(2)};")
+            else:
+                rest.append(l)
+        # chunks read ahead at a time: at most 64 VGPRs of 16-byte loads
+        ahead = 16
+        while ahead > 1 and ahead * len(pre_fields) > 16:
+            ahead //= 2
         lines = [
             '#include "gemm.h"',
             "struct EpiKNAME {",
             *["  " + f for f in fields],
-            "  __device__ __forceinline__ void operator()(int64_t r, int64_t c, float4 acc) const {",
+            f"  static constexpr int kPrefetch = {ahead};",
+            "  struct Pre {", *["    " + f for f in pre_fields], "  };",
+            "  __device__ __forceinline__ Pre load(int64_t r, int64_t c) const {",
             f"    const int64_t base = r * {n}LL + c;",
-            *["    " + l for l in pro + body + stores],
+            "    Pre p;", *["    " + l for l in pre_loads], "    return p;",
+            "  }",
+            "  __device__ __forceinline__ void operator()(int64_t r, int64_t c, float4 acc, const Pre &pre) const {",
+            f"    const int64_t base = r * {n}LL + c;",
+            *["    " + l for l in pre_uses + rest + body + stores],
             "  }",
             "};",
             f'extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) '

@@ -410,9 +410,26 @@ __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyS
     }
 }
 
+// Writes the float32 sums of a wave's 64-row half `half` (MFMA tiles 2 half and 2 half + 1) to its LDS stage:
+// acc[i][j][e] is row 32 i + l32, column 32 j + 8 (e / 4) + 4 h + e % 4 of the wave's block.
+template <int FM, int FN, int PITCH>
+__device__ __forceinline__ void stage_acc(const f32x16_t (&acc)[FM][FN], int half, char *stage, int l32, int h) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * half + ii;
+        const int r = 32 * ii + l32;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4)
+                *reinterpret_cast<float4 *>(stage + r * PITCH + (32 * j + 8 * e4 + 4 * h) * 4) =
+                    make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
+    }
+}
+
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
-// functor called as out(row, col, float4) with the float32 sums of four consecutive columns (col a multiple
-// of 4; columns at or past n are the functor's to skip). `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
+// functor called as out(row, col, float4, pre) with the float32 sums of four consecutive columns (col a
+// multiple of 4, within m x n) and pre = out.load(row, col), its other operands read ahead. `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
 template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
@@ -582,28 +599,41 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     constexpr int PITCH = gemm_stream_stage_pitch<WN, TM>();
     __syncthreads();  // operand stages are dead: reuse LDS for the output
     char *stage = smem + wave * (64 * PITCH);
+    // a generated epilogue reads its other operands with Out::load(row, col) into Out::Pre, kPrefetch chunks of
+    // four columns at a time: the first group's loads are issued before the sums are staged, so their latency
+    // overlaps the staging and the barrier instead of stalling every chunk
+    constexpr int CPR = WCOLS / 4;  // four-column chunks a wave row; a lane takes CPR of the 64 x CPR chunks a half
 #pragma unroll
     for (int half = 0; half < FM / 2; ++half) {
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const int i = 2 * half + ii;
-            const int r = 32 * ii + l32;
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int e4 = 0; e4 < 4; ++e4)
-                    *reinterpret_cast<float4 *>(stage + r * PITCH + (32 * j + 8 * e4 + 4 * h) * 4) =
-                        make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
-        }
-        __syncthreads();
         if constexpr (std::is_same<Out, AnyStore>::value) {
+            stage_acc<FM, FN, PITCH>(acc, half, stage, l32, h);
+            __syncthreads();
             stream_store_rows<WCOLS, PITCH>(s, out, od, stage, rbase + 64 * half, cbase, lane);
         } else {
-            // four consecutive columns a lane, WCOLS / 4 lanes a row
-            for (int idx = lane; idx < 64 * (WCOLS / 4); idx += 64) {
-                const int r = idx / (WCOLS / 4), ch = idx % (WCOLS / 4);
-                const int64_t gr = rbase + 64 * half + r, gc = cbase + 4 * ch;
-                if (gr < s.m && gc < s.n) out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16));
+            constexpr int G = Out::kPrefetch < CPR ? Out::kPrefetch : CPR;
+            static_assert(CPR % G == 0, "prefetch groups must divide a lane's chunks");
+            typename Out::Pre pre[G];
+            auto fetch = [&](int g0) {
+#pragma unroll
+                for (int q = 0; q < G; ++q) {
+                    const int idx = lane + 64 * (g0 + q);
+                    const int64_t gr = rbase + 64 * half + idx / CPR, gc = cbase + 4 * (idx % CPR);
+                    if (gr < s.m && gc < s.n) pre[q] = out.load(gr, gc);
+                }
+            };
+            fetch(0);
+            stage_acc<FM, FN, PITCH>(acc, half, stage, l32, h);
+            __syncthreads();
+#pragma unroll
+            for (int g0 = 0; g0 < CPR; g0 += G) {
+                if (g0) fetch(g0);
+#pragma unroll
+                for (int q = 0; q < G; ++q) {
+                    const int idx = lane + 64 * (g0 + q);
+                    const int r = idx / CPR, ch = idx % CPR;
+                    const int64_t gr = rbase + 64 * half + r, gc = cbase + 4 * ch;
+                    if (gr < s.m && gc < s.n) out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16), pre[q]);
+                }
             }
         }
         __syncthreads();

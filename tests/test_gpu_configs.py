@@ -172,3 +172,20 @@ def test_softmax_gradient_joins_its_statistics_row_kernel(hip):
     want = oracle.values(L.make_graph(fn)(L.from_numpy(x), L.from_numpy(t)), [x, t])
     np.testing.assert_allclose(float(L.to_numpy(loss)), float(want[0]), rtol=1e-4)
     np.testing.assert_allclose(np.asarray(L.to_numpy(dx), np.float32), want[1], rtol=1e-4, atol=1e-4 * np.abs(want[1]).max())
+
+
+def test_float32_tanh_is_within_4_ulp(hip):
+    """The generated kernels' float32 tanh (odd series below 0.55, exp2/reciprocal form above) against float64
+    tanh rounded to float32 over a log-spaced sweep of both signs, with zeros, infinities and NaN: at most 4
+    ulp, and the special values exact."""
+    mags = np.logspace(-30, 1.7, 200001).astype(np.float32)
+    x = np.concatenate([mags, -mags, np.float32([0.0, -0.0, np.inf, -np.inf, np.nan, 0.55, -0.55, 44.0, 100.0])])
+    f = L.compile(lambda x: F.tanh(x), device="hip")
+    got = np.asarray(L.to_numpy(f(L.from_numpy(x))), np.float32)
+    want = np.tanh(x.astype(np.float64))
+    fin = np.isfinite(x)
+    ulp = np.spacing(np.abs(want[fin]).astype(np.float32)).astype(np.float64)
+    err = np.abs(got[fin].astype(np.float64) - want[fin]) / ulp
+    assert err.max() <= 4.0, (err.max(), x[fin][err.argmax()])
+    assert got[-7] == 1.0 and got[-6] == -1.0 and np.isnan(got[-5])
+    assert np.array_equal(np.signbit(got[-9:-7]), [False, True]) and np.all(got[-9:-7] == 0)
