@@ -268,8 +268,8 @@ def _inputs_of(nodes):
 def _rematerialize(graph, steps, prod):
     """Recomputes values instead of storing them (``passes/fusion/mod.rs`` duplicates cheap producers the
     same way). A loop or row kernel that reads a value computed elementwise from values already in memory
-    computes it itself, when that adds at most one new operand read (or new operands of at most the replaced
-    value's bytes, or at most 1 MiB): the training graph's backward kernels then recompute an activation's
+    computes it itself, when the new operands it reads hold at most the replaced value's bytes (or at most
+    1 MiB): the training graph's backward kernels then recompute an activation's
     intermediates (GELU's tanh argument and friends) from its input instead of reading them back, and the
     forward kernels stop writing them."""
     in_memory = set(graph.inputs)
@@ -304,19 +304,26 @@ def _rematerialize(graph, steps, prod):
                 if not ok:
                     continue
                 new = [v for v in leaves if v not in st.inputs]
-                if len(new) > 1 and sum(graph.types[v].nbytes() for v in new) > max(graph.types[u].nbytes(), REMAT_SMALL):
-                    continue  # more bytes to read than the value it replaces (small per-row vectors are free)
+                if sum(graph.types[v].nbytes() for v in new) > max(graph.types[u].nbytes(), REMAT_SMALL):
+                    # more bytes to read than the value it replaces (small per-row vectors are free): repeated
+                    # one operand at a time this would unroll a running sum (a residual stream's gradient, bf16)
+                    # into reads of every float32 term
+                    continue
                 have = {m.output for m in st.nodes}
                 st.nodes.extend(m for v, m in expr.items() if v not in have)
                 st.nodes.sort(key=lambda m: m.output)
                 st.inputs = _inputs_of(st.nodes)
                 changed = True
                 break
-    # values nobody reads any more: a kernel stops writing its extra outputs and computing what fed only them
+    return _drop_unread(graph, steps)
+
+
+def _drop_unread(graph, steps):
+    """A loop or row kernel stops writing extra outputs nobody reads any more, and computing what fed only
+    them."""
     read = set(graph.outputs)
     for st in steps:
         read.update(st.inputs)
-    kept = []
     for st in steps:
         if st.kind in ("loop", "row") and len(st.outputs) > 1:
             outs = [st.outputs[0]] + [v for v in st.outputs[1:] if v in read]
@@ -332,8 +339,96 @@ def _rematerialize(graph, steps, prod):
                     stack.extend(by_out[v].inputs)
                 st.nodes = [m for m in st.nodes if m.output in live]
                 st.inputs = _inputs_of(st.nodes)
-        kept.append(st)
-    return kept
+    return steps
+
+
+def _space(graph, st):
+    """The [shape] a loop or row kernel's elementwise outputs share (a flat index of one is an element of
+    the others), or None."""
+    if st.kind == "row":
+        if st.rows is None:
+            return None
+        numel = st.rows[0] * st.rows[1]
+    elif st.kind == "loop" and st.outputs:
+        numel = graph.types[st.outputs[0]].numel()
+    else:
+        return None
+    shapes = {graph.types[v].shape for v in st.outputs if graph.types[v].numel() == numel}
+    return next(iter(shapes)) if len(shapes) == 1 else None
+
+
+def hoist_to_producers(graph, steps):
+    """Moves an elementwise expression out of a kernel into the earlier loop or row kernel that writes the
+    last of its operands, when the kernel then reads less: it reads the expression's value instead of its
+    operands, and the producer computes it in its own pass over the same elements. A running sum whose only
+    reader is a late kernel (a bf16 residual stream's gradient, summed term by term over the layers) becomes
+    one term added per producer instead of every float32 term held in memory and read at the end."""
+    def nbytes(v):
+        return graph.types[v].nbytes()
+
+    moved = True
+    while moved:
+        moved = False
+        pos, readers = {}, {}
+        for si, st in enumerate(steps):
+            for v in st.outputs:
+                pos[v] = si
+            for u in st.inputs:
+                readers.setdefault(u, set()).add(si)
+        outputs = set(graph.outputs)
+        for ki, kt in enumerate(steps):
+            if kt.kind not in ("loop", "row"):
+                continue
+            inner = {m.output: m for m in kt.nodes}
+            users = {}
+            for m in kt.nodes:
+                for u in m.inputs:
+                    users.setdefault(u, set()).add(m.output)
+            for n in kt.nodes:
+                if n.prim not in ELEMENTWISE:
+                    continue
+                # n and the kernel's elementwise nodes feeding only it; leaves are the kernel's inputs
+                tree, leaves, stack, ok = {n.output}, set(), list(n.inputs), True
+                while stack and ok:
+                    u = stack.pop()
+                    m = inner.get(u)
+                    if m is None:
+                        leaves.add(u)
+                    elif m.prim in ELEMENTWISE and users.get(u, set()) <= tree and u not in kt.outputs:
+                        tree.add(u)
+                        stack.extend(m.inputs)
+                    else:
+                        ok = False
+                shape = graph.types[n.output].shape
+                if not ok or not leaves or any(graph.types[u].shape != shape for u in leaves):
+                    continue
+                if any(u not in pos and u not in graph.inputs for u in leaves):
+                    continue
+                pi = max(pos.get(u, -1) for u in leaves)
+                if pi < 0 or pi >= ki or _space(graph, steps[pi]) != shape:
+                    continue
+                pt = steps[pi]
+                saved = sum(nbytes(u) for u in leaves if users[u] <= tree)
+                have = set(pt.inputs) | {m.output for m in pt.nodes}
+                extra = sum(nbytes(u) for u in leaves if u not in have)
+                freed = sum(nbytes(u) for u in leaves if pos.get(u) == pi and users[u] <= tree
+                            and readers.get(u, set()) == {ki} and u not in outputs)
+                if saved - nbytes(n.output) + freed <= extra + nbytes(n.output):
+                    continue
+                moving = [m for m in kt.nodes if m.output in tree]
+                kt.nodes = [m for m in kt.nodes if m.output not in tree]
+                if n.output in kt.outputs:
+                    kt.outputs = [v for v in kt.outputs if v != n.output]
+                kt.inputs = _inputs_of(kt.nodes)
+                pt.nodes = sorted(pt.nodes + moving, key=lambda m: m.output)
+                pt.outputs = list(pt.outputs) + [n.output]
+                pt.inputs = _inputs_of(pt.nodes)
+                moved = True
+                break
+            if moved:
+                break
+    steps = [st for st in steps if st.kind not in ("loop", "row") or st.outputs]
+    return _drop_unread(graph, steps)
 
 
 def absorb_rows(graph, steps):

@@ -197,6 +197,7 @@ class Plan:
     def _fuse(self):
         steps = fusion.fuse(self.graph, fuse_loops=config.compiler.fuse, packed=self.packed)
         if config.compiler.fuse:
+            steps = fusion.hoist_to_producers(self.graph, steps)
             steps = fusion.absorb_rows(self.graph, steps)
         if config.compiler.fuse and config.compiler.horizontal_fusion:
             steps = fusion.horizontal(self.graph, steps)
