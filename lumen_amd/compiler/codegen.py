@@ -571,6 +571,9 @@ class LoopKernel:
     # another; at 512 threads two rows share a CU and overlap (0.51 -> 0.37 ms for the [8192, 32000]
     # cross-entropy row on MI355X)
     ROW_MAX_THREADS = 512
+    # sums over leading axes: rows a workgroup sums before its atomic adds, and loads a thread keeps in flight
+    LEAD_CHUNK = 128
+    LEAD_UNROLL = 8
 
     def __init__(self, graph, step, name, views: dict, out_views: dict):
         self.graph, self.step, self.name = graph, step, name
@@ -845,7 +848,8 @@ class LoopKernel:
         chunk = max(1, min(Q, 64)) if atomic else Q
         nchunks = -(-Q // chunk)
         if atomic and tuple(axes) == tuple(range(len(axes))) and O % 4 == 0 and O >= 1024:
-            return self._reduce_leading(red, Q, O, chunk, nchunks)
+            chunk = max(1, min(Q, self.LEAD_CHUNK))
+            return self._reduce_leading(red, Q, O, chunk, -(-Q // chunk))
         em = self._emitter()
         om = em.multi(("flat", "o"), oshape)
         qm = em.multi(("flat", "q"), rshape)
@@ -885,9 +889,11 @@ class LoopKernel:
 
 
     def _reduce_leading(self, red, Q, O, chunk, nchunks):
-        """float32 sum over the leading axes of a [Q, O] row-major value (a bias or norm-weight gradient):
-        each thread sums 4 consecutive columns over ``chunk`` rows with 16-byte loads (four rows in flight),
-        then adds them atomically into the zero-filled output."""
+        """float32 sum over the leading axes of a [Q, O] row-major value (a bias or norm-weight gradient): a
+        workgroup covers 256 columns of ``chunk`` rows, each thread 4 consecutive columns (16-byte loads) of
+        every fourth row; the four row lanes combine through LDS and the workgroup adds its 256 sums atomically
+        into the zero-filled output (one atomic a column per chunk: the adds, not the loads, bound this kernel
+        when chunks are short)."""
         g = self.graph
         em = self._emitter()
         em.vec = 4
@@ -897,24 +903,29 @@ class LoopKernel:
         body = self._vec_prologue(em, 4) + em.lines
         self.atomic = True
         threads = 256
-        self.grid, self.block, self.lds = (-(-(O // 4) // threads), nchunks, 1), (threads, 1, 1), 0
+        self.grid, self.block, self.lds = (-(-O // 256), nchunks, 1), (threads, 1, 1), 0
         view = self.out_views[red.output]
         oshape = g.types[red.output].shape
-        adds = [f"atomicAdd(&out0[{self._out_addr(view, oshape, f'(o + {l})')}], acc{l});" for l in range(4)]
+        adds = [f"atomicAdd(&out0[{self._out_addr(view, oshape, f'(o + {l})')}], part[0][tx][{l}] + part[1][tx][{l}]"
+                f" + part[2][tx][{l}] + part[3][tx][{l}]);" for l in range(4)]
         src = [
             f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{',
-            f"  const int64_t o = ((int64_t)blockIdx.x * {threads} + threadIdx.x) * 4;",
-            f"  if (o >= {O}LL) return;",
+            "  __shared__ float part[4][64][4];",
+            "  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;",
+            f"  const int64_t o = ((int64_t)blockIdx.x * 64 + tx) * 4;",
             f"  const int64_t q0 = (int64_t)blockIdx.y * {chunk}LL;",
             f"  const int64_t q1 = min(q0 + {chunk}LL, {Q}LL);",
             "  float acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;",
-            "#pragma unroll 4",
-            "  for (int64_t q = q0; q < q1; ++q) {",
+            f"  if (o < {O}LL) {{",
+            f"#pragma unroll {self.LEAD_UNROLL}",
+            "  for (int64_t q = q0 + ty; q < q1; q += 4) {",
             f"    const int64_t qb = q * {O}LL + o;",
         ]
         src += ["    " + l for l in body]
         src += [f"    acc{l} = ((float)(acc{l} + {vals[l]}));" for l in range(4)]
-        src += ["  }"] + ["  " + a for a in adds] + ["}"]
+        src += ["  }", "  }"]
+        src += [f"  part[ty][tx][{l}] = acc{l};" for l in range(4)]
+        src += ["  __syncthreads();", f"  if (ty == 0 && o < {O}LL) {{"] + ["    " + a for a in adds] + ["  }", "}"]
         return "\n".join(src)
 
 
