@@ -640,6 +640,237 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     }
 }
 
+// Writes a wave's sums straight from the MFMA accumulators: acc[i][j][4 e4 .. 4 e4 + 3] are four consecutive
+// columns of one row, a 16-byte (float32) or 8-byte (16-bit) store when D is row-major with rows a multiple
+// of 4 elements; the L2 merges the 32-byte pieces of a row the wave writes into whole lines. LDS is not used,
+// so the next tile's operands can stream into it meanwhile.
+template <int FM, int FN>
+__device__ __forceinline__ void stream_store_direct(const GemmShape &s, const AnyStore &out, int64_t od,
+                                                    const f32x16_t (&acc)[FM][FN], int64_t rbase, int64_t cbase,
+                                                    int l32, int h) {
+    const int esize = out.dtype == 0 ? 4 : 2;
+    const bool vec = s.d_n == 1 && s.d_m % 4 == 0 && ((reinterpret_cast<uintptr_t>(out.d) + od * esize) & 15) == 0;
+    char *dbase = static_cast<char *>(out.d) + od * esize;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int64_t gr = rbase + 32 * i + l32;
+        if (gr >= s.m) continue;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int64_t gc = cbase + 32 * j + 8 * e4 + 4 * h;
+                const float x0 = acc[i][j][4 * e4], x1 = acc[i][j][4 * e4 + 1], x2 = acc[i][j][4 * e4 + 2],
+                            x3 = acc[i][j][4 * e4 + 3];
+                if (vec && gc + 4 <= s.n) {
+                    char *p = dbase + (gr * s.d_m + gc) * esize;
+                    if (out.dtype == 0)
+                        *reinterpret_cast<float4 *>(p) = make_float4(x0, x1, x2, x3);
+                    else if (out.dtype == 1)
+                        *reinterpret_cast<uint2 *>(p) = make_uint2(uint32_t(f32_to_bf16(x0)) | (uint32_t(f32_to_bf16(x1)) << 16),
+                                                                   uint32_t(f32_to_bf16(x2)) | (uint32_t(f32_to_bf16(x3)) << 16));
+                    else
+                        *reinterpret_cast<uint2 *>(p) = make_uint2(uint32_t(f32_to_f16(x0)) | (uint32_t(f32_to_f16(x1)) << 16),
+                                                                   uint32_t(f32_to_f16(x2)) | (uint32_t(f32_to_f16(x3)) << 16));
+                } else if (gc < s.n) {
+                    const float xs[4] = {x0, x1, x2, x3};
+                    out.visit([&](auto stf) {
+                        for (int e = 0; e < 4 && gc + e < s.n; ++e) stf(s, od, gr, gc + e, xs[e]);
+                    });
+                }
+            }
+    }
+}
+
+// The persistent 256 x 256 streamed GEMM: a workgroup a CU walks tiles blockIdx.x, + gridDim.x, ... and
+// overlaps each tile's end with the next one's start. During a tile's last k step the stage the step does
+// not read fills with the next tile's first k tile, and the sums are stored from registers, so the next
+// tile's first loads are in flight across the last MFMAs and the stores, and no workgroup launches between
+// tiles. Same operand staging, k loop and results as gemm_stream_tile (one batch, one split: z and split-k
+// go through gemm_stream).
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
+__device__ __forceinline__ void gemm_stream_persist_run(const GemmShape &s, const uint16_t *__restrict__ a,
+                                                        const uint16_t *__restrict__ b, const AnyStore &out,
+                                                        char *smem) {
+    constexpr int TM = 256;
+    constexpr int NW = 2 * WN;
+    constexpr int WR = TM / 2;
+    constexpr int FM = WR / 32;
+    constexpr int WCOLS = TM / WN;
+    constexpr int FN = WCOLS / 32;
+    constexpr int STAGES = gemm_stream_stages<BK, TM>();
+    static_assert(STAGES == 2, "the persistent kernel alternates two stages");
+    using TA = StreamTile<BK, AT, TM>;
+    using TB = StreamTile<BK, BT, TM>;
+    constexpr int STAGE_BYTES = TA::bytes + TB::bytes;
+    constexpr int LPS = (TA::segs + TB::segs) / NW;
+    constexpr int NRD = (AT ? 2 * FM : FM) + (BT ? 2 * FN : FN);
+
+    const int ntiles = s.tiles_m * s.tiles_n;
+    int t = blockIdx.x;
+    if (t >= ntiles) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int h = lane >> 5, l32 = lane & 31, g = lane >> 4, s16 = lane & 15;
+    const int64_t od = 0;
+    const uint16_t *pa = a, *pb = b;
+    const int ktiles = int(s.k / BK);
+
+    struct Ctx {
+        int64_t m0, n0;
+        __amdgpu_buffer_rsrc_t rsa, rsb;
+    };
+    auto ctx_of = [&](int tile) {
+        int tm, tn;
+        tile_of(tile, s.tiles_m, s.tiles_n, tm, tn);
+        Ctx c;
+        c.m0 = int64_t(tm) * TM;
+        c.n0 = int64_t(tn) * TM;
+        const int64_t mrem = s.m - c.m0 < TM ? s.m - c.m0 : TM, nrem = s.n - c.n0 < TM ? s.n - c.n0 : TM;
+        const int64_t abytes = AT ? ((s.k - 1) * s.a_k + mrem) * 2 : ((mrem - 1) * s.a_m + s.k) * 2;
+        const int64_t bbytes = BT ? ((s.k - 1) * s.b_k + nrem) * 2 : ((nrem - 1) * s.b_n + s.k) * 2;
+        c.rsa = __builtin_amdgcn_make_buffer_rsrc((void *)(AT ? pa + c.m0 : pa + c.m0 * s.a_m), (short)0,
+                                                  int(abytes), 0x00020000);
+        c.rsb = __builtin_amdgcn_make_buffer_rsrc((void *)(BT ? pb + c.n0 : pb + c.n0 * s.b_n), (short)0,
+                                                  int(bbytes), 0x00020000);
+        return c;
+    };
+    auto issue = [&](const Ctx &c, int st, int kt, int lo, int hi) {
+        char *base = smem + st * STAGE_BYTES;
+        const int64_t k0 = int64_t(kt) * BK;
+#pragma unroll
+        for (int i = 0; i < TA::segs / NW; ++i) {
+            if (i < lo || i >= hi) continue;
+            const int seg = wave + NW * i;
+            const int line = seg * TA::lines_per_seg + lane / TA::chunks, ch = lane % TA::chunks;
+            if constexpr (BUF) {
+                const uint32_t vo = AT ? uint32_t((line * s.a_k + ((ch ^ mnmaj_swz(line)) << 3)) * 2)
+                                       : uint32_t((line * s.a_m + ((ch ^ kmaj_swz<BK>(line)) << 3)) * 2);
+                const uint32_t so = AT ? uint32_t(k0 * s.a_k * 2) : uint32_t(k0 * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsa, (glds_void_t *)(base + seg * 1024), 16, vo, so, 0, 0);
+                continue;
+            }
+            const uint16_t *src;
+            if (AT) {
+                int64_t mm = c.m0 + ((ch ^ mnmaj_swz(line)) << 3);
+                mm = mm < s.m ? mm : s.m - 8;
+                src = pa + (k0 + line) * s.a_k + mm;
+            } else {
+                int64_t mm = c.m0 + line;
+                mm = mm < s.m ? mm : s.m - 1;
+                src = pa + mm * s.a_m + k0 + ((ch ^ kmaj_swz<BK>(line)) << 3);
+            }
+            __builtin_amdgcn_global_load_lds(src, (glds_void_t *)(base + seg * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < TB::segs / NW; ++i) {
+            if (TA::segs / NW + i < lo || TA::segs / NW + i >= hi) continue;
+            const int seg = wave + NW * i;
+            const int line = seg * TB::lines_per_seg + lane / TB::chunks, ch = lane % TB::chunks;
+            if constexpr (BUF) {
+                const uint32_t vo = BT ? uint32_t((line * s.b_k + ((ch ^ mnmaj_swz(line)) << 3)) * 2)
+                                       : uint32_t((line * s.b_n + ((ch ^ kmaj_swz<BK>(line)) << 3)) * 2);
+                const uint32_t so = BT ? uint32_t(k0 * s.b_k * 2) : uint32_t(k0 * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rsb, (glds_void_t *)(base + TA::bytes + seg * 1024), 16, vo, so, 0, 0);
+                continue;
+            }
+            const uint16_t *src;
+            if (BT) {
+                int64_t nn = c.n0 + ((ch ^ mnmaj_swz(line)) << 3);
+                nn = nn < s.n ? nn : s.n - 8;
+                src = pb + (k0 + line) * s.b_k + nn;
+            } else {
+                int64_t nn = c.n0 + line;
+                nn = nn < s.n ? nn : s.n - 1;
+                src = pb + nn * s.b_n + k0 + ((ch ^ kmaj_swz<BK>(line)) << 3);
+            }
+            __builtin_amdgcn_global_load_lds(src, (glds_void_t *)(base + TA::bytes + seg * 1024), 16, 0, 0);
+        }
+    };
+    auto frag = [&](const char *tile, int r0, int kk, auto tr) -> uint4 {
+        if constexpr (decltype(tr)::value) {
+            const int kl = kk + 8 * h + s16 / 4;
+            const int mn = r0 + 16 * (g & 1) + 4 * (s16 & 3);
+            const char *p0 = tile + kl * (TM * 2) + (((mn >> 3) ^ mnmaj_swz(kl)) << 4) + ((mn & 7) << 1);
+            const char *p1 = tile + (kl + 4) * (TM * 2) + (((mn >> 3) ^ mnmaj_swz(kl + 4)) << 4) + ((mn & 7) << 1);
+            gv4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p0));
+            gv4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((glds_v4i16_t *)(p1));
+            uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+            return make_uint4(xa.x, xa.y, ya.x, ya.y);
+        } else {
+            const int r = r0 + l32;
+            return *reinterpret_cast<const uint4 *>(tile + r * (BK * 2) + ((((kk >> 3) + h) ^ kmaj_swz<BK>(r)) << 4));
+        }
+    };
+
+    Ctx cur = ctx_of(t);
+    int stage = 0;  // stage holding the current k tile
+    issue(cur, 0, 0, 0, LPS);
+    for (;;) {
+        const int tnext = t + int(gridDim.x);
+        const bool has_next = tnext < ntiles;
+        const Ctx nxt = ctx_of(has_next ? tnext : t);
+        f32x16_t acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int kt = 0; kt < ktiles; ++kt) {
+            // every load of this thread has landed (the previous tile's stores count too: vmcnt holds both)
+            __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);
+            __syncthreads();  // all threads' loads of this k tile landed; the other stage is free
+            const bool more = kt + 1 < ktiles;
+            const bool prefetch = !more && has_next;
+            const char *ta = smem + stage * STAGE_BYTES;
+            const char *tb = ta + TA::bytes;
+            uint4 fa[2][FM], fb[2][FN];
+            auto read = [&](int bsel, int kk) {
+                fa[bsel][0] = frag(ta, wm * WR, kk, std::integral_constant<bool, AT>{});
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[bsel][j] = frag(tb, wn * WCOLS + 32 * j, kk, std::integral_constant<bool, BT>{});
+#pragma unroll
+                for (int i = 1; i < FM; ++i) fa[bsel][i] = frag(ta, wm * WR + 32 * i, kk, std::integral_constant<bool, AT>{});
+            };
+            read(0, 0);
+            auto step = [&](auto kkc) {
+                constexpr int kk = decltype(kkc)::value;
+                constexpr int cb = (kk / 16) & 1;
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (kk + 16 < BK) read(cb ^ 1, kk + 16);
+                constexpr int lo = (kk / 16) * LPS * 16 / BK, hi = (kk / 16 + 1) * LPS * 16 / BK;
+                if (more) issue(cur, stage ^ 1, kt + 1, lo, hi);
+                else if (prefetch) issue(nxt, stage ^ 1, 0, lo, hi);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<F16>::run(fb[cb][j], fa[cb][i], acc[i][j]);
+                if constexpr (kk + 16 < BK) mfma_ds_interleave<0, FM * FN, NRD, kk / 16 + 1>();
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 16>{});
+            if constexpr (BK > 32) {
+                step(std::integral_constant<int, 32>{});
+                step(std::integral_constant<int, 48>{});
+            }
+            stage ^= 1;
+        }
+        stream_store_direct<FM, FN>(s, out, od, acc, cur.m0 + wm * WR, cur.n0 + wn * WCOLS, l32, h);
+        if (!has_next) break;
+        t = tnext;
+        cur = nxt;
+    }
+}
+
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
+__global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream_persist(
+    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
+    extern __shared__ __align__(1024) char smem[];
+    gemm_stream_persist_run<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
+}
+
 template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
 __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {

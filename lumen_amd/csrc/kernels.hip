@@ -27,10 +27,11 @@ constexpr TileConfig kConfigs[] = {
 constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // Configs past the tiled ones: gemm_stream (256 x 256, operands streamed into LDS): k tile 64 with 4 waves of
 // 128 x 128 (2 stages) and with 8 waves of 128 x 64 (2 stages); k tile 32 with 8 waves (4 stages); and
-// gemm_stream128 (128 x 128 tiles, 4 waves of 64 x 64, 2 stages, two workgroups a CU).
+// gemm_stream128 (128 x 128 tiles, 4 waves of 64 x 64, 2 stages, two workgroups a CU); and
+// gemm_stream_persist (the 8-wave 256 x 256 kernel, one persistent workgroup a CU walking the tiles).
 constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
-              kStream128 = kNumTiled + 3;
-constexpr int kNumConfigs = kNumTiled + 4;
+              kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4;
+constexpr int kNumConfigs = kNumTiled + 5;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -167,6 +168,51 @@ int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const v
     return launch_stream_kernel<F16, BK, WN, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
 }
 
+// CUs of the current device (the persistent kernel's grid), asked once per device
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <bool F16, bool AT, bool BT, bool BUF>
+int launch_stream_persist_kernel(hipStream_t st, const GemmShape &s, const void *a, const void *b, void *out,
+                                 int dtype) {
+    constexpr int lds = gemm_stream_stages<64, 256>() * 2 * 256 * 64 * 2;
+    auto kern = gemm_stream_persist<F16, 64, 4, AT, BT, BUF>;
+    static bool attr = false;
+    if (!attr) {
+        if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                  "hipFuncSetAttribute"))
+            return 1;
+        attr = true;
+    }
+    const int tiles = s.tiles_m * s.tiles_n;
+    const int cus = device_cus();
+    dim3 grid(tiles < cus ? tiles : cus, 1, 1);
+    hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, s, static_cast<const uint16_t *>(a),
+                       static_cast<const uint16_t *>(b), AnyStore{out, dtype});
+    return check(hipGetLastError(), "gemm_stream_persist launch");
+}
+
+// One batch: the persistent kernel; batched dots take the one-workgroup-a-tile kernel
+template <bool F16, bool AT, bool BT>
+int launch_stream_persist(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype) {
+    if (z != 1) return launch_stream<F16, 64, 4, AT, BT>(st, s, z, a, b, out, dtype);
+    s.tiles_m = int((s.m + 255) / 256);
+    s.tiles_n = int((s.n + 255) / 256);
+    if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
+        return launch_stream_persist_kernel<F16, AT, BT, true>(st, s, a, b, out, dtype);
+    return launch_stream_persist_kernel<F16, AT, BT, false>(st, s, a, b, out, dtype);
+}
+
+
 template <bool F16, bool AT, bool BT>
 int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype) {
     switch (cfg) {
@@ -174,6 +220,7 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream8w: return launch_stream<F16, 64, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8w32: return launch_stream<F16, 32, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
+        case kStreamPersist: return launch_stream_persist<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case 1: return launch_mfma_cfg<F16, 256, 128, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
         case 2: return launch_mfma_cfg<F16, 128, 256, 64, 2, 2, AT, BT>(st, s, z, a, b, out, dtype);
@@ -276,7 +323,8 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
-        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128) && d->k % 64) || (cfg == kStream8w32 && d->k % 32))
+        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist) && d->k % 64) ||
+            (cfg == kStream8w32 && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
         return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);

@@ -29,7 +29,7 @@ def _desc(m, n, k, a_m, a_k, b_k, b_n, dt=nv.NHIP_BF16, out=nv.NHIP_F32, cfg=-1,
 @pytest.mark.parametrize(
     "m,n,k,cfg",
     [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0), (520, 264, 192, 6), (264, 776, 128, 7),
-     (264, 136, 96, 8), (200, 392, 192, 9)],
+     (264, 136, 96, 8), (200, 392, 192, 9), (520, 776, 192, 10)],
 )
 def test_gemm_layouts(hip, at, bt, m, n, k, cfg):
     """A as [m][k] or [k][m] in memory, B as [n][k] or [k][n]: float32 results within float32 rounding of
@@ -61,7 +61,7 @@ def test_gemm_batched_bf16_output(hip):
 
 
 @pytest.mark.parametrize("cfg,out", [(6, nv.NHIP_BF16), (7, nv.NHIP_F16), (7, nv.NHIP_F32), (8, nv.NHIP_BF16),
-                                     (9, nv.NHIP_BF16), (9, nv.NHIP_F32)])
+                                     (9, nv.NHIP_BF16), (9, nv.NHIP_F32), (10, nv.NHIP_BF16)])
 def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
     """The streamed kernels' LDS-staged row stores (256 x 256 tiles, configs 6-8; 128 x 128, config 9):
     16-bit and float32 outputs, m and n not multiples of the tile, two batches."""
@@ -79,6 +79,34 @@ def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
         assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
     else:
         raw = dd.get((z, m, n), np.uint16)
+        got = D.bf16_to_f32(raw) if out == nv.NHIP_BF16 else raw.view(np.float16).astype(np.float32)
+        np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("m,n,k,at,bt,out", [(4300, 4400, 128, False, False, nv.NHIP_F32),
+                                              (4352, 4401, 64, True, False, nv.NHIP_BF16),
+                                              (4400, 4352, 192, False, True, nv.NHIP_F16),
+                                              (4352, 4352, 128, True, True, nv.NHIP_BF16)])
+def test_gemm_persistent_walks_every_tile(hip, m, n, k, at, bt, out):
+    """The persistent 256 x 256 kernel (config 10) with more tiles than CUs, so each workgroup runs several
+    and prefetches the next one's first k tile during its last: ragged m and n, a single k tile (k = 64),
+    every layout, stores from registers as 16-byte / 8-byte vectors and, for a row length that is not a
+    multiple of 4 (n = 4401), element by element."""
+    rng = np.random.default_rng(m + n + k)
+    a = D.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    b = D.bf16_bits(rng.standard_normal((k, n)).astype(np.float32))
+    want = D.bf16_to_f32(a).astype(np.float64) @ D.bf16_to_f32(b).astype(np.float64)
+    am = np.ascontiguousarray(a.T) if at else a
+    bm = b if bt else np.ascontiguousarray(b.T)
+    es = 4 if out == nv.NHIP_F32 else 2
+    da, db, dd = Dev(am), Dev(bm), Dev(nbytes=m * n * es)
+    desc = _desc(m, n, k, 1 if at else k, m if at else 1, n if bt else 1, 1 if bt else k, out=out, cfg=10)
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    if out == nv.NHIP_F32:
+        got = dd.get((m, n), np.float32)
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
+    else:
+        raw = dd.get((m, n), np.uint16)
         got = D.bf16_to_f32(raw) if out == nv.NHIP_BF16 else raw.view(np.float16).astype(np.float32)
         np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
 
