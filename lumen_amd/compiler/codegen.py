@@ -41,12 +41,9 @@ HEADER = r"""
 #include <math.h>
 #define DEV __device__ __forceinline__
 DEV float lb_bf16(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
-DEV uint16_t sb_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
+// float32 -> bfloat16 round to nearest even, NaN -> (bits >> 16) | 0x40: gfx950's v_cvt_pk_bf16_f32, equal to
+// that integer rounding on all 2^32 float32 inputs (checked on MI355X)
+DEV uint16_t sb_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 DEV float r_bf16(float f) { return lb_bf16(sb_bf16(f)); }
 DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }

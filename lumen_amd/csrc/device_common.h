@@ -22,14 +22,11 @@ struct f16_t {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 
-// float32 -> bfloat16, round to nearest even; NaN stays a quiet NaN of its sign. A float32 value is the
-// exact value here, so this is the reference's one correct rounding (lumen/tensor/dtype.rs:215-239).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
-}
+// float32 -> bfloat16, round to nearest even; a NaN keeps its sign and top payload bits with the quiet bit
+// set. A float32 value is the exact value here, so this is the reference's one correct rounding
+// (lumen/tensor/dtype.rs:215-239). gfx950's conversion instruction (v_cvt_pk_bf16_f32) does exactly this: on
+// MI355X it equals the integer form (u + 0x7fff + lsb) >> 16, NaN -> (u >> 16) | 0x40, on all 2^32 inputs.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) {
     _Float16 h = __builtin_bit_cast(_Float16, b);

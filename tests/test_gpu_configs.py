@@ -189,3 +189,22 @@ def test_float32_tanh_is_within_4_ulp(hip):
     assert err.max() <= 4.0, (err.max(), x[fin][err.argmax()])
     assert got[-7] == 1.0 and got[-6] == -1.0 and np.isnan(got[-5])
     assert np.array_equal(np.signbit(got[-9:-7]), [False, True]) and np.all(got[-9:-7] == 0)
+
+
+def test_bf16_stores_round_to_nearest_even_bit_for_bit(hip):
+    """float32 -> bfloat16 in generated kernels (the hardware conversion) against the reference's rounding
+    restated on the host (round to nearest even; NaN -> its top 16 bits with the quiet bit): every tie and
+    half-ulp neighbour of a sweep of exponents, NaN payloads of both signs, infinities, subnormals, the
+    largest finite values, and 2^24 random bit patterns, bit for bit."""
+    rng = np.random.default_rng(12)
+    hi = (np.arange(0, 1 << 16, 7, dtype=np.uint32) << 16)
+    lows = np.uint32([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x4000, 0xC000])
+    grid = (hi[:, None] | lows[None, :]).ravel()
+    special = np.uint32([0x7F800000, 0xFF800000, 0x7F800001, 0xFF800001, 0x7FC00000, 0xFFC00000, 0x7FFFFFFF,
+                         0xFFFFFFFF, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x00000001, 0x80000001, 0x007FFFFF,
+                         0x00008000, 0x00018000, 0x0, 0x80000000])
+    bits = np.concatenate([grid, special, rng.integers(0, 1 << 32, 1 << 24, dtype=np.uint64).astype(np.uint32)])
+    x = bits.view(np.float32)
+    f = L.compile(lambda x: x.bfloat16(), device="hip")
+    got = np.asarray(f(L.from_numpy(x)).raw()).view(np.uint16).ravel()
+    assert np.array_equal(got, D.bf16_bits(x))
