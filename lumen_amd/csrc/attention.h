@@ -338,6 +338,39 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *ls
     }
 }
 
+// The same with 16-byte loads: D / 8 lanes a query row (a wavefront takes 64 / (D / 8) rows), the lanes'
+// products summed in fixed order (each lane's eight, then a butterfly across the lanes of the row). Needs D
+// a multiple of 8 dividing 512 and 16-byte aligned rows (the launcher checks).
+template <int D, bool F16>
+__global__ __launch_bounds__(256) void flash_prep_vec_kernel(AttnParams p, float *lse2) {
+    constexpr int LPR = D / 8;          // lanes a row
+    constexpr int RPB = 256 / LPR;      // rows a workgroup
+    static_assert(D % 8 == 0 && 64 % LPR == 0, "rows must tile a wavefront");
+    const int sub = threadIdx.x % LPR;
+    const int64_t row = int64_t(blockIdx.x) * RPB + threadIdx.x / LPR;
+    const int64_t b = blockIdx.y;
+    const bool live = row < p.heads * p.sq;
+    const int64_t n = live ? row / p.sq : 0, q = live ? row % p.sq : 0;
+    float acc = 0.0f;
+    if (live) {
+        const uint4 ov = *reinterpret_cast<const uint4 *>(p.o_in + b * p.o_b + n * p.o_n + q * p.o_s + 8 * sub);
+        const uint4 gv = *reinterpret_cast<const uint4 *>(p.d_o + b * p.do_b + n * p.do_n + q * p.do_s + 8 * sub);
+        const uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc += half_to_f32<F16>(uint16_t(gw[e] & 0xffffu)) * half_to_f32<F16>(uint16_t(ow[e] & 0xffffu));
+            acc += half_to_f32<F16>(uint16_t(gw[e] >> 16)) * half_to_f32<F16>(uint16_t(ow[e] >> 16));
+        }
+    }
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (live && sub == 0) {
+        const int64_t i = (b * p.heads + n) * p.sq + q;
+        p.delta[i] = acc * p.scale;
+        lse2[i] = p.lse_in[i] * 1.4426950408889634f;
+    }
+}
+
 // Component i (a constant) of a float4.
 __device__ __forceinline__ float f4_at(const float4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
@@ -759,7 +792,21 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
     dim3 gk(unsigned((d->sk + 127) / 128 * d->kv_heads * d->batch));
     dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
     float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
-    hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
+    // 16-byte rows: D / 8 lanes each; else one wavefront a row
+    const bool vec = D % 8 == 0 && 64 % (D / 8 > 0 ? D / 8 : 1) == 0 && D / 8 <= 64 &&
+                     ((reinterpret_cast<uintptr_t>(p.o_in) | reinterpret_cast<uintptr_t>(p.d_o)) & 15) == 0 &&
+                     (p.o_b | p.o_n | p.o_s | p.do_b | p.do_n | p.do_s) % 8 == 0;
+    if constexpr (D % 8 == 0 && D >= 8 && D <= 512 && 64 % (D / 8) == 0) {
+        if (vec) {
+            constexpr int RPB = 256 / (D / 8);
+            dim3 gv(unsigned((d->heads * d->sq + RPB - 1) / RPB), unsigned(d->batch));
+            hipLaunchKernelGGL((nhipk::flash_prep_vec_kernel<D, F16>), gv, dim3(256), 0, s, p, lse2);
+        } else {
+            hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
+        }
+    } else {
+        hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
+    }
     if (check(hipGetLastError(), "flash delta launch")) return 1;
     hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p, lse2);
     if (check(hipGetLastError(), "flash dkdv launch")) return 1;
