@@ -75,6 +75,17 @@ DEV float tanh_f32(float x) {
   const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * ax);
   return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), x);
 }
+// exp in float32: x log2 e split into the rounded product hi and its error lo (fma residual plus x times
+// the low part of log2 e), then 2^hi on the hardware exp2 times (1 + lo ln 2). Within 2 ulp of the exact
+// value for normal results with a correctly rounded exp2 (checked on the host over every 13th float); results
+// below 2^-126 flush to zero; +-inf and NaN map to inf / 0 / NaN.
+DEV float exp_f32(float x) {
+  const float hi = x * 1.4426950216293335f;
+  float lo = fmaf(x, 1.4426950216293335f, -hi) + x * 1.9259629890910901e-08f;
+  lo = __builtin_isinf(x) ? 0.0f : lo;
+  const float r = __builtin_amdgcn_exp2f(hi);
+  return r * fmaf(lo, 0.6931471805599453f, 1.0f);
+}
 DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
 DEV float fmin_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
@@ -343,8 +354,10 @@ class Emitter:
             one = "1.0f" if f32 else "1.0"
             if p == "tanh" and f32:
                 expr = f"tanh_f32({a})"
+            elif p == "exp" and f32:
+                expr = f"exp_f32({a})"
             elif p == "logistic":
-                expr = f"{one} / ({one} + exp{s}(-{a}))"
+                expr = f"{one} / ({one} + {'exp_f32' if f32 else 'exp'}(-{a}))"
             elif p == "rsqrt":
                 expr = f"{one} / sqrt{s}({a})"
             else:
@@ -717,6 +730,8 @@ class LoopKernel:
             rows_per_block = 1
         J = -(-chunks // T)
         exact = C % (T * V) == 0
+        # column indices in 32 bits when the row allows (they stay live across the row's passes)
+        cty, csuf = ("int", "") if C < (1 << 31) else ("int64_t", "LL")
         em = self._emitter(rows=(R, C))
         # C % V == 0, so a V-element chunk is wholly inside the row or wholly past it: past-the-end chunks load
         # the row's last chunk (a clamped base keeps vector loads in bounds) and are masked out of reductions
@@ -738,7 +753,7 @@ class LoopKernel:
                     cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
                     cidx = f"c{j}_{lane}"
                     if cidx not in _declared(em):
-                        em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
+                        em.emit(f"const {cty} {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}{csuf})'};")
                         _declared(em).add(cidx)
                     idx = ("rc", "r", cidx, vbase(j), lane)
                     val = em.value(red.inputs[0], idx)
@@ -773,7 +788,7 @@ class LoopKernel:
                 cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
                 cidx = f"c{j}_{lane}"
                 if cidx not in _declared(em):
-                    em.emit(f"const int64_t {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}LL)'};")
+                    em.emit(f"const {cty} {cidx} = {'' if exact else 'min('}{cexpr}{'' if exact else f', {C - 1}{csuf})'};")
                     _declared(em).add(cidx)
                 idx = ("rc", "r", cidx, vbase(j), lane)
                 lanes.append([em.value(v, idx) for v in outs_elem])
@@ -791,7 +806,7 @@ class LoopKernel:
                     )
                 if not exact:
                     s = f"if ((({j} * {T} + tid) * {V}) < {C}LL) {{ {s} }}"
-                stores.append(s)
+                em.emit(s)  # stored as soon as computed: a chunk's results are not held across the row
         for v in outs_row:
             oi = st.outputs.index(v)
             val = em.value(v, ("r", "r"))
@@ -818,7 +833,7 @@ class LoopKernel:
             ]
         src += ["  (void)lane; (void)wave;"]
         # vector loads need the c indices declared before them: emit prologue after index decls
-        decl = [l for l in body if l.startswith("const int64_t c") and "(( " not in l]
+        decl = [l for l in body if (l.startswith("const int64_t c") or l.startswith("const int c")) and "(( " not in l]
         rest = [l for l in body if l not in decl]
         src += ["  " + l for l in decl + pro + rest + stores]
         src += ["}"]

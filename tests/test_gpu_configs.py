@@ -208,3 +208,21 @@ def test_bf16_stores_round_to_nearest_even_bit_for_bit(hip):
     f = L.compile(lambda x: x.bfloat16(), device="hip")
     got = np.asarray(f(L.from_numpy(x)).raw()).view(np.uint16).ravel()
     assert np.array_equal(got, D.bf16_bits(x))
+
+
+def test_float32_exp_is_within_4_ulp(hip):
+    """The generated kernels' float32 exp (compensated x log2 e, hardware exp2) against float64 exp over a
+    sweep of [-87.3, 88.7] (normal results): at most 4 ulp; below that results are within 2^-126 of exact
+    (flushed), above it inf, and exp(-inf) = 0, exp(inf) = inf, exp(NaN) = NaN."""
+    x = np.concatenate([np.linspace(-87.3, 88.7, 400001, dtype=np.float32),
+                        np.float32([-1e-30, 0.0, -0.0, 1e-30, -100.0, -104.0, 89.0, -np.inf, np.inf, np.nan])])
+    f = L.compile(lambda x: F.exp(x), device="hip")
+    got = np.asarray(L.to_numpy(f(L.from_numpy(x))), np.float64)
+    want = np.exp(x.astype(np.float64))
+    n = 400001
+    ulp = np.spacing(want[:n].astype(np.float32)).astype(np.float64)
+    err = np.abs(got[:n] - want[:n]) / ulp
+    assert err.max() <= 4.0, (err.max(), x[:n][err.argmax()])
+    assert np.array_equal(got[n:n + 4], [1.0, 1.0, 1.0, 1.0])
+    assert np.all(np.abs(got[n + 4:n + 6] - want[n + 4:n + 6]) <= 2.0 ** -126)
+    assert got[n + 6] == np.inf and got[n + 7] == 0.0 and got[n + 8] == np.inf and np.isnan(got[n + 9])
