@@ -160,6 +160,31 @@ int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, con
                    const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace);
 int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes);
 
+/* ---- linear cross entropy (Primitive::LinearCrossEntropy, lumen/reference/mod.rs:1092-1120; the Triton kernel
+ * lumen/codegen/dot_general/triton/linear_cross_entropy_kernel.py; the pass that emits it,
+ * lumen/graph_compiler/passes/linear_cross_entropy.rs) ---------------------------------------------------- *
+ *
+ * h [b, d] and w [v, d] row-major (both bf16, both f16, or both float32), target [b] int32 or int64 (as
+ * target_dtype NHIP_LCE_I32 / NHIP_LCE_I64). out is float32 [2, b]: row 0 the loss lse - logit[class], row 1
+ * lse = max + log(sum_j exp(logit_j - max)), class = target clamped into [0, v). The float32 logits of
+ * chunk_rows rows at a time go through `workspace` (nhip_linear_cross_entropy_workspace bytes: chunk_rows * v
+ * float32) by nhip_gemm, then one workgroup a row reduces them (maximum, float64 sum of exponentials, picked
+ * logit), so the [b, v] logits never exist whole. */
+enum {
+    NHIP_LCE_I32 = 0,
+    NHIP_LCE_I64 = 1,
+};
+typedef struct {
+    int64_t b, v, d;
+    int64_t chunk_rows;  /* rows a pass; <= 0: all b */
+    int32_t dtype;       /* NHIP_BF16, NHIP_F16 or NHIP_F32 */
+    int32_t target_dtype;
+} nhip_lce_desc;
+
+int nhip_linear_cross_entropy(const nhip_lce_desc *desc, const void *h, const void *w, const void *target, float *out,
+                              void *workspace);
+int nhip_linear_cross_entropy_workspace(const nhip_lce_desc *desc, size_t *bytes);
+
 /* ---- static plans (lumen/plan/run.rs:356-427 execute; lumen/plan/step/cuda.rs:17-63) ----------------- *
  *
  * A plan is a list of steps run in order on the stream: generated kernels (a function of a loaded module)
@@ -187,6 +212,7 @@ enum {
     NHIP_STEP_FLASH_BWD = 3,  /* desc: nhip_attn_desc; pointers: q, k, v, o, do, lse, dq, dk, dv, ws */
     NHIP_STEP_COPY = 4,       /* desc: uint64 bytes; pointers: dst, src */
     NHIP_STEP_FILL = 5,       /* desc: uint64 bytes, uint32 byte value; pointers: dst */
+    NHIP_STEP_LCE = 6,        /* desc: nhip_lce_desc; pointers: h, w, target, out, workspace */
 };
 
 int nhip_plan_create(void **plan);

@@ -309,6 +309,8 @@ class Plan:
                 if st.splits > 1:
                     d, _ = self._gemm_desc(st.nodes[0])
                     st.scratch = st.splits * max(1, math.prod(d.batch[i] for i in range(d.nbatch))) * d.m * d.n * 4
+            if st.kind == "linear_cross_entropy":
+                st.scratch = self._lce_desc(st.nodes[0]).chunk_rows * g.types[st.nodes[0].inputs[1]].shape[0] * 4
             if st.scratch:
                 off, size = take(st.scratch)
                 self.scratch[id(st)] = Loc(("ws", 0), off // 4, (1,), "float32", (st.scratch // 4,))
@@ -613,6 +615,12 @@ class Plan:
                 kind, desc, ops = attn_pass.lower(self, st)
                 rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
                 call("nhip_plan_add_builtin", plan, kind, C.byref(desc), C.sizeof(desc), rr, len(ops))
+            elif st.kind == "linear_cross_entropy":
+                n = st.nodes[0]
+                desc = self._lce_desc(n)
+                ops = [self.loc[u] for u in n.inputs] + [self.loc[n.output], self.scratch[id(st)]]
+                rr = (nv.Reloc * len(ops))(*[reloc(i, l) for i, l in enumerate(ops)])
+                call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_LCE, C.byref(desc), C.sizeof(desc), rr, len(ops))
             elif st.kind == "copy":
                 src, dst = self._copies[si]
                 desc = struct.pack("<Q", g.types[st.outputs[0]].nbytes())
@@ -683,6 +691,30 @@ class Plan:
         d.a_m, d.a_k, d.b_k, d.b_n, d.d_m, d.d_n = a_m, a_k, b_k, b_n, d_m, d_n
         d.config = -1
         return d, [lhs, rhs, out]
+
+    # Linear cross entropy (Primitive::LinearCrossEntropy, lumen/reference/mod.rs:1092-1120): nhip_gemm writes the
+    # float32 logits of LCE_SCRATCH bytes' worth of rows at a time into the step's scratch, a row kernel reduces
+    # them; the [b, v] logits never exist whole.
+    LCE_SCRATCH = 512 << 20
+
+    def _lce_desc(self, n):
+        from lumen_amd import native as nv
+
+        g = self.graph
+        h, w, t = (g.types[u] for u in n.inputs)
+        for u in n.inputs:
+            if not self.loc[u].contiguous():
+                raise NotImplementedError("linear_cross_entropy of strided operands: the hip backend has no kernel for it yet")
+        if h.dtype != w.dtype or h.dtype not in NHIP_DT or t.dtype not in ("int32", "int64"):
+            raise NotImplementedError(f"linear_cross_entropy of {h.dtype}, {w.dtype}, {t.dtype}: the hip backend has no "
+                                      "kernel for it yet")
+        d = nv.LceDesc()
+        d.b, d.d = h.shape
+        d.v = w.shape[0]
+        d.chunk_rows = max(1, min(d.b, self.LCE_SCRATCH // max(1, d.v * 4)))
+        d.dtype = NHIP_DT[h.dtype]
+        d.target_dtype = nv.NHIP_LCE_I64 if t.dtype == "int64" else nv.NHIP_LCE_I32
+        return d
 
     # ---- autotuning (lumen/autotune/mod.rs:20-150): bf16/f16 dots of at least 2^30 multiply-adds try every tile
     # config the kernel accepts, timed with HIP events on the step's own operands (their values do not change

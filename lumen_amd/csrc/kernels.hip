@@ -358,6 +358,81 @@ int fill_on(hipStream_t st, void *dst, size_t bytes, unsigned char value) {
     return check(hipGetLastError(), "fill launch");
 }
 
+// ---- linear cross entropy (lumen/reference/mod.rs:1092-1120) ---------------------------------------------
+
+// One workgroup a row of float32 logits [rows, v]: the maximum, the float64 sum of exp(logit - max) (each term
+// in float64, as the reference evaluates it), lse = max + log(sum) rounded to float32, and the loss lse minus
+// the logit of the clamped class, rounded once. out[r0 + row] = loss, out[b + r0 + row] = lse.
+__global__ __launch_bounds__(256) void lce_rows_kernel(const float *__restrict__ logits, int64_t v,
+                                                       const void *__restrict__ target, int t64,
+                                                       float *__restrict__ out, int64_t b, int64_t r0) {
+    __shared__ float smax[4];
+    __shared__ double ssum[4];
+    const int64_t row = blockIdx.x;
+    const float *x = logits + row * v;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float m = -INFINITY;
+    for (int64_t j = tid; j < v; j += 256) m = fmaxf(m, x[j]);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) smax[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    double sum = 0.0;
+    for (int64_t j = tid; j < v; j += 256) sum += exp(double(x[j]) - double(m));
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) ssum[wave] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        sum = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
+        const int64_t t = t64 ? static_cast<const int64_t *>(target)[r0 + row] : static_cast<const int32_t *>(target)[r0 + row];
+        const int64_t cls = t < 0 ? 0 : (t >= v ? v - 1 : t);
+        const float l = float(double(m) + log(sum));
+        out[r0 + row] = float(double(l) - double(x[cls]));
+        out[b + r0 + row] = l;
+    }
+}
+
+int64_t lce_chunk(const nhip_lce_desc *d) {
+    return d->chunk_rows <= 0 || d->chunk_rows > d->b ? d->b : d->chunk_rows;
+}
+
+int lce_on(hipStream_t st, const nhip_lce_desc *d, const void *h, const void *w, const void *target, float *out,
+           void *ws) {
+    if (d->b < 0 || d->v < 1 || d->d < 0) return fail("nhip_linear_cross_entropy: needs b >= 0, v >= 1, d >= 0");
+    if (d->dtype != NHIP_F32 && d->dtype != NHIP_BF16 && d->dtype != NHIP_F16)
+        return fail("nhip_linear_cross_entropy: h and w must be float32, bf16 or f16");
+    if (d->target_dtype != NHIP_LCE_I32 && d->target_dtype != NHIP_LCE_I64)
+        return fail("nhip_linear_cross_entropy: targets must be int32 or int64");
+    if (d->b == 0) return 0;
+    if (!ws) return fail("nhip_linear_cross_entropy: no workspace");
+    const int64_t chunk = lce_chunk(d);
+    const int64_t esize = d->dtype == NHIP_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < d->b; r0 += chunk) {
+        const int64_t rows = d->b - r0 < chunk ? d->b - r0 : chunk;
+        nhip_gemm_desc g;
+        std::memset(&g, 0, sizeof(g));
+        g.m = rows;
+        g.n = d->v;
+        g.k = d->d;
+        g.a_dtype = g.b_dtype = d->dtype;
+        g.d_dtype = NHIP_F32;
+        g.a_m = d->d;  // h rows
+        g.a_k = 1;
+        g.b_k = 1;     // w [v, d]: B[k][n] = w[n * d + k]
+        g.b_n = d->d;
+        g.d_m = d->v;
+        g.d_n = 1;
+        g.config = -1;
+        g.splits = 1;
+        if (int rc = gemm_on(st, &g, static_cast<const char *>(h) + r0 * d->d * esize, w, ws)) return rc;
+        if (rows > 0x7fffffff) return fail("nhip_linear_cross_entropy: more than 2^31 rows a chunk");
+        hipLaunchKernelGGL(lce_rows_kernel, dim3(unsigned(rows)), dim3(256), 0, st, static_cast<const float *>(ws),
+                           d->v, target, int(d->target_dtype == NHIP_LCE_I64), out, d->b, r0);
+        if (int rc = check(hipGetLastError(), "lce_rows_kernel launch")) return rc;
+    }
+    return 0;
+}
+
 }  // namespace nhip
 
 using namespace nhip;
@@ -383,6 +458,18 @@ int nhip_gemm_splitk(const nhip_gemm_desc *desc, const void *a, const void *b, v
 
 int nhip_gemm_workspace(const nhip_gemm_desc *desc, size_t *bytes) {
     *bytes = splitk_workspace_bytes(desc);
+    return 0;
+}
+
+int nhip_linear_cross_entropy(const nhip_lce_desc *desc, const void *h, const void *w, const void *target, float *out,
+                              void *workspace) {
+    hipStream_t s = stream_of_current();
+    if (!s) return fail("no HIP stream: call nhip_set_device first");
+    return lce_on(s, desc, h, w, target, out, workspace);
+}
+
+int nhip_linear_cross_entropy_workspace(const nhip_lce_desc *desc, size_t *bytes) {
+    *bytes = desc->b > 0 && desc->v > 0 ? size_t(lce_chunk(desc)) * size_t(desc->v) * 4 : 0;
     return 0;
 }
 

@@ -24,5 +24,7 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
 int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v,
                  const void *o, const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *ws);
 int fill_on(hipStream_t s, void *dst, size_t bytes, unsigned char value);
+int lce_on(hipStream_t s, const nhip_lce_desc *d, const void *h, const void *w, const void *target, float *out,
+           void *ws);
 
 }  // namespace nhip

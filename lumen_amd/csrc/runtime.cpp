@@ -470,7 +470,7 @@ int nhip_plan_add_launch(void *plan, void *function, const uint32_t grid[3], con
 
 int nhip_plan_add_builtin(void *plan, int kind, const void *desc, size_t desc_bytes, const nhip_reloc *relocs,
                           size_t nrelocs) {
-    if (kind < NHIP_STEP_GEMM || kind > NHIP_STEP_FILL) return fail("nhip_plan_add_builtin: unknown step kind");
+    if (kind < NHIP_STEP_GEMM || kind > NHIP_STEP_LCE) return fail("nhip_plan_add_builtin: unknown step kind");
     if (check_relocs(relocs, nrelocs, 16, false)) return 1;
     Step s;
     s.kind = kind;
@@ -606,6 +606,10 @@ static int run_steps(Plan *plan, void *workspace, void *const *inputs, size_t ni
                 if (n) rc = check(hipMemcpyAsync(ptrs[0], ptrs[1], n, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
                 break;
             }
+            case NHIP_STEP_LCE:
+                rc = lce_on(s, reinterpret_cast<const nhip_lce_desc *>(st.args.data()), ptrs[0], ptrs[1], ptrs[2],
+                            static_cast<float *>(ptrs[3]), ptrs[4]);
+                break;
             case NHIP_STEP_FILL: {
                 uint64_t n;
                 uint32_t v;

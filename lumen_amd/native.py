@@ -16,7 +16,8 @@ _lib = None
 
 NHIP_F32, NHIP_BF16, NHIP_F16 = 0, 1, 2
 NHIP_BASE_WORKSPACE, NHIP_BASE_INPUT = 0, 1
-NHIP_STEP_GEMM, NHIP_STEP_FLASH_FWD, NHIP_STEP_FLASH_BWD, NHIP_STEP_COPY, NHIP_STEP_FILL = 1, 2, 3, 4, 5
+NHIP_STEP_GEMM, NHIP_STEP_FLASH_FWD, NHIP_STEP_FLASH_BWD, NHIP_STEP_COPY, NHIP_STEP_FILL, NHIP_STEP_LCE = 1, 2, 3, 4, 5, 6
+NHIP_LCE_I32, NHIP_LCE_I64 = 0, 1
 
 
 class Props(C.Structure):
@@ -56,6 +57,13 @@ class GemmDesc(C.Structure):
         ("config", C.c_int32),
         ("splits", C.c_int32),
     ]
+
+
+class LceDesc(C.Structure):
+    """``nhip_lce_desc``: linear cross entropy of h [b, d] and w [v, d] (include/nhip.h)."""
+
+    _fields_ = [("b", C.c_int64), ("v", C.c_int64), ("d", C.c_int64), ("chunk_rows", C.c_int64),
+                ("dtype", C.c_int32), ("target_dtype", C.c_int32)]
 
 
 class AttnDesc(C.Structure):
@@ -112,6 +120,9 @@ SIGNATURES = {
     "nhip_gemm_config_count": ([C.POINTER(C.c_int)], C.c_int),
     "nhip_gemm_splitk": ([C.POINTER(GemmDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "nhip_gemm_workspace": ([C.POINTER(GemmDesc), C.POINTER(C.c_size_t)], C.c_int),
+    "nhip_linear_cross_entropy": ([C.POINTER(LceDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+                                  C.c_int),
+    "nhip_linear_cross_entropy_workspace": ([C.POINTER(LceDesc), C.POINTER(C.c_size_t)], C.c_int),
     "nhip_flash_fwd": ([C.POINTER(AttnDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "nhip_flash_bwd": (
         [C.POINTER(AttnDesc)] + [C.c_void_p] * 10,

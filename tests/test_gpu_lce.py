@@ -1,0 +1,80 @@
+"""The fused linear cross entropy (Primitive::LinearCrossEntropy, lumen/reference/mod.rs:1092-1120) on the GPU:
+loss and log-sum-exp rows of h [b, d] . w [v, d]^T without the [b, v] logits, against the oracle."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import lumen_amd as L
+from lumen_amd import dtypes as D
+from lumen_amd import native as nv
+from lumen_amd.compiler.plan import Plan
+from lumen_amd.graph import prims
+from oracle import oracle
+from tests.hiputil import Dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(h, w, t, hdt):
+    args = [L.tensor(D.bf16_to_f32(h) if hdt == "bfloat16" else h, hdt),
+            L.tensor(D.bf16_to_f32(w) if hdt == "bfloat16" else w, hdt), L.from_numpy(t)]
+    f = L.compile(lambda h, w, t: prims.linear_cross_entropy(h, w, t), device="hip")
+    got = np.asarray(L.to_numpy(f(*args)), np.float32)
+    assert [s["kind"] for s in f.plan.describe()] == ["linear_cross_entropy"]
+    (want,) = oracle.values(L.make_graph(lambda h, w, t: prims.linear_cross_entropy(h, w, t))(*args), [h, w, t])
+    return got, np.asarray(want, np.float32), f
+
+
+@pytest.mark.parametrize("b,v,d", [(64, 1000, 96), (37, 4097, 64)])
+def test_float32_loss_and_lse_are_within_an_ulp(hip, b, v, d):
+    """float32 h and w: the logits are the reference's sequential k fold (the exact GEMM), the sum of
+    exponentials float64 like the reference's; loss and lse agree with the oracle to 1 ulp (the float64 exp
+    and log of two libms may differ in the last bits)."""
+    rng = np.random.default_rng(b + v)
+    h = rng.standard_normal((b, d)).astype(np.float32)
+    w = rng.standard_normal((v, d)).astype(np.float32) * 0.2
+    t = rng.integers(0, v, b).astype(np.int32)
+    got, want, _ = _run(h, w, t, "float32")
+    assert got.shape == (2, b)
+    ulp = np.spacing(np.abs(want))
+    assert np.all(np.abs(got - want) <= ulp), np.abs(got - want).max()
+
+
+def test_bf16_with_clamped_int64_targets_and_chunks(hip, monkeypatch):
+    """bf16 operands (MFMA logits, float32 accumulation), int64 targets below 0 and past v (clamped to the
+    first and last class, like the reference), and a scratch so small that the rows go in 13-row chunks with
+    a ragged last one: float32 tolerance (rtol 1e-4 of the row's scale) against the oracle."""
+    monkeypatch.setattr(Plan, "LCE_SCRATCH", 13 * 3000 * 4)
+    rng = np.random.default_rng(5)
+    b, v, d = 200, 3000, 128
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.1).astype(np.float32))
+    t = rng.integers(-5, v + 5, b).astype(np.int64)
+    t[:3] = [-7, v, v + 100]
+    got, want, f = _run(h, w, t, "bfloat16")
+    assert f.plan._lce_desc(f.plan.steps[0].nodes[0]).chunk_rows == 13
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+
+
+def test_c_abi_matches_plan(hip):
+    """nhip_linear_cross_entropy through the C ABI (workspace from nhip_linear_cross_entropy_workspace, two
+    chunks) against the compiled plan (one chunk): the same float32 values up to the GEMM tile the row
+    count selects (rtol 1e-5)."""
+    rng = np.random.default_rng(8)
+    b, v, d = 96, 2048, 64
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.1).astype(np.float32))
+    t = rng.integers(0, v, b).astype(np.int32)
+    want, _, _ = _run(h, w, t, "bfloat16")
+    desc = nv.LceDesc()
+    desc.b, desc.v, desc.d, desc.chunk_rows = b, v, d, 50
+    desc.dtype, desc.target_dtype = nv.NHIP_BF16, nv.NHIP_LCE_I32
+    ws = C.c_size_t()
+    nv.call("nhip_linear_cross_entropy_workspace", C.byref(desc), C.byref(ws))
+    assert ws.value == 50 * v * 4
+    dh, dw, dt, do, dws = Dev(h), Dev(w), Dev(t), Dev(nbytes=2 * b * 4), Dev(nbytes=ws.value)
+    nv.call("nhip_linear_cross_entropy", C.byref(desc), dh.ptr, dw.ptr, dt.ptr, do.ptr, dws.ptr)
+    got = do.get((2, b), np.float32)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())

@@ -141,3 +141,19 @@ def test_loop_over_a_row_space_joins_the_row_kernel():
     big = [s for s in p.steps if s.outputs and p.graph.types[s.outputs[0]].numel() == 512 * 3000
            or any(p.graph.types[v].numel() == 512 * 3000 for v in s.outputs)]
     assert [s.kind for s in big] == ["row"], [(s.kind, s.label()) for s in p.steps]
+
+
+def test_linear_cross_entropy_is_a_builtin_step_with_bounded_scratch(monkeypatch):
+    """Primitive::LinearCrossEntropy lowers to one built-in step whose scratch holds a chunk of float32 logit
+    rows (Plan.LCE_SCRATCH bytes at most), not the whole [b, v]."""
+    from lumen_amd.compiler.plan import Plan
+    from lumen_amd.graph import prims
+
+    monkeypatch.setattr(Plan, "LCE_SCRATCH", 1 << 20)
+    h = L.empty([4096, 256], "bfloat16", "meta")
+    w = L.empty([32000, 256], "bfloat16", "meta")
+    t = L.empty([4096], "int64", "meta")
+    p = Plan(L.make_graph(lambda h, w, t: prims.linear_cross_entropy(h, w, t))(h, w, t), build_kernels=False)
+    assert [s.kind for s in p.steps] == ["linear_cross_entropy"]
+    d = p._lce_desc(p.steps[0].nodes[0])
+    assert d.chunk_rows == (1 << 20) // (32000 * 4) and p.steps[0].scratch == d.chunk_rows * 32000 * 4
