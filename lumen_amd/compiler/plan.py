@@ -154,12 +154,15 @@ def _reshape_strides(shape, strides, new):
 
 def compile_graph(graph: Graph, packable=()) -> tuple[Graph, list]:
     """The hip pipeline (``graph_compiler/pipeline.rs:162-320`` picks): frontend (cse, simplify), flash
-    attention forward and backward matching, merge_dots over the weights at input positions ``packable``,
+    attention forward and backward matching, linear cross entropy, merge_dots over the weights at input
+    positions ``packable``,
     simplify again. Returns the graph and merge_dots' packs (weight input positions stored back to back)."""
     g = passes.frontend(graph)
     if config.compiler.flash_attention:
         g = attn_pass.match(g)
         g = passes.frontend(g)
+    if config.compiler.fuse and config.compiler.fused_linear_cross_entropy:
+        g = passes.linear_cross_entropy(g)  # after the attention passes, as the reference orders it
     packs = []
     if config.compiler.merge_dots and packable:
         g, packs = merge.merge_dots(g, set(packable))

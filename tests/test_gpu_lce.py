@@ -78,3 +78,24 @@ def test_c_abi_matches_plan(hip):
     nv.call("nhip_linear_cross_entropy", C.byref(desc), dh.ptr, dw.ptr, dt.ptr, do.ptr, dws.ptr)
     got = do.get((2, b), np.float32)
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_compiled_eval_loss_uses_the_fused_step(hip):
+    """mean(cross_entropy(h . w^T, t)) compiled for hip: the linear_cross_entropy pass (on by default) turns it
+    into the fused step, and the loss equals the oracle's on the unfused graph within float32 tolerance."""
+    import lumen_amd.functional as F
+
+    def fn(h, w, t):
+        return F.mean(F.cross_entropy(F.matmul(h, w.t(), "float32", "float32"), t))
+
+    rng = np.random.default_rng(21)
+    b, v, d = 512, 5000, 256
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.05).astype(np.float32))
+    t = rng.integers(0, v, b).astype(np.int64)
+    args = [L.tensor(D.bf16_to_f32(h), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(t)]
+    f = L.compile(fn, device="hip")
+    got = float(L.to_numpy(f(*args)))
+    assert "linear_cross_entropy" in [s["kind"] for s in f.plan.describe()]
+    (want,) = oracle.values(L.make_graph(fn)(*args), [h, w, t])
+    np.testing.assert_allclose(got, float(want), rtol=1e-4)

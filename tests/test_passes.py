@@ -135,3 +135,55 @@ def test_merge_dots_packs_projections_and_their_gradients():
     for a, b in zip(oracle.run(g0, xs), oracle.run(g1, xs)):
         np.testing.assert_allclose(np.asarray(a, np.float64), np.asarray(b, np.float64), rtol=1e-5,
                                    atol=1e-5 * max(1.0, float(np.abs(a).max())))
+
+
+def _eval_ce(h, w, t):
+    return F.mean(F.cross_entropy(F.matmul(h, w.t(), "float32", "float32"), t))
+
+
+def test_linear_cross_entropy_pass_rewrites_an_eval_loss_and_keeps_its_value():
+    """A cross entropy whose logits only it reads becomes one linear_cross_entropy node (the weight's
+    transpose folded away); the oracle gives the same loss on both graphs (float32 rounding of the sums:
+    the fused op sums exponentials in float64, the unfused graph in float32)."""
+    from lumen_amd.compiler import passes
+    from oracle import oracle
+
+    rng = np.random.default_rng(3)
+    b, v, d = 48, 300, 40
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.3).astype(np.float32))
+    t = rng.integers(0, v, b).astype(np.int64)
+    args = [L.tensor(D.bf16_to_f32(h), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(t)]
+    g = passes.frontend(L.make_graph(_eval_ce)(*args))
+    g2 = passes.linear_cross_entropy(g)
+    prims_ = [n.prim for n in g2.nodes]
+    assert "linear_cross_entropy" in prims_ and "dot_general" not in prims_ and "transpose" not in prims_
+    (a,) = oracle.run(g, [h, w, t])
+    (b_,) = oracle.run(g2, [h, w, t])
+    np.testing.assert_allclose(b_, a, rtol=1e-6)
+
+
+def test_linear_cross_entropy_pass_leaves_a_training_step():
+    """With the gradient the backward reads the logits, so nothing is rewritten (as in the reference)."""
+    from lumen_amd.compiler import passes
+
+    h = L.empty([16, 8], "bfloat16", "meta")
+    w = L.empty([40, 8], "bfloat16", "meta")
+    t = L.empty([16], "int32", "meta")
+    g = passes.frontend(L.make_graph(lambda h, w, t: L.value_and_grad(lambda h: _eval_ce(h, w, t))(h))(h, w, t))
+    assert all(n.prim != "linear_cross_entropy" for n in passes.linear_cross_entropy(g).nodes)
+
+
+def test_linear_cross_entropy_through_the_pipeline():
+    """Through compile_graph (simplify twice, attention matching) the eval loss still becomes the fused
+    step: the row max may reach the log-sum-exp without its reshape."""
+    from lumen_amd.compiler.plan import Plan
+
+    h = L.empty([512, 256], "bfloat16", "meta")
+    w = L.empty([5000, 256], "bfloat16", "meta")
+    t = L.empty([512], "int64", "meta")
+    p = Plan(L.make_graph(_eval_ce)(h, w, t), build_kernels=False)
+    assert [s.kind for s in p.steps][0] == "linear_cross_entropy"
+    with L.config.compiler.patch(fused_linear_cross_entropy=False):
+        p = Plan(L.make_graph(_eval_ce)(h, w, t), build_kernels=False)
+    assert "linear_cross_entropy" not in [s.kind for s in p.steps]
