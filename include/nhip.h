@@ -168,8 +168,8 @@ int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes);
  * target_dtype NHIP_LCE_I32 / NHIP_LCE_I64). out is float32 [2, b]: row 0 the loss lse - logit[class], row 1
  * lse = max + log(sum_j exp(logit_j - max)), class = target clamped into [0, v). The float32 logits of
  * chunk_rows rows at a time go through `workspace` (nhip_linear_cross_entropy_workspace bytes: chunk_rows * v
- * float32) by nhip_gemm, then one workgroup a row reduces them (maximum, float64 sum of exponentials, picked
- * logit), so the [b, v] logits never exist whole. */
+ * float32) by nhip_gemm, then one workgroup a row reduces them (maximum, float32 exponentials summed in
+ * float64, picked logit), so the [b, v] logits never exist whole. */
 enum {
     NHIP_LCE_I32 = 0,
     NHIP_LCE_I64 = 1,

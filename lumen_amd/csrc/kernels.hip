@@ -360,9 +360,30 @@ int fill_on(hipStream_t st, void *dst, size_t bytes, unsigned char value) {
 
 // ---- linear cross entropy (lumen/reference/mod.rs:1092-1120) ---------------------------------------------
 
-// One workgroup a row of float32 logits [rows, v]: the maximum, the float64 sum of exp(logit - max) (each term
-// in float64, as the reference evaluates it), lse = max + log(sum) rounded to float32, and the loss lse minus
-// the logit of the clamped class, rounded once. out[r0 + row] = loss, out[b + r0 + row] = lse.
+// exp(x) for x <= 0 in float32: x log2 e as a rounded product and its fma residual, the hardware exp2 of the
+// product times (1 + residual ln 2); within 2 ulp, results below 2^-126 flushed to zero.
+__device__ __forceinline__ float lce_exp(float x) {
+    const float hi = x * 1.4426950216293335f;
+    float lo = fmaf(x, 1.4426950216293335f, -hi) + x * 1.9259629890910901e-08f;
+    lo = __builtin_isinf(x) ? 0.0f : lo;
+    const float r = __builtin_amdgcn_exp2f(hi);
+    return r * fmaf(lo, 0.6931471805599453f, 1.0f);
+}
+
+// One workgroup a row of float32 logits [rows, v], read once: each thread keeps a running maximum and the
+// float64 sum of exp(logit - that maximum) (four float32 terms at a time), rescaled when the maximum grows; the
+// threads' sums are rescaled to
+// the row maximum and added in float64 (float32 exponentials within 2 ulp where the reference takes float64
+// ones). lse = max + log(sum) rounded to float32; the loss is lse minus the logit of the clamped class,
+// rounded once. out[r0 + row] = loss, out[b + r0 + row] = lse. 16-byte loads when rows are a multiple of 4.
+__device__ __forceinline__ void lce_add(float x, float &m, double &sum) {
+    if (x > m) {  // a new running maximum: earlier terms scale by exp(m - x) (0 when m is -inf)
+        sum *= double(lce_exp(m - x));
+        m = x;
+    }
+    sum += double(lce_exp(x - m));
+}
+
 __global__ __launch_bounds__(256) void lce_rows_kernel(const float *__restrict__ logits, int64_t v,
                                                        const void *__restrict__ target, int t64,
                                                        float *__restrict__ out, int64_t b, int64_t r0) {
@@ -372,13 +393,35 @@ __global__ __launch_bounds__(256) void lce_rows_kernel(const float *__restrict__
     const float *x = logits + row * v;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = -INFINITY;
-    for (int64_t j = tid; j < v; j += 256) m = fmaxf(m, x[j]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if (lane == 0) smax[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
     double sum = 0.0;
-    for (int64_t j = tid; j < v; j += 256) sum += exp(double(x[j]) - double(m));
+    if ((v & 3) == 0) {
+        auto add4 = [&](const float4 &q) {
+            const float mq = fmaxf(fmaxf(q.x, q.y), fmaxf(q.z, q.w));
+            if (mq > m) {  // one rescale for four logits
+                sum *= double(lce_exp(m - mq));
+                m = mq;
+            }
+            // four float32 terms (each at most 1) summed in float32, then added in float64
+            sum += double((lce_exp(q.x - m) + lce_exp(q.y - m)) + (lce_exp(q.z - m) + lce_exp(q.w - m)));
+        };
+        int64_t j = 4 * tid;
+        for (; j + 3 * 1024 < v; j += 4 * 1024) {  // four loads in flight before any is used
+            float4 q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) q[u] = *reinterpret_cast<const float4 *>(x + j + u * 1024);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) add4(q[u]);
+        }
+        for (; j < v; j += 1024) add4(*reinterpret_cast<const float4 *>(x + j));
+    } else {
+        for (int64_t j = tid; j < v; j += 256) lce_add(x[j], m, sum);
+    }
+    float rm = m;
+    for (int o = 32; o > 0; o >>= 1) rm = fmaxf(rm, __shfl_xor(rm, o, 64));
+    if (lane == 0) smax[wave] = rm;
+    __syncthreads();
+    rm = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    sum = m == -INFINITY ? 0.0 : sum * double(lce_exp(m - rm));
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
     if (lane == 0) ssum[wave] = sum;
     __syncthreads();
@@ -386,7 +429,7 @@ __global__ __launch_bounds__(256) void lce_rows_kernel(const float *__restrict__
         sum = ((ssum[0] + ssum[1]) + ssum[2]) + ssum[3];
         const int64_t t = t64 ? static_cast<const int64_t *>(target)[r0 + row] : static_cast<const int32_t *>(target)[r0 + row];
         const int64_t cls = t < 0 ? 0 : (t >= v ? v - 1 : t);
-        const float l = float(double(m) + log(sum));
+        const float l = float(double(rm) + log(sum));
         out[r0 + row] = float(double(l) - double(x[cls]));
         out[b + r0 + row] = l;
     }

@@ -28,10 +28,10 @@ def _run(h, w, t, hdt):
 
 
 @pytest.mark.parametrize("b,v,d", [(64, 1000, 96), (37, 4097, 64)])
-def test_float32_loss_and_lse_are_within_an_ulp(hip, b, v, d):
-    """float32 h and w: the logits are the reference's sequential k fold (the exact GEMM), the sum of
-    exponentials float64 like the reference's; loss and lse agree with the oracle to 1 ulp (the float64 exp
-    and log of two libms may differ in the last bits)."""
+def test_float32_loss_and_lse_are_within_2_ulp(hip, b, v, d):
+    """float32 h and w: the logits are the reference's sequential k fold (the exact GEMM); the exponentials
+    are float32 (within 2 ulp) summed in float64 where the reference takes float64 exponentials; loss and lse
+    agree with the oracle to 2 ulp."""
     rng = np.random.default_rng(b + v)
     h = rng.standard_normal((b, d)).astype(np.float32)
     w = rng.standard_normal((v, d)).astype(np.float32) * 0.2
@@ -39,7 +39,7 @@ def test_float32_loss_and_lse_are_within_an_ulp(hip, b, v, d):
     got, want, _ = _run(h, w, t, "float32")
     assert got.shape == (2, b)
     ulp = np.spacing(np.abs(want))
-    assert np.all(np.abs(got - want) <= ulp), np.abs(got - want).max()
+    assert np.all(np.abs(got - want) <= 2 * ulp), np.abs(got - want).max()
 
 
 def test_bf16_with_clamped_int64_targets_and_chunks(hip, monkeypatch):
