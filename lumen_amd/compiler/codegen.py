@@ -1035,9 +1035,12 @@ class GemmEpilogueKernel:
     (mn-contiguous operands), as nhip_gemm takes them."""
 
 
-    def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views):
+    def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None):
         self.graph, self.dot, self.loop = graph, dot_step, loop_step
         self.desc, self.at, self.bt, self.f16, self.store_dot = desc, at, bt, f16, store_dot
+        # (value, sum): a float32 loop output summed over the rows into `sum` [n] (atomically, into zeros)
+        # instead of being stored
+        self.colsum = colsum
         self.views, self.out_views = views, out_views
         self.name = "KNAME"
         d = desc
@@ -1080,14 +1083,18 @@ class GemmEpilogueKernel:
             raise Unfusable(dv, "the fused loop reads the dot's result at another index")
 
         em.given[dv] = given
+        stored = [v for v in loop.outputs if not (self.colsum and v == self.colsum[0])]
         per_lane = []
+        summed = []
         for lane in range(4):
             idx = ("flat", f"(base + {lane})", "base", lane)
-            per_lane.append([em.value(v, idx) for v in loop.outputs])
+            per_lane.append([em.value(v, idx) for v in stored])
+            if self.colsum:
+                summed.append(em.value(self.colsum[0], idx))
         body = em.lines
         pro = lk._vec_prologue(em, 4, lin)
         stores = []
-        outs = ([dv] if self.store_dot else []) + list(loop.outputs)
+        outs = ([dv] if self.store_dot else []) + stored
         for k, v in enumerate(outs):
             dt = g.types[v].dtype
             names = dnames if (self.store_dot and k == 0) else [per_lane[l][k - (1 if self.store_dot else 0)] for l in range(4)]
@@ -1098,6 +1105,15 @@ class GemmEpilogueKernel:
                 for lane in range(4):
                     addr = lk._out_addr(view, g.types[v].shape, f"(base + {lane})")
                     stores.append(f"out{k}[{addr}] = {_store(names[lane], dt)};")
+        if self.colsum:
+            outs = outs + [self.colsum[1]]  # the float32 [n] sums, last
+            ret = f"return make_float4({', '.join(summed)});"
+            colsum_fn = ["  __device__ __forceinline__ void colsum_add(int64_t c, float4 v) const {",
+                         f"    float* p = out{len(outs) - 1} + c;",
+                         "    atomicAdd(p, v.x); atomicAdd(p + 1, v.y); atomicAdd(p + 2, v.z); atomicAdd(p + 3, v.w);",
+                         "  }"]
+        else:
+            ret, colsum_fn = "", []
         self.args = [("in", dot.nodes[0].inputs[0]), ("in", dot.nodes[0].inputs[1])]
         self.args += [("in", v) for v in lin] + [("out", v) for v in outs]
         fields = [f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k};" for k, v in enumerate(lin)]
@@ -1128,14 +1144,17 @@ class GemmEpilogueKernel:
             "struct EpiKNAME {",
             *["  " + f for f in fields],
             f"  static constexpr int kPrefetch = {ahead};",
+            f"  static constexpr bool kColSum = {'true' if self.colsum else 'false'};",
+            *colsum_fn,
             "  struct Pre {", *["    " + f for f in pre_fields], "  };",
             "  __device__ __forceinline__ Pre load(int64_t r, int64_t c) const {",
             f"    const int64_t base = r * {n}LL + c;",
             "    Pre p;", *["    " + l for l in pre_loads], "    return p;",
             "  }",
-            "  __device__ __forceinline__ void operator()(int64_t r, int64_t c, float4 acc, const Pre &pre) const {",
+            f"  __device__ __forceinline__ {'float4' if self.colsum else 'void'} operator()(int64_t r, int64_t c, float4 acc, "
+            "const Pre &pre) const {",
             f"    const int64_t base = r * {n}LL + c;",
-            *["    " + l for l in pre_uses + rest + body + stores],
+            *["    " + l for l in pre_uses + rest + body + stores + ([ret] if ret else [])],
             "  }",
             "};",
             f'extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) '

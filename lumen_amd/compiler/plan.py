@@ -421,10 +421,41 @@ class Plan:
                 st.nodes = list(st.nodes) + list(lt.nodes)
                 merged.add(li)
                 break
-        if not merged:
-            return False
         self.steps = [st for i, st in enumerate(self.steps) if i not in merged]
-        return True
+        return bool(merged) | self._fuse_column_sums()
+
+    def _fuse_column_sums(self):
+        """A float32 sum over the rows of a GEMM epilogue's [m, n] output that only the sum reads (a bias or
+        norm-weight gradient) moves into the epilogue: each wave adds its column sums atomically into the
+        zero-filled [n] result and the [m, n] value is never stored. Returns whether any moved."""
+        g = self.graph
+        outputs = set(g.outputs)
+        readers: dict[int, list] = {}
+        for st in self.steps:
+            for u in st.inputs:
+                readers.setdefault(u, []).append(st)
+        gone = set()
+        for st in self.steps:
+            if st.kind != "dot" or getattr(st, "epi", None) is None or getattr(st, "epi_colsum", None):
+                continue
+            shape = g.types[st.nodes[0].output].shape
+            for u in st.epi.outputs:
+                rs = readers.get(u, [])
+                if len(rs) != 1 or u in outputs or g.types[u].dtype != "float32" or g.types[u].shape != shape:
+                    continue
+                r = rs[0]
+                if r.kind != "reduce" or len(r.nodes) != 1 or r.nodes[0].prim != "reduce_sum":
+                    continue
+                n = r.nodes[0]
+                if n.inputs[0] != u or tuple(n.params["axes"]) != (0,) or g.types[n.output].dtype != "float32":
+                    continue
+                st.epi_colsum = (u, n.output)
+                st.outputs = [v for v in st.outputs if v != u] + [n.output]
+                st.nodes = list(st.nodes) + [n]
+                gone.add(id(r))
+                break
+        self.steps = [st for st in self.steps if id(st) not in gone]
+        return bool(gone)
 
     # the producers that may write an operand of a concatenation in place, through a strided view
     ALIAS_PRODUCERS = ("flash_fwd", "flash_bwd", "dot", "loop")
@@ -503,7 +534,8 @@ class Plan:
                 lin = [v for v in st.epi.inputs if v != st.nodes[0].output]
                 views = {v: self.loc[v].view() for v in lin}
                 outs = {v: self.loc[v].view() for v in st.outputs}
-                k = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs)
+                k = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
+                                               colsum=getattr(st, "epi_colsum", None))
                 body = k.source()
                 name = f"gemm_epi_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
                 k.name = st.name = name
@@ -593,6 +625,11 @@ class Plan:
                     st.kind == "dot" and getattr(st, "epi", None) is not None):
                 k = self.kernels[si]
                 fn = nv.module_function(self.objects[si], k.name)
+                if st.kind == "dot" and getattr(st, "epi_colsum", None):  # the column sums add into zeros
+                    out = self.loc[st.epi_colsum[1]]
+                    desc = struct.pack("<QI", g.types[st.epi_colsum[1]].nbytes(), 0) + b"\0" * 4
+                    relocs = (nv.Reloc * 1)(reloc(0, out))
+                    call("nhip_plan_add_builtin", plan, nv.NHIP_STEP_FILL, desc, len(desc), relocs, 1)
                 if st.kind == "reduce" and getattr(k, "atomic", False):
                     out = self.loc[st.outputs[0]]
                     desc = struct.pack("<QI", g.types[st.outputs[0]].nbytes(), 0) + b"\0" * 4

@@ -603,6 +603,11 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     // four columns at a time: the first group's loads are issued before the sums are staged, so their latency
     // overlaps the staging and the barrier instead of stalling every chunk
     constexpr int CPR = WCOLS / 4;  // four-column chunks a wave row; a lane takes CPR of the 64 x CPR chunks a half
+    // a column-summing epilogue (Out::kColSum): a lane's chunks all hold columns cbase + 4 (lane % CPR) .. + 3,
+    // so it sums its rows' values of them here; the lanes of a column combine at the end and the wave adds
+    // its 4 x CPR column sums atomically (Out::colsum_add)
+    float4 colsum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    (void)colsum;
 #pragma unroll
     for (int half = 0; half < FM / 2; ++half) {
         if constexpr (std::is_same<Out, AnyStore>::value) {
@@ -612,6 +617,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         } else {
             constexpr int G = Out::kPrefetch < CPR ? Out::kPrefetch : CPR;
             static_assert(CPR % G == 0, "prefetch groups must divide a lane's chunks");
+            static_assert(64 % CPR == 0, "a lane keeps the same four columns over its chunks");
             typename Out::Pre pre[G];
             auto fetch = [&](int g0) {
 #pragma unroll
@@ -632,11 +638,34 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                     const int idx = lane + 64 * (g0 + q);
                     const int r = idx / CPR, ch = idx % CPR;
                     const int64_t gr = rbase + 64 * half + r, gc = cbase + 4 * ch;
-                    if (gr < s.m && gc < s.n) out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16), pre[q]);
+                    if (gr < s.m && gc < s.n) {
+                        if constexpr (Out::kColSum) {
+                            const float4 c4 = out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16), pre[q]);
+                            colsum.x += c4.x;
+                            colsum.y += c4.y;
+                            colsum.z += c4.z;
+                            colsum.w += c4.w;
+                        } else {
+                            out(gr, gc, *reinterpret_cast<const float4 *>(stage + r * PITCH + ch * 16), pre[q]);
+                        }
+                    }
                 }
             }
         }
         __syncthreads();
+    }
+    if constexpr (!std::is_same<Out, AnyStore>::value) {
+        if constexpr (Out::kColSum) {
+#pragma unroll
+            for (int o = CPR; o < 64; o <<= 1) {
+                colsum.x += __shfl_xor(colsum.x, o, 64);
+                colsum.y += __shfl_xor(colsum.y, o, 64);
+                colsum.z += __shfl_xor(colsum.z, o, 64);
+                colsum.w += __shfl_xor(colsum.w, o, 64);
+            }
+            const int64_t gc = cbase + 4 * lane;
+            if (lane < CPR && gc < s.n && rbase < s.m) out.colsum_add(gc, colsum);
+        }
     }
 }
 

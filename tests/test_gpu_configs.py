@@ -226,3 +226,38 @@ def test_float32_exp_is_within_4_ulp(hip):
     assert np.array_equal(got[n:n + 4], [1.0, 1.0, 1.0, 1.0])
     assert np.all(np.abs(got[n + 4:n + 6] - want[n + 4:n + 6]) <= 2.0 ** -126)
     assert got[n + 6] == np.inf and got[n + 7] == 0.0 and got[n + 8] == np.inf and np.isnan(got[n + 9])
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 256), (1000, 776, 320)])
+def test_gemm_epilogue_column_sums_match_oracle(hip, m, n, k, monkeypatch):
+    """A row sum of a GEMM epilogue's float32 output (a bias / norm-weight gradient shape) computed inside the
+    epilogue: per-wave column sums added atomically, the [m, n] product never stored (no reduce step left),
+    ragged m and n. Against the oracle's sequential sums within float32 reassociation (1e-4 of the sum of
+    magnitudes) and against the same plan without epilogue fusion."""
+    from lumen_amd.compiler.plan import Plan
+
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
+
+    def fn(x, w, h):
+        z = F.matmul(x, w, "float32", "float32") * h
+        return F.sum(z, dim=(0,)), (z + 1.0).bfloat16()
+
+    rng = np.random.default_rng(17)
+    x = _bf16(rng.standard_normal((m, k)) * 0.25)
+    w = _bf16(rng.standard_normal((k, n)) * 0.25)
+    h = rng.standard_normal((m, n)).astype(np.float32)
+    args = [L.tensor(D.bf16_to_f32(x), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(h)]
+    with L.config.compiler.patch(horizontal_fusion=False):
+        f = L.compile(fn, device="hip")
+        got = [np.asarray(L.to_numpy(t), np.float32) for t in f(*args)]
+        kinds = [s["kind"] for s in f.plan.describe()]
+        assert "reduce" not in kinds and any(s["name"].startswith("gemm_epi_") for s in f.plan.describe())
+    with L.config.compiler.patch(horizontal_fusion=False, epilogue_fusion=False):
+        u = L.compile(fn, device="hip")
+        ref = [np.asarray(L.to_numpy(t), np.float32) for t in u(*args)]
+    want = [np.asarray(v, np.float32) for v in oracle.values(L.make_graph(fn)(*args), [x, w, h])]
+    y = D.bf16_to_f32(x).astype(np.float64) @ D.bf16_to_f32(w).astype(np.float64)
+    scale = np.abs(y * h).sum(axis=0)
+    assert np.all(np.abs(got[0] - want[0]) <= 1e-4 * scale + 1e-6)
+    assert np.all(np.abs(got[0] - ref[0]) <= 1e-4 * scale + 1e-6)
+    np.testing.assert_allclose(got[1], want[1], rtol=2e-2, atol=1e-2 * np.abs(want[1]).max())
