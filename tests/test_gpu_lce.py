@@ -99,3 +99,19 @@ def test_compiled_eval_loss_uses_the_fused_step(hip):
     assert "linear_cross_entropy" in [s["kind"] for s in f.plan.describe()]
     (want,) = oracle.values(L.make_graph(fn)(*args), [h, w, t])
     np.testing.assert_allclose(got, float(want), rtol=1e-4)
+
+
+def test_f16_operands_and_ragged_rows(hip):
+    """float16 h and w (the f16 MFMA GEMM) with a class count that is not a multiple of 4 (the row kernel's
+    element-by-element loads) against the oracle at float32 tolerance."""
+    rng = np.random.default_rng(31)
+    b, v, d = 130, 1003, 64
+    h = (rng.standard_normal((b, d)) * 0.5).astype(np.float16)
+    w = (rng.standard_normal((v, d)) * 0.2).astype(np.float16)
+    t = rng.integers(0, v, b).astype(np.int32)
+    args = [L.tensor(h.astype(np.float32), "float16"), L.tensor(w.astype(np.float32), "float16"), L.from_numpy(t)]
+    f = L.compile(lambda h, w, t: prims.linear_cross_entropy(h, w, t), device="hip")
+    got = np.asarray(L.to_numpy(f(*args)), np.float32)
+    (want,) = oracle.values(L.make_graph(lambda h, w, t: prims.linear_cross_entropy(h, w, t))(*args),
+                            [h.astype(np.float32), w.astype(np.float32), t])
+    np.testing.assert_allclose(got, np.asarray(want, np.float32), rtol=1e-4, atol=1e-4 * np.abs(want).max())
