@@ -220,6 +220,18 @@ class Plan:
         for i, v in enumerate(g.inputs):
             t = g.types[v]
             self.loc[v] = Loc(("in", i), 0, _contig(t.shape), t.dtype, t.shape)
+        # a flash forward output read only through one transpose that keeps the head dim innermost (the
+        # attention output going back to [B, S, N, H]) is written in the transposed order: the kernel takes
+        # any strides, and the output projection then reads it in place instead of through a copy
+        o_perm = {}
+        gusers = g.users()
+        for st in self.steps if self.FLASH_OUT_TRANSPOSED else ():
+            if st.kind == "flash_fwd" and st.outputs[0] not in g.outputs:
+                us = [u for u in gusers.get(st.outputs[0], []) if u.prim != "fusion_output"]
+                if len(us) == 1 and us[0].prim == "transpose":
+                    perm = tuple(us[0].params["permutation"])
+                    if perm[-1] == len(perm) - 1:
+                        o_perm[st.outputs[0]] = perm
         # views first: resolved lazily in step order; a view that strides cannot express becomes a copy
         last_use: dict[int, int] = {}
         base_of: dict[int, int] = {}
@@ -304,7 +316,15 @@ class Plan:
                     continue
                 off, size = take(t.nbytes())
                 live[v] = (off, size)
-                self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), _contig(t.shape), t.dtype, t.shape)
+                strides = _contig(t.shape)
+                if v in o_perm:  # laid out as its transpose: the transpose (and a reshape of it) is then a view
+                    perm = o_perm[v]
+                    dense = _contig(tuple(t.shape[d] for d in perm))
+                    strides = [0] * len(perm)
+                    for j, d in enumerate(perm):
+                        strides[d] = dense[j]
+                    strides = tuple(strides)
+                self.loc[v] = Loc(("ws", 0), off // D.size_of(t.dtype), strides, t.dtype, t.shape)
             if st.kind == "dot":
                 st.splits, split_cfg = (1, None) if getattr(st, "epi", None) is not None else self._split_count(st.nodes[0])
                 if split_cfg is not None:
@@ -340,6 +360,7 @@ class Plan:
 
     # ---- GEMM epilogues (lumen/graph_compiler/passes/fusion/mod.rs:20-112, the CUDA backend's `epilogue`):
     # a loop step that reads a dot's [m, n] result element for element runs inside the dot's store
+    FLASH_OUT_TRANSPOSED = True  # flash outputs laid out as the transpose that reads them (see _place)
     EPI_MIN_TILES = 256  # the streamed GEMM's own default threshold (kernels.hip: default_config)
 
     def _epilogue_layout(self, st):
