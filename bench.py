@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark: the transformer training step compiled for hip on one MI355X (BASELINE.json's metric).
+"""Benchmark: the transformer training step compiled for hip on one MI355X (the headline metric: train-step ms).
 
 One step = one call of the compiled ``train_step`` (forward, autograd backward and SGD update of every weight,
 one static plan) on synthetic data of the configured shape, inputs resident on the device. The timed region
@@ -220,7 +220,7 @@ def main():
     del np
 
 
-# ---- single-op configurations (SURVEY-style configs 1-3): one compiled call (or C-ABI call) is a step
+# ---- single-op configurations (configs 1-3): one compiled call (or C-ABI call) is a step
 
 
 def _op_line(args, metric, ms, unit_value, unit, config, roof, cpu, dtype, extra=None):

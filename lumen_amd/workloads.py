@@ -1,4 +1,4 @@
-"""The BASELINE workloads as lumen programs: the decoder-only transformer training step of configs 4 and 5
+"""The benchmark workloads as lumen programs: the decoder-only transformer training step of configs 4 and 5
 (``examples/transformer.py`` style: pre-norm blocks, causal flash attention, a GELU FFN, a cross-entropy head,
 autograd backward and an SGD update inside one compiled function) and its synthetic inputs.
 
@@ -46,7 +46,8 @@ class TransformerConfig:
         return 3 * fwd
 
 
-# BASELINE.json configs 4 and 5, and a small one for parity tests and the smoke check.
+# The benchmark's configs 4 (2 layers, d 512) and 5 (12 layers, d 2048), and a small one for parity tests
+# and the smoke check.
 CONFIG4 = TransformerConfig(vocab=32000, dim=512, heads=8, ffn=2048, seq=512, batch=16, layers=2)
 CONFIG5 = TransformerConfig(vocab=32000, dim=2048, heads=16, ffn=8192, seq=4096, batch=4, layers=12)
 TINY = TransformerConfig(vocab=256, dim=128, heads=2, ffn=256, seq=128, batch=2, layers=2)

@@ -1,4 +1,4 @@
-"""The decoder training step (the BASELINE transformer at a small size) compiled for hip against the CPU
+"""The decoder training step (the benchmark transformer at a small size) compiled for hip against the CPU
 oracle running the same traced graph: loss, every gradient, and the SGD-updated weights."""
 
 import numpy as np
