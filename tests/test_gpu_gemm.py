@@ -196,3 +196,17 @@ def test_plan_autotunes_large_dots(hip):
     dots = [st for st in fn.plan.steps if st.kind == "dot"]
     assert dots and all(getattr(st, "config", -1) >= 0 for st in dots)
     assert any(v >= 0 for v in Plan._tuned.values())
+
+
+def test_gemm_persistent_f16_operands(hip):
+    """The persistent kernel (config 10) with float16 operands (the f16 MFMA) and more tiles than CUs."""
+    rng = np.random.default_rng(40)
+    m, n, k = 4352, 4352, 128
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = rng.standard_normal((n, k)).astype(np.float16)
+    want = a.astype(np.float64) @ b.astype(np.float64).T
+    da, db, dd = Dev(a.view(np.uint16)), Dev(b.view(np.uint16)), Dev(nbytes=m * n * 4)
+    desc = _desc(m, n, k, k, 1, 1, k, dt=nv.NHIP_F16, cfg=10)
+    nv.call("nhip_gemm", C.byref(desc), da.ptr, db.ptr, dd.ptr)
+    got = dd.get((m, n), np.float32)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-4
