@@ -157,3 +157,31 @@ def test_linear_cross_entropy_is_a_builtin_step_with_bounded_scratch(monkeypatch
     assert [s.kind for s in p.steps] == ["linear_cross_entropy"]
     d = p._lce_desc(p.steps[0].nodes[0])
     assert d.chunk_rows == (1 << 20) // (32000 * 4) and p.steps[0].scratch == d.chunk_rows * 32000 * 4
+
+
+def test_hoisting_casts_into_producers_reads_fewer_bytes(monkeypatch):
+    """The config-4 step: the embedding-gradient kernel at the end reads the residual-gradient terms as bf16
+    (each cast where its float32 term is made) instead of every float32 term, and the plan's row/loop bytes
+    drop against the same plan without the pass."""
+    from lumen_amd.compiler import fusion
+
+    cfg = W.CONFIG4
+    model, opt = W.build(cfg, lr=1e-2)
+    ids = L.empty([cfg.batch, cfg.seq], "int32", "meta")
+    tg = L.empty([cfg.batch, cfg.seq], "int32", "meta")
+    graph = L.make_graph(W.train_step)(model, opt, ids, tg)
+
+    def loop_bytes(p):
+        return sum(p.cost(i)[1] for i, s in enumerate(p.steps) if s.kind in ("loop", "row"))
+
+    with_pass = Plan(graph, build_kernels=False)
+    monkeypatch.setattr(fusion, "hoist_to_producers", lambda g, s: s)
+    without = Plan(graph, build_kernels=False)
+    assert loop_bytes(with_pass) < loop_bytes(without)
+
+    def f32_terms(p):  # float32 [tokens, dim] operands of the row kernel reading the most of them
+        g = p.graph
+        return max(sum(g.types[v].dtype == "float32" and g.types[v].shape == (cfg.batch * cfg.seq, cfg.dim)
+                       for v in s.inputs) for s in p.steps if s.kind == "row")
+
+    assert f32_terms(with_pass) < f32_terms(without)
