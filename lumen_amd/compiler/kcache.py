@@ -1,15 +1,23 @@
-"""Compiles generated HIP sources to gfx950 code objects, cached by source hash
+"""Compiles generated HIP sources to gfx950 code objects, cached by content
 (the reference's compile-once-per-layout-key, ``lumen/runtime/kernel/cuda/driver.rs:148-179``).
 
 The cache lives in ``lumen_amd/_kcache/`` inside the package, so code objects built here on the CPU travel
 with the repository to the GPU box; a miss there compiles with the same hipcc.
+
+A code object's key covers everything that decides its bits: the architecture, the flags, the hipcc
+version, the generated source and the text of every ``csrc/`` header it includes, transitively. Objects are
+filed under a directory named by the hash of that header set (``_kcache/<headers>/<key>.hsaco``), so an
+edit to a header leaves its old objects in a directory no current key names, and ``prune()`` removes them.
 """
 
 from __future__ import annotations
 
 import concurrent.futures
+import functools
 import hashlib
 import os
+import re
+import shutil
 import subprocess
 import tempfile
 
@@ -19,6 +27,7 @@ CSRC = os.path.join(os.path.dirname(HERE), "csrc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-Wno-unused-variable", "-Wno-unused-but-set-variable"]
+_INCLUDE = re.compile(r'^\s*#\s*include\s+"([^"]+)"', re.M)
 
 
 def hipcc():
@@ -28,9 +37,75 @@ def hipcc():
     return "hipcc"
 
 
-def path_for(source: str) -> str:
-    h = hashlib.sha256((ARCH + " ".join(FLAGS) + source).encode()).hexdigest()[:24]
-    return os.path.join(CACHE, f"{h}.hsaco")
+@functools.lru_cache(maxsize=None)
+def hipcc_version() -> str:
+    """The compiler's own version text (part of every key: a new compiler makes new objects)."""
+    try:
+        r = subprocess.run([hipcc(), "--version"], capture_output=True, text=True, timeout=120)
+        return "\n".join(r.stdout.splitlines()[:2])
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+
+
+def includes(text: str, csrc: str = CSRC) -> list:
+    """The quoted includes of ``text`` that resolve to files under ``csrc``, transitively, in first-seen
+    order (a cycle or a repeated header is visited once)."""
+    seen, order, todo = set(), [], list(_INCLUDE.findall(text))
+    while todo:
+        name = todo.pop(0)
+        path = os.path.normpath(os.path.join(csrc, name))
+        if path in seen or not os.path.isfile(path):
+            continue
+        seen.add(path)
+        order.append(path)
+        with open(path) as f:
+            todo.extend(_INCLUDE.findall(f.read()))
+    return order
+
+
+def header_digest(source: str, csrc: str = CSRC) -> str:
+    h = hashlib.sha256()
+    for path in includes(source, csrc):
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
+def path_for(source: str, csrc: str = CSRC, cache: str = CACHE) -> str:
+    headers = header_digest(source, csrc)
+    key = "\0".join([ARCH, " ".join(FLAGS), hipcc_version(), headers, source])
+    h = hashlib.sha256(key.encode()).hexdigest()[:24]
+    return os.path.join(cache, headers, f"{h}.hsaco")
+
+
+def live_dirs(csrc: str = CSRC) -> set:
+    """Header-set directories the current sources can name: one per csrc header taken as the root include,
+    plus the one of a source that includes none of them."""
+    names = {header_digest("")}
+    for f in sorted(os.listdir(csrc)):
+        if f.endswith(".h"):
+            names.add(header_digest(f'#include "{f}"\n', csrc))
+    return names
+
+
+def prune(csrc: str = CSRC, cache: str = CACHE) -> int:
+    """Removes cached objects built against headers that have since changed (and files from the older flat
+    layout); returns how many entries were removed."""
+    if not os.path.isdir(cache):
+        return 0
+    keep, removed = live_dirs(csrc), 0
+    for name in os.listdir(cache):
+        p = os.path.join(cache, name)
+        if os.path.isdir(p) and name in keep:
+            continue
+        removed += 1
+        if os.path.isdir(p):
+            shutil.rmtree(p, ignore_errors=True)
+        else:
+            os.remove(p)
+    return removed
 
 
 def compile_source(source: str) -> str:
@@ -38,7 +113,7 @@ def compile_source(source: str) -> str:
     out = path_for(source)
     if os.path.exists(out):
         return out
-    os.makedirs(CACHE, exist_ok=True)
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     with tempfile.TemporaryDirectory() as d:
         src = os.path.join(d, "k.hip")
         with open(src, "w") as f:

@@ -17,11 +17,10 @@ from lumen_amd import native
 
 
 def device_name(d) -> str:
-    """``"hip:0"`` from ``"hip"``, ``"hip:0"``, ``"cuda"`` (an alias of hip on ROCm), ``"cpu"``, ``"meta"``."""
+    """``"hip:0"`` from ``"hip"``, ``"hip:0"``, ``"cpu"``, ``"meta"``. The GPU device is named ``hip``; there is
+    no CUDA alias."""
     d = str(d)
     kind, _, idx = d.partition(":")
-    if kind == "cuda":
-        kind = "hip"
     if kind not in ("cpu", "hip", "meta"):
         raise ValueError(f"unknown device {d!r}: this backend has cpu (host data), hip and meta")
     return f"{kind}:{idx or 0}"
@@ -127,7 +126,7 @@ class Tensor:
 
     def to(self, *args, dtype=None, device=None, **_):
         for a in args:
-            if isinstance(a, str) and a.split(":")[0] in ("cpu", "hip", "meta", "cuda"):
+            if isinstance(a, str) and a.split(":")[0] in ("cpu", "hip", "meta"):
                 device = a
             elif isinstance(a, Tensor):
                 dtype = a.dtype

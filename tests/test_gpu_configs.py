@@ -34,10 +34,39 @@ def _chain(x, a, b):
     return F.softmax(t, -1).bfloat16()
 
 
+def _chain2(x, a, b):
+    """The config-2 chain with the layer norm's output as a second (bf16) result."""
+    t = (x * a + b).float()
+    t = F.gelu(t)
+    n = F.layer_norm(t, x.shape[-1])
+    return F.softmax(n, -1).bfloat16(), n.bfloat16()
+
+
+def _ulps_bf16(got, want):
+    """Distance in bf16 steps between two bf16-valued float32 arrays (monotone integer mapping)."""
+    def key(v):
+        u = D.bf16_bits(np.asarray(v, np.float32)).astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - u, u)
+    return np.abs(key(got) - key(want))
+
+
+def check_softmax_rows(got, want):
+    """A bf16 softmax output against the oracle, scaled to the values it holds (the entries of a 4096-wide
+    row are ~2e-4, so a fixed atol of 1e-2 would accept zeros): every entry within rtol 2e-2 plus 1e-2 of
+    its row's largest entry, every entry at most 2 bf16 steps from the oracle's, every row summing to 1
+    within 1e-2."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rowmax = np.abs(want).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want) + 1e-2 * rowmax), "softmax entries off"
+    assert _ulps_bf16(got, want).max() <= 2, "softmax entries more than 2 bf16 steps from the oracle"
+    assert np.all(np.abs(got.sum(axis=-1) - 1.0) <= 1e-2), "softmax rows do not sum to 1"
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (37, 512), (16, 64), (8, 1000)])
 def test_config2_fused_chain_matches_oracle(hip, rows, cols):
-    """layernorm(gelu(x*a+b)) then softmax, bf16 in and out, float32 statistics: one row kernel, within
-    the bf16 tolerance (rtol 2e-2, atol 1e-2)."""
+    """layernorm(gelu(x*a+b)) then softmax, bf16 in and out, float32 statistics: one row kernel, each
+    softmax entry checked against the oracle relative to the row's own scale."""
     rng = np.random.default_rng(1)
     x = _bf16(rng.standard_normal((rows, cols)))
     a = _bf16(1.0 + 0.1 * rng.standard_normal(cols))
@@ -47,7 +76,30 @@ def test_config2_fused_chain_matches_oracle(hip, rows, cols):
     got = L.to_numpy(f(*args))
     assert [s["kind"] for s in f.plan.describe()] == ["row"]
     (want,) = oracle.values(L.make_graph(_chain)(*args), [x, a, b])
-    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2)
+    check_softmax_rows(got, want)
+    with pytest.raises(AssertionError):  # the check rejects a kernel that wrote zeros
+        check_softmax_rows(np.zeros_like(got), want)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (16, 1000)])
+def test_config2_chain_with_layernorm_output_matches_oracle(hip, rows, cols):
+    """The same chain also returning the layer norm's output (values of order 1, so the bf16 tolerance is
+    meaningful at face value): the softmax by the row-scaled check and the layer norm within rtol 2e-2 /
+    atol 1e-2 and (away from zero) 2 bf16 steps of the oracle."""
+    rng = np.random.default_rng(5)
+    x = _bf16(rng.standard_normal((rows, cols)))
+    a = _bf16(1.0 + 0.1 * rng.standard_normal(cols))
+    b = _bf16(0.1 * rng.standard_normal(cols))
+    args = [L.tensor(D.bf16_to_f32(v), "bfloat16") for v in (x, a, b)]
+    f = L.compile(_chain2, device="hip")
+    sm, ln = (L.to_numpy(t) for t in f(*args))
+    assert {s["kind"] for s in f.plan.describe()} == {"row"}
+    want_sm, want_ln = oracle.values(L.make_graph(_chain2)(*args), [x, a, b])
+    check_softmax_rows(sm, want_sm)
+    np.testing.assert_allclose(ln, want_ln, rtol=2e-2, atol=1e-2)
+    big = np.abs(np.asarray(want_ln, np.float64)) >= 1e-2  # near zero the float32 cancellation in x - mean dominates
+    assert _ulps_bf16(ln, want_ln)[big].max() <= 2
+    assert np.abs(np.asarray(want_ln, np.float64)).max() > 1.0  # the atol is small against these values
 
 
 def test_horizontally_fused_loops_match_oracle_bit_for_bit(hip):
