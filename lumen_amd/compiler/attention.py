@@ -223,7 +223,9 @@ def match_forward(g: Graph):
             continue
         sq, sk = st.shape[2], st.shape[3]
         causal = _causal(G, pred, sq, sk)
-        if causal is None:
+        if causal is None or (causal and sk < sq):
+            # causal with fewer keys than queries leaves the first sq - sk rows with no key: the written
+            # attention gives NaN there, which the unfused plan reproduces and the flash kernel does not
             continue
         qt, kt, vt = (g.types[u] for u in (d1.inputs[0], d1.inputs[1], d2.inputs[1]))
         if qt.dtype not in ("bfloat16", "float16") or not (qt.dtype == kt.dtype == vt.dtype):
@@ -331,7 +333,7 @@ def match_backward(g: Graph):
         sq_, sk_ = g.types[pt].shape[3], g.types[pt].shape[2]
         # the mask here is over [Sk, Sq]: evaluate transposed
         causal = _causal_t(G, pred, sk_, sq_)
-        if causal is None:
+        if causal is None or (causal and sk_ < sq_):  # rows with no key: left to the unfused plan
             continue
         outs = []
         tail = []

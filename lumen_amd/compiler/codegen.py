@@ -90,16 +90,35 @@ DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf(
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
 DEV float fmin_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
 DEV double dmin_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmin(a, b); }
+// float -> integer saturating at the result dtype's limits, NaN -> 0 (lumen/reference/mod.rs saturate). lo and
+// hi are the dtype's limits as doubles (T is its compute type, which may be wider); the 64-bit maxima round to
+// 2^63 / 2^64 as doubles, which do not convert back, so those return T's own maximum instead.
 template <typename T> DEV T sat_cast(double x, double lo, double hi) {
   if (x != x) return T(0);
   if (x <= lo) return T(lo);
-  if (x >= hi) return T(hi);
+  if (x >= hi) return hi < 9.2233720368547758e18 ? T(hi) : (T(0) < T(-1) ? T(~T(0)) : T(~(T(1) << (8 * sizeof(T) - 1))));
   return T(x);
 }
 DEV float wsum(float v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
 DEV double wsum(double v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
 DEV float wmax(float v) { for (int o = 32; o > 0; o >>= 1) v = fmax_n(v, __shfl_xor(v, o, 64)); return v; }
 DEV double wmax(double v) { for (int o = 32; o > 0; o >>= 1) v = dmax_n(v, __shfl_xor(v, o, 64)); return v; }
+// integer wavefront sums wrap (unsigned adds, two's complement: any order gives the same bits) and maxima;
+// 64-bit values cross lanes as two 32-bit halves
+DEV uint64_t shfl64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_xor((unsigned)(v & 0xffffffffu), o, 64), hi = __shfl_xor((unsigned)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+DEV int32_t wsum(int32_t v) { for (int o = 32; o > 0; o >>= 1) v = (int32_t)((uint32_t)v + (uint32_t)__shfl_xor(v, o, 64)); return v; }
+DEV uint32_t wsum(uint32_t v) { for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor(v, o, 64); return v; }
+DEV int64_t wsum(int64_t v) { for (int o = 32; o > 0; o >>= 1) v = (int64_t)((uint64_t)v + shfl64((uint64_t)v, o)); return v; }
+DEV uint64_t wsum(uint64_t v) { for (int o = 32; o > 0; o >>= 1) v += shfl64(v, o); return v; }
+DEV int32_t wmax(int32_t v) { for (int o = 32; o > 0; o >>= 1) { int32_t w = __shfl_xor(v, o, 64); v = w > v ? w : v; } return v; }
+DEV uint32_t wmax(uint32_t v) { for (int o = 32; o > 0; o >>= 1) { uint32_t w = __shfl_xor(v, o, 64); v = w > v ? w : v; } return v; }
+DEV int64_t wmax(int64_t v) { for (int o = 32; o > 0; o >>= 1) { int64_t w = (int64_t)shfl64((uint64_t)v, o); v = w > v ? w : v; } return v; }
+DEV uint64_t wmax(uint64_t v) { for (int o = 32; o > 0; o >>= 1) { uint64_t w = shfl64(v, o); v = w > v ? w : v; } return v; }
+// integer add with wraparound in the width of T (no signed overflow)
+template <typename T> DEV T wrap_add(T a, T b) { return (T)((uint64_t)(int64_t)a + (uint64_t)(int64_t)b); }
 template <int N> struct alignas(N * 2) u16v { uint16_t e[N]; };
 template <int N> struct alignas(N * 4) f32v { float e[N]; };
 template <int N> struct alignas(N * 4) u32v { uint32_t e[N]; };
@@ -326,9 +345,48 @@ class Emitter:
                 if D.is_float(dt):
                     self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
                 elif p == "div":
-                    self.emit(f"const {ct} {out} = ({b} == 0 ? ({ct})-1 : {self.round(f'{a} / {b}', dt)});")
+                    # truncating; x / 0 = -1 and int64 min / -1 wraps to itself (the reference divides in i128
+                    # and wraps); narrower types divide exactly in 64 bits
+                    if dt == "int64":
+                        q = f"({b} == -1 ? (int64_t)(0ULL - (uint64_t){a}) : {a} / {b})"
+                    elif dt == "uint64":
+                        q = f"({a} / {b})"
+                    else:
+                        q = self.round(f"(int64_t){a} / (int64_t){b}", dt)
+                    self.emit(f"const {ct} {out} = ({b} == 0 ? ({ct})-1 : {q});")
                 else:
-                    self.emit(f"const {ct} {out} = {self.round(f'(int64_t){a} {op} (int64_t){b}', dt)};")
+                    # two's-complement wraparound: the operation in 64-bit unsigned arithmetic, then narrowed
+                    expr = f"(uint64_t)(int64_t){a} {op} (uint64_t)(int64_t){b}"
+                    self.emit(f"const {ct} {out} = {self.round(expr, dt)};")
+            return out
+        if p in ("shift_left", "shift_right_logical", "shift_right_arithmetic"):
+            # amounts outside [0, width) saturate: 0, or -1 for an arithmetic shift of a negative value
+            # (reference mod.rs:571-578); the value's bits are taken in its own width
+            a, b = same(0), same(1)
+            w = D.bits(dt)
+            mask = "0xffffffffffffffffULL" if w == 64 else f"0x{(1 << w) - 1:x}ULL"
+            ubits = f"((uint64_t)(int64_t){a} & {mask})"
+            sbits = f"(int64_t)({'(int64_t)' + ubits if w == 64 else f'(int64_t)({ubits} << {64 - w}) >> {64 - w}'})"
+            amt = f"(int64_t){b}"
+            inside = f"({amt} >= 0 && {amt} < {w})"
+            if p == "shift_left":
+                val, outside = f"({ubits} << {amt})", "0"
+            elif p == "shift_right_logical":
+                val, outside = f"({ubits} >> {amt})", "0"
+            else:
+                val, outside = f"(uint64_t)({sbits} >> {amt})", f"({sbits} < 0 ? ~0ULL : 0ULL)"
+            self.emit(f"const {ct} {out} = {self.round(f'({inside} ? {val} : {outside})', dt)};")
+            return out
+        if p in ("population_count", "clz"):
+            a = same()
+            w = D.bits(dt)
+            mask = "0xffffffffffffffffULL" if w == 64 else f"0x{(1 << w) - 1:x}ULL"
+            ubits = f"((uint64_t)(int64_t){a} & {mask})"
+            if p == "population_count":
+                expr = f"__popcll({ubits})"
+            else:
+                expr = f"({ubits} == 0 ? {w} : __clzll({ubits}) - {64 - w})"
+            self.emit(f"const {ct} {out} = ({ct})({expr});")
             return out
         if p == "neg":
             a = same()
@@ -394,7 +452,14 @@ class Emitter:
                     s = "" if dt == "float64" else "f"
                     self.emit(f"const {ct} {out} = {self.round(f'fmod{s}({a}, {b})', dt)};")
                 else:
-                    self.emit(f"const {ct} {out} = ({b} == 0 ? {a} : {a} % {b});")
+                    # x % 0 = x; int64 min % -1 = 0; narrower types in exact 64-bit arithmetic
+                    if dt == "int64":
+                        r = f"({b} == -1 ? (int64_t)0 : {a} % {b})"
+                    elif dt == "uint64":
+                        r = f"({a} % {b})"
+                    else:
+                        r = f"({ct})((int64_t){a} % (int64_t){b})"
+                    self.emit(f"const {ct} {out} = ({b} == 0 ? {a} : {r});")
             else:
                 op = {"and": "&", "or": "|", "xor": "^"}[p]
                 self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
@@ -523,27 +588,45 @@ class Emitter:
             return self.value(n.inputs[0], ("multi", tuple(sm)))
         if p in ("reduce_sum", "reduce_max"):
             if var in self.row_scalars:
+                # a row statistic is held for the current row only: reading it at any other index (a transposed
+                # broadcast of it, say) would silently take this row's value
+                if idx[0] != "r":
+                    raise Unfusable(var, f"{p} %{var} read at another row's index ({idx[0]})")
                 return self.row_scalars[var]
             raise Unfusable(var, f"{p} %{var} read outside its row")
         raise Unfusable(var, f"{p} has no loop-kernel lowering")
 
     def _row_broadcast(self, src, out, dims):
-        """Whether broadcasting ``src`` (numel R) to ``out`` (the R x C row space) repeats each row value over
-        the row's C elements."""
-        if self.rows is None or src.numel() != self.rows[0] or out.numel() != self.rows[0] * self.rows[1]:
-            return False
-        # the source's non-1 dims must be the leading output dims, equal in size, covering R
-        lead = 1
-        for i, d in enumerate(dims):
-            if src.shape[i] == 1:
-                continue
-            if d != i or out.shape[d] != src.shape[i]:
-                return False
-            lead *= src.shape[i]
-        k = 0
-        while k < len(out.shape) and math.prod(out.shape[:k]) < self.rows[0]:
-            k += 1
-        return lead == self.rows[0] and math.prod(out.shape[:k]) == self.rows[0]
+        """Whether broadcasting ``src`` repeats each row value over the row's elements of this kernel's row
+        space."""
+        from lumen_amd.compiler.fusion import row_broadcast
+
+        return self.rows is not None and row_broadcast(src, out, dims, self.rows)
+
+
+def _red_identity(prim, dt):
+    """The C literal a reduction of ``dt`` starts from: 0 for sums, -inf or the integer minimum for maxima."""
+    if prim == "reduce_sum":
+        return "0"
+    if D.is_float(dt):
+        return "-INFINITY"
+    if dt == "bool":
+        return "0"
+    lo = int(_int_range(dt)[0])
+    return f"({COMP_T[dt]})({lo + 1}LL - 1LL)" if lo else "0"
+
+
+def _red_update(em, prim, dt, acc, val):
+    """The expression folding ``val`` into the accumulator ``acc`` of a reduction of ``dt``: rounded float
+    sums, wrapping integer sums, NaN-propagating float maxima, integer maxima."""
+    ct = COMP_T[dt]
+    if prim == "reduce_sum":
+        if D.is_float(dt):
+            return em.round(f"{acc} + {val}", dt)
+        return em.round(f"wrap_add<{ct}>({acc}, ({ct})({val}))", dt)
+    if D.is_float(dt):
+        return f"{'dmax_n' if ct == 'double' else 'fmax_n'}({acc}, {val})"
+    return f"(({ct})({val}) > {acc} ? ({ct})({val}) : {acc})"
 
 
 def _int_range(dt):
@@ -742,12 +825,12 @@ class LoopKernel:
             b = f"(({j} * {T} + tid) * {V})"
             return b if exact else f"({b} < {C - V} ? (int64_t){b} : {C - V}LL)"
         body = []
-        red_identity = {"reduce_sum": "0", "reduce_max": "-INFINITY"}
         for red in reds:
             acc_dt = g.types[red.output].dtype
             act = COMP_T[acc_dt]
+            isf = D.is_float(acc_dt)
             accn = em.tmp("acc")
-            em.emit(f"{act} {accn} = {red_identity[red.prim] if act != 'double' else red_identity[red.prim]};")
+            em.emit(f"{act} {accn} = {_red_identity(red.prim, acc_dt)};")
             for j in range(J):
                 for lane in range(V):
                     cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
@@ -758,26 +841,19 @@ class LoopKernel:
                     idx = ("rc", "r", cidx, vbase(j), lane)
                     val = em.value(red.inputs[0], idx)
                     guard = "" if exact else f"if ({cexpr} < {C}LL) "
-                    if red.prim == "reduce_sum":
-                        em.emit(f"{guard}{accn} = {em.round(f'{accn} + {val}', acc_dt)};")
-                    else:
-                        fn = "dmax_n" if act == "double" else "fmax_n"
-                        em.emit(f"{guard}{accn} = {fn}({accn}, {val});")
+                    em.emit(f"{guard}{accn} = {_red_update(em, red.prim, acc_dt, accn, val)};")
             total = em.tmp("red")
             op = "wsum" if red.prim == "reduce_sum" else "wmax"
-            em.emit(f"{act} {total} = {op}({accn});")
+            em.emit(f"{act} {total} = {op}(({act}){accn});")
             if rows_per_block == 1 and T > 64:
                 nw = T // 64
-                comb = "+" if red.prim == "reduce_sum" else "max"
-                em.emit(f"if (lane == 0) red_lds[wave] = (double){total};")
+                # float partials cross waves as doubles (exact for float32), integers as their 64-bit pattern
+                lds = "red_lds" if isf else "red_ldsi"
+                em.emit(f"if (lane == 0) {lds}[wave] = ({'double' if isf else 'int64_t'}){total};")
                 em.emit("__syncthreads();")
-                em.emit(f"{total} = ({act})red_lds[0];")
+                em.emit(f"{total} = ({act}){lds}[0];")
                 for w in range(1, nw):
-                    if comb == "+":
-                        em.emit(f"{total} = {total} + ({act})red_lds[{w}];")
-                    else:
-                        fn = "dmax_n" if act == "double" else "fmax_n"
-                        em.emit(f"{total} = {fn}({total}, ({act})red_lds[{w}]);")
+                    em.emit(f"{total} = {_red_update(em, red.prim, acc_dt, total, f'({act}){lds}[{w}]')};")
                 em.emit("__syncthreads();")
             em.row_scalars[red.output] = total
         # element outputs
@@ -830,6 +906,7 @@ class LoopKernel:
                 "  const int tid = threadIdx.x; const int lane = tid & 63; const int wave = tid >> 6;",
                 "  const int64_t r = blockIdx.x;",
                 "  __shared__ double red_lds[16];",
+                "  __shared__ int64_t red_ldsi[16];",
             ]
         src += ["  (void)lane; (void)wave;"]
         # vector loads need the c indices declared before them: emit prologue after index decls
@@ -871,13 +948,8 @@ class LoopKernel:
         val = em.value(red.inputs[0], ("multi", tuple(xm)))
         body = em.lines
         act = COMP_T[out_dt]
-        if red.prim == "reduce_sum":
-            upd = f"acc = {em.round(f'acc + {val}', out_dt)};"
-            init = "0"
-        else:
-            fn = "dmax_n" if act == "double" else "fmax_n"
-            upd = f"acc = {fn}(acc, {val});" if D.is_float(out_dt) else f"acc = acc > {val} ? acc : {val};"
-            init = "-INFINITY" if D.is_float(out_dt) else str(_int_range(out_dt)[0]).split(".")[0] + "LL"
+        upd = f"acc = {_red_update(em, red.prim, out_dt, 'acc', val)};"
+        init = _red_identity(red.prim, out_dt)
         self.atomic = atomic
         threads = 256
         self.grid, self.block, self.lds = (-(-O // threads), nchunks, 1), (threads, 1, 1), 0
@@ -978,14 +1050,19 @@ class HorizontalKernel:
 
 def _scatter_kernel(self):
     """``scatter_add``: the output already holds the operand (a fill or copy step before it); each update
-    element is added atomically at the entry its index picks (float32; the order of the adds differs from the
-    reference's sequential one, within float32 rounding)."""
+    element is added atomically at the entry its index picks (float32: the order of the adds differs from the
+    reference's sequential one, within float32 rounding; 32/64-bit integers: bit-exact, wrapping)."""
     g, st = self.graph, self.step
     n = st.nodes[0]
     x, ix, u = (g.types[v] for v in n.inputs)
     axis = n.params["axis"]
-    if x.dtype != "float32":
-        raise Unfusable(n.output, f"scatter_add into {x.dtype} (atomic adds are float32)")
+    # float32 adds are atomic float adds; 32/64-bit integers add as unsigned words, which wrap exactly like
+    # the reference's two's-complement sum in any order
+    atom = {"float32": ("float", "float"), "int32": ("unsigned int", "unsigned int"),
+            "uint32": ("unsigned int", "unsigned int"), "int64": ("unsigned long long", "unsigned long long"),
+            "uint64": ("unsigned long long", "unsigned long long")}.get(x.dtype)
+    if atom is None:
+        raise Unfusable(n.output, f"scatter_add into {x.dtype} (atomic adds are float32 or 32/64-bit integers)")
     em = Emitter(g, [], {v: (k, self.views[v]) for k, v in enumerate(st.inputs)})
     um = em.multi(("flat", "e"), u.shape)
     r = len(ix.shape)
@@ -1004,14 +1081,15 @@ def _scatter_kernel(self):
     for k, v in enumerate(st.inputs):
         params.append(f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k}")
         self.args.append(("in", v))
-    params.append(f"float* __restrict__ out0")
+    params.append(f"{atom[0]}* __restrict__ out0")
     self.args.append(("out", n.output))
     src = [
         f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({", ".join(params)}) {{',
         f"  for (int64_t e = (int64_t)blockIdx.x * {threads} + threadIdx.x; e < {NU}LL; e += (int64_t)gridDim.x * {threads}) {{",
     ]
     src += ["    " + l for l in em.lines]
-    src += [f"    atomicAdd(&out0[{addr}], (float){val});", "  }", "}"]
+    cv = f"(float){val}" if x.dtype == "float32" else f"({atom[1]})(int64_t){val}"
+    src += [f"    atomicAdd(&out0[{addr}], {cv});", "  }", "}"]
     return "\n".join(src)
 
 

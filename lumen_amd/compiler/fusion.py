@@ -46,6 +46,59 @@ class Step:
         return " → ".join(n.prim for n in self.nodes[:6]) + (" → …" if len(self.nodes) > 6 else "")
 
 
+def row_broadcast(src, out, dims, rows) -> bool:
+    """Whether broadcasting ``src`` (numel R) to ``out`` (numel R x C) along ``dims`` repeats each row's
+    value over that row's C elements of the row space ``rows`` = (R, C): the output's leading axes spanning R
+    each come from a source axis of the same size (in order), and every other source axis has size 1."""
+    R, C = rows
+    if src.numel() != R or out.numel() != R * C:
+        return False
+    k = 0
+    while k < len(out.shape) and math.prod(out.shape[:k]) < R:
+        k += 1
+    if math.prod(out.shape[:k]) != R:
+        return False
+    covered = set()
+    for i, d in enumerate(dims):
+        if d < k:
+            if src.shape[i] != out.shape[d]:
+                return False
+            covered.add(d)
+        elif src.shape[i] != 1:
+            return False
+    return all(out.shape[d] == 1 for d in range(k) if d not in covered)
+
+
+def row_reads_ok(graph, nodes, rows) -> bool:
+    """Whether a row kernel of ``nodes`` over ``rows`` reads every row statistic (its reductions and values
+    computed from them alone) at its own row. The kernel holds a statistic for the current row only, so a
+    statistic that reaches the elements through anything but a row broadcast (a transposed broadcast of a
+    log-sum-exp, say) cannot be computed there."""
+    if rows is None:
+        return True
+    R = rows[0]
+    users = {}
+    for m in nodes:
+        for u in m.inputs:
+            users.setdefault(u, []).append(m)
+    stack = [m.output for m in nodes if m.prim in ("reduce_sum", "reduce_max")]
+    seen = set(stack)
+    while stack:
+        v = stack.pop()
+        for c in users.get(v, []):
+            t = graph.types[c.output]
+            if c.prim == "broadcast_in_dim" and t.numel() != R:
+                if not row_broadcast(graph.types[v], t, c.params["broadcast_dimensions"], rows):
+                    return False
+                continue
+            if t.numel() != R or not (c.prim in ("reshape", "broadcast_in_dim") or c.prim in ELEMENTWISE):
+                return False
+            if c.output not in seen:
+                seen.add(c.output)
+                stack.append(c.output)
+    return True
+
+
 def _row_space(graph, n):
     """``(R, C)`` of a reduction over trailing axes, or None."""
     x = graph.types[n.inputs[0]]
@@ -174,6 +227,8 @@ def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
                 if rs is None or (rows[k] is not None and rows[k] != rs):
                     continue
                 if not all(graph.types[r].numel() in (rs[0] * rs[1], rs[0]) for r in roots[k]):
+                    continue
+                if not row_reads_ok(graph, [m for m in graph.nodes if m.output in mem or m.output == u], rs):
                     continue
             if outside or u in must:
                 if not _fits(graph, u, roots[k], rows[k] if p.prim not in ("reduce_sum", "reduce_max") else _row_space(graph, p)):
@@ -459,7 +514,10 @@ def absorb_rows(graph, steps):
             if not ok:
                 continue
             have = {m.output for m in rt.nodes}
-            rt.nodes = sorted(rt.nodes + [m for m in lt.nodes if m.output not in have], key=lambda m: m.output)
+            joined = sorted(rt.nodes + [m for m in lt.nodes if m.output not in have], key=lambda m: m.output)
+            if not row_reads_ok(graph, joined, rt.rows):
+                continue
+            rt.nodes = joined
             rt.outputs = list(rt.outputs) + [v for v in lt.outputs if v not in rt.outputs]
             rt.inputs = _inputs_of(rt.nodes)
             for v in lt.outputs:

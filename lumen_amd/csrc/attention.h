@@ -751,6 +751,8 @@ inline int check_attn(const nhip_attn_desc *d, const char *what) {
         return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
+    if (d->causal && d->sk < d->sq)
+        return fail(std::string(what) + ": causal with fewer keys than queries (rows without keys) has no kernel");
     if ((d->sq + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31) || (d->sk + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31))
         return fail(std::string(what) + ": more than 2^31 workgroups");
     return 0;

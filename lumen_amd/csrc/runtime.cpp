@@ -471,6 +471,19 @@ int nhip_plan_add_launch(void *plan, void *function, const uint32_t grid[3], con
 int nhip_plan_add_builtin(void *plan, int kind, const void *desc, size_t desc_bytes, const nhip_reloc *relocs,
                           size_t nrelocs) {
     if (kind < NHIP_STEP_GEMM || kind > NHIP_STEP_LCE) return fail("nhip_plan_add_builtin: unknown step kind");
+    // the descriptor must hold what run_steps reads for the kind
+    size_t need = 0;
+    switch (kind) {
+        case NHIP_STEP_GEMM: need = sizeof(nhip_gemm_desc); break;
+        case NHIP_STEP_FLASH_FWD:
+        case NHIP_STEP_FLASH_BWD: need = sizeof(nhip_attn_desc); break;
+        case NHIP_STEP_COPY: need = 8; break;
+        case NHIP_STEP_FILL: need = 12; break;
+        case NHIP_STEP_LCE: need = sizeof(nhip_lce_desc); break;
+    }
+    if (!desc || desc_bytes < need)
+        return fail("nhip_plan_add_builtin: a descriptor of " + std::to_string(desc_bytes) + " bytes for a step kind " +
+                    "that reads " + std::to_string(need));
     if (check_relocs(relocs, nrelocs, 16, false)) return 1;
     Step s;
     s.kind = kind;
@@ -554,11 +567,14 @@ static int run_steps(Plan *plan, void *workspace, void *const *inputs, size_t ni
     if (begin > end || end > plan->steps.size())
         return fail("nhip_plan_run_steps: steps [" + std::to_string(begin) + ", " + std::to_string(end) + ") of " +
                     std::to_string(plan->steps.size()));
-    const bool whole = events && begin == 0 && end == plan->steps.size();
+    // per-step events only when profiling has created one for every step boundary (steps added after
+    // nhip_plan_profile(1) run untimed until it is called again)
+    const bool whole = events && begin == 0 && end == plan->steps.size() && plan->profile &&
+                       plan->events.size() >= plan->steps.size() + 1;
     char *ws = static_cast<char *>(workspace);
     for (size_t i = begin; i < end; ++i) {
         Step &st = plan->steps[i];
-        if (whole && plan->profile && check(hipEventRecord(plan->events[i], s), "hipEventRecord")) return 1;
+        if (whole && check(hipEventRecord(plan->events[i], s), "hipEventRecord")) return 1;
         auto resolve = [&](const nhip_reloc &r, void **out) -> int {
             char *base;
             if (r.base == NHIP_BASE_WORKSPACE) {
@@ -621,7 +637,7 @@ static int run_steps(Plan *plan, void *workspace, void *const *inputs, size_t ni
         }
         if (rc) return fail("plan step " + std::to_string(i) + ": " + g_error);
     }
-    if (whole && plan->profile && check(hipEventRecord(plan->events[plan->steps.size()], s), "hipEventRecord"))
+    if (whole && check(hipEventRecord(plan->events[plan->steps.size()], s), "hipEventRecord"))
         return 1;
     return 0;
 }

@@ -270,15 +270,42 @@ def stack(tensors, dim=0):
     return cat([t.unsqueeze(d) for t in tensors], d)
 
 
-def argmax(input, dim=-1):
-    """Index of the first maximum along ``dim`` (int64), as the smallest index whose value equals the max."""
+def _order_flip(x):
+    """Reverses the order of ``x``'s values bijectively: negation, or bitwise not for unsigned and bool
+    (whose negation would not reverse their order)."""
+    if x.dtype == "bool" or x.dtype.startswith("uint"):
+        return prims.not_(x)
+    return prims.neg(x)
+
+
+def amin(input, dim=(), keepdim=False):
+    """Minimum over ``dim`` (every axis if empty), as the order-flipped maximum of the order-flipped values
+    (``functions.py:581-592``; the graph has no separate minimum reduction)."""
     x = lift(input)
+    return _order_flip(amax(_order_flip(x), dim, keepdim))
+
+
+def _first_index(x, dim, keepdim, best):
+    """Smallest position along ``dim`` at which ``x`` equals ``best`` over that axis, int32
+    (``functions.py:613-626``). Positions not attaining it are replaced by the axis length, so the minimum of
+    the candidates is the first hit; a NaN maximum compares unequal everywhere, giving the axis length."""
+    if dim is None:
+        return _first_index(x.reshape((-1,)), 0, False, best)
     d = dim_of(dim, x.ndim)
-    m = amax(x, d, keepdim=True)
-    idx = prims.iota("int64", x.shape, d)
-    big = prims.full(x.shape, x.shape[d], "int64")
-    cand = prims.select(prims.eq(x, broadcast_to(m, x.shape)), idx, big)
-    return prims.neg(prims.reduce_max(prims.neg(cand), (d,)))
+    hit = prims.eq(x, broadcast_to(best(x, d, keepdim=True), x.shape))
+    pos = prims.iota("int32", x.shape, d)
+    miss = prims.full(x.shape, x.shape[d], "int32")
+    return amin(prims.select(hit, pos, miss), d, keepdim)
+
+
+def argmax(input, dim=None, keepdim=False):
+    """Index of the first maximum over ``dim`` (over every element when None), int32."""
+    return _first_index(lift(input), dim, keepdim, amax)
+
+
+def argmin(input, dim=None, keepdim=False):
+    """Index of the first minimum over ``dim`` (over every element when None), int32."""
+    return _first_index(lift(input), dim, keepdim, amin)
 
 
 __all__ = [n for n in dir() if not n.startswith("_") and n not in ("builtins", "math", "D", "Function", "prims")]

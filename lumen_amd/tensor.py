@@ -272,8 +272,8 @@ def empty(shape, dtype="float32", device="cpu", alignment=256):
 
 
 def from_numpy(arr):
-    arr = np.ascontiguousarray(arr)
-    return Tensor(D.canonical(arr.dtype), arr.shape, "cpu", host=arr.copy())
+    arr = np.array(arr, order="C", copy=True)  # keeps 0-d arrays 0-d (ascontiguousarray makes them 1-d)
+    return Tensor(D.canonical(arr.dtype), arr.shape, "cpu", host=arr)
 
 
 def tensor(data, dtype=None, device="cpu"):
@@ -283,7 +283,7 @@ def tensor(data, dtype=None, device="cpu"):
         dtype = "float32" if arr.dtype == np.float64 else src
     dtype = D.canonical(dtype)
     host = _convert(arr, src, dtype) if src != dtype else arr.astype(D.storage(dtype))
-    t = Tensor(dtype, arr.shape, "cpu", host=np.ascontiguousarray(host))
+    t = Tensor(dtype, arr.shape, "cpu", host=np.asarray(host, order="C"))
     return t.to(device=device) if device_type(device) != "cpu" else t
 
 

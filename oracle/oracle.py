@@ -122,3 +122,16 @@ def philox4x32(key, counter):
     o = (C.c_uint32 * 4)()
     lib().oracle_philox4x32(k, c, o)
     return list(o)
+
+
+def env(graph: Graph, inputs: list) -> dict:
+    """Every value of ``graph`` (inputs and each node's output) as NumPy values, keyed by value number: the
+    oracle's view of each intermediate, for step-by-step comparisons."""
+    import copy
+
+    g2 = copy.copy(graph)
+    g2.outputs = [n.output for n in graph.nodes]
+    out = dict(zip(g2.outputs, values(g2, inputs)))
+    for v, x in zip(graph.inputs, inputs):
+        out[v] = D.to_numpy_values(np.asarray(x.raw() if hasattr(x, "raw") else x), graph.types[v].dtype)
+    return out

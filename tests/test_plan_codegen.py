@@ -1,6 +1,7 @@
 """Plans on the CPU (no GPU needed): workspace placement never overlaps live values, layout ops feeding
 dots are strided views, and every generated loop kernel compiles for gfx950 with hipcc."""
 
+import numpy as np
 import pytest
 
 import lumen_amd as L
@@ -185,3 +186,30 @@ def test_hoisting_casts_into_producers_reads_fewer_bytes(monkeypatch):
                        for v in s.inputs) for s in p.steps if s.kind == "row")
 
     assert f32_terms(with_pass) < f32_terms(without)
+
+
+def test_row_statistics_are_read_only_at_their_own_row():
+    """A row kernel holds each statistic for its current row: a broadcast that repeats a row's value over
+    its row qualifies, a transposed one (the log-sum-exp of query i spread over the key axis of P^T, as
+    grouped-query attention's unfused backward reads it) does not, and fusion keeps such a reader out of
+    the row kernel so the generated kernel computes the right values."""
+    from lumen_amd.compiler.fusion import row_broadcast
+    from lumen_amd.graph.ir import TensorType as T
+
+    rows = (160, 40)
+    assert row_broadcast(T("float32", (1, 4, 40, 1)), T("float32", (1, 4, 40, 40)), (0, 1, 2, 3), rows)
+    assert row_broadcast(T("float32", (1, 4, 40)), T("float32", (1, 4, 40, 40)), (0, 1, 2), rows)
+    assert not row_broadcast(T("float32", (1, 4, 1, 40)), T("float32", (1, 4, 40, 40)), (0, 1, 2, 3), rows)
+    assert not row_broadcast(T("float32", (4, 40)), T("float32", (4, 40, 40)), (0, 2), rows)
+
+    rng = np.random.default_rng(0)
+    shapes = (1, 40, 4, 32), (1, 40, 2, 32), (1, 40, 2, 32), (1, 40, 4, 32)
+    ts = [L.tensor(rng.standard_normal(s).astype(np.float32), "bfloat16") for s in shapes]
+
+    def loss(q, k, v, w):
+        return F.sum((F.flash_attention(q, k, v, is_causal=True) * w).float())
+
+    p = Plan(L.make_graph(L.grad(loss, (0, 1, 2)))(*ts), "hip:0", build_kernels=False)
+    for si, st in enumerate(p.steps):
+        if st.kind == "row":
+            assert si in p.sources  # the generated source exists: no statistic read at another row
