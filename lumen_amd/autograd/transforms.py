@@ -11,7 +11,7 @@ import functools
 
 from lumen_amd import dtypes as D
 from lumen_amd.autograd import cross_entropy
-from lumen_amd.autograd.function import FUNCTION, gradients
+from lumen_amd.autograd.function import FUNCTION
 from lumen_amd.autograd.rules import NON_DIFFERENTIABLE, RULES
 from lumen_amd.graph import prims as P
 from lumen_amd.graph import tracer
@@ -69,18 +69,21 @@ def backward(out, ct, tape, leaves):
     return [cts.get(p.var) if D.is_float(p.dtype) else None for p in leaves]
 
 
-def _function_transpose(params, outs, cts, live):
+def _function_transpose(call, outs, cts, live):
+    """A recorded ``FunctionCall`` in reverse: its ``backward`` on the outputs' cotangents (zeros for outputs
+    without one), each gradient accumulated into its argument when that argument is differentiated."""
     cs = [cts.pop(o, None) for o in outs]
     if all(c is None for c in cs):
         return
-    fn, entries, n = params["function"], params["entries"], params["nargs"]
     filled = [c if c is not None else _zeros(o) for c, o in zip(cs, outs)]
-    grads = fn.backward(params["ctx"], *filled)
-    for (_, v), g in zip(entries, gradients(fn, grads, entries, n)):
-        if isinstance(v, TracedTensor) and g is not None and v.var in live:
-            if (g.dtype, tuple(g.shape)) != (v.dtype, tuple(v.shape)):
-                raise TypeError(f"{fn.__name__}.backward: returned {g.dtype}{list(g.shape)} for {v.dtype}{list(v.shape)}")
-            _accumulate(cts, v.var, g)
+    returned = call.function.backward(call.ctx, *filled)
+    for (_, v), g in zip(call.arguments, call.argument_gradients(returned)):
+        if not (isinstance(v, TracedTensor) and g is not None and v.var in live):
+            continue
+        if (g.dtype, tuple(g.shape)) != (v.dtype, tuple(v.shape)):
+            raise TypeError(f"{call.function.__name__}.backward: a {g.dtype}{list(g.shape)} gradient for a "
+                            f"{v.dtype}{list(v.shape)} argument")
+        _accumulate(cts, v.var, g)
 
 
 def _zeros(var):

@@ -14,6 +14,7 @@
  */
 #include <ctype.h>
 #include <math.h>
+#include <omp.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -644,6 +645,65 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
             csize *= (size_t)cshape[i];
         }
         Values v = vnew(args[0]->is_float, n);
+        /* Float32 accumulation over one contracting axis (every dot of the benchmark programs): the same
+           sequential k fold, acc = round(acc + round(x*y)), evaluated in float arithmetic. A float32 product
+           or sum rounded from the exact double result equals the float operation's own result (binary64
+           holds more than 2*24+2 bits, so rounding the double result to float is innocuous), so the values
+           are identical; the loop runs k-outer over a row of accumulators instead of one output at a
+           time. */
+        if (v.is_float && accum == F32 && nc == 1) {
+            size_t nr = 1;
+            int64_t rsh[8];
+            for (int i = 0; i < nrf; ++i) nr *= (size_t)(rsh[i] = r->shape[rfree[i]]);
+            size_t nouter = nr ? n / nr : 0;
+            int64_t *roff = (int64_t *)malloc((nr ? nr : 1) * sizeof(int64_t));
+            int64_t ridx[8] = {0};
+            for (size_t j = 0; j < nr; ++j) {
+                int64_t o2 = 0;
+                for (int i = 0; i < nrf; ++i) o2 += ridx[i] * rst[rfree[i]];
+                roff[j] = o2;
+                step_index(ridx, rsh, nrf);
+            }
+            int64_t osh[8];
+            int orank = lb->nints + nlf;
+            for (int i = 0; i < orank; ++i) osh[i] = out->shape[i];
+            const double *xf = args[0]->f, *yf = args[1]->f;
+            const int64_t sl = cl[0], sr = cr[0], K = cshape[0];
+            int unit = 1; /* rhs free elements consecutive in memory */
+            for (size_t j = 0; j < nr; ++j) unit &= roff[j] == (int64_t)j;
+            /* output rows are independent: threads split them (each row's fold is unchanged) */
+#pragma omp parallel
+            {
+                float *acc = (float *)malloc((nr ? nr : 1) * sizeof(float));
+#pragma omp for schedule(dynamic, 4)
+                for (size_t o = 0; o < nouter; ++o) {
+                    int64_t oi[8], rem = (int64_t)o;
+                    for (int i = orank - 1; i >= 0; --i) {
+                        oi[i] = rem % osh[i];
+                        rem /= osh[i];
+                    }
+                    int64_t lo = 0, ro = 0, pos = 0;
+                    for (int i = 0; i < lb->nints; ++i, ++pos) {
+                        lo += oi[pos] * lst[lb->ints[i]];
+                        ro += oi[pos] * rst[rb->ints[i]];
+                    }
+                    for (int i = 0; i < nlf; ++i, ++pos) lo += oi[pos] * lst[lfree[i]];
+                    for (size_t j = 0; j < nr; ++j) acc[j] = 0.0f;
+                    for (int64_t c = 0; c < K; ++c) {
+                        const double x = xf[lo + c * sl];
+                        const double *yb = yf + ro + c * sr;
+                        if (unit)
+                            for (size_t j = 0; j < nr; ++j) acc[j] = acc[j] + (float)(x * yb[j]);
+                        else
+                            for (size_t j = 0; j < nr; ++j) acc[j] = acc[j] + (float)(x * yb[roff[j]]);
+                    }
+                    for (size_t j = 0; j < nr; ++j) v.f[o * nr + j] = round_to((double)acc[j], dt);
+                }
+                free(acc);
+            }
+            free(roff);
+            return v;
+        }
         int64_t oidx[8] = {0};
         for (size_t o = 0; o < n; ++o) {
             int64_t lo = 0, ro = 0, pos = 0;
@@ -996,6 +1056,13 @@ static Values *eval_graph(const Graph *g, Values *inputs) {
         env[g->inputs[i]] = vclone(&inputs[i]);
         have[g->inputs[i]] = 1;
     }
+    /* each value is released after the last node reading it (outputs are kept): the evaluation order and
+       every value computed are unchanged, only the peak memory of large programs drops */
+    int *last = (int *)malloc((g->ntypes ? g->ntypes : 1) * sizeof(int));
+    for (int v = 0; v < g->ntypes; ++v) last[v] = -1;
+    for (int i = 0; i < g->nnodes; ++i)
+        for (int k = 0; k < g->nodes[i].nin; ++k) last[g->nodes[i].ins[k]] = i;
+    for (int i = 0; i < g->noutputs; ++i) last[g->outputs[i]] = g->nnodes;
     for (int i = 0; i < g->nnodes; ++i) {
         const Node *nd = &g->nodes[i];
         Values *args[64];
@@ -1021,7 +1088,15 @@ static Values *eval_graph(const Graph *g, Values *inputs) {
             env[nd->out] = eval_node(nd, args, types, &g->types[nd->out]);
         }
         have[nd->out] = 1;
+        for (int k = 0; k < nd->nin; ++k) {
+            const int u = nd->ins[k];
+            if (last[u] == i && have[u] && !extra[u]) {
+                vfree(&env[u]);
+                have[u] = 0;
+            }
+        }
     }
+    free(last);
     Values *outs = (Values *)calloc(g->noutputs ? g->noutputs : 1, sizeof(Values));
     for (int i = 0; i < g->noutputs; ++i) outs[i] = vclone(&env[g->outputs[i]]);
     for (int v = 0; v < g->ntypes; ++v) {
@@ -1094,6 +1169,9 @@ const char *oracle_error(void) { return g_err; }
 
 /* Evaluates the serialized graph `text` on raw input buffers, writing each output's storage into
  * `outputs[i]` (sized by the graph's output types). Returns 0 on success. */
+/* Threads the dot fold may split its independent output rows over (1 = the reference's single thread). */
+void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+
 int oracle_run(const char *text, const void *const *inputs, void *const *outputs) {
     g_err[0] = 0;
     Cursor c = {text};

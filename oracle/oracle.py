@@ -34,6 +34,8 @@ def lib():
         _lib = C.CDLL(LIBRARY)
         _lib.oracle_run.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]
         _lib.oracle_run.restype = C.c_int
+        _lib.oracle_set_threads.argtypes = [C.c_int]
+        _lib.oracle_set_threads.restype = None
         _lib.oracle_error.restype = C.c_char_p
         _lib.oracle_to_bf16.argtypes = [C.c_double]
         _lib.oracle_to_bf16.restype = C.c_uint16
@@ -87,6 +89,11 @@ def serialize(g: Graph) -> str:
     lines.append(f"outputs {len(g.outputs)} " + " ".join(map(str, g.outputs)))
     lines.append("end")
     return "\n".join(lines)
+
+
+def set_threads(n: int) -> None:
+    """Threads the oracle's dots may use (their output rows are independent; each fold is unchanged)."""
+    lib().oracle_set_threads(int(n))
 
 
 def run(graph: Graph, inputs: list) -> list:

@@ -1,0 +1,70 @@
+"""The benchmark's training step at its real widths compiled for hip, against golden fixtures the CPU oracle
+wrote for the same traced program (``tests/golden/make_transformer_golden.py``): config 4's model at batch 1
+of its 16 (every shape of the step but the batch), and one config-5 layer at batch 1.
+
+Bounds, on every sampled entry (2048 fixed entries per parameter, plus each full gradient's norm):
+- loss: within 1e-2 relative (``tests/test_transformer_example.py:316``);
+- each gradient (bf16): within rtol 2e-2 plus 1e-2 of that gradient's largest magnitude — the bf16 bound
+  with its absolute part scaled to the tensor, as the reference scales its attention-gradient atol
+  (``tests/functional/test_attention.py:413-416``); the norm within 2e-2 relative;
+- each SGD-updated weight (bf16): within one bf16 step of the oracle's plus the learning rate times the
+  gradient bound above — the update differs only through the gradient, then by one rounding (the
+  reference's rule of exact agreement where the gradient is clear of zero and a bounded update where it is
+  not, ``tests/test_transformer_example.py:318-331``, restated for SGD).
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import lumen_amd as L
+from lumen_amd import dtypes as D
+from tests.golden import transformer_cases as TC
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _bf16_step(w):
+    """The spacing of bf16 values at |w| (8 significant bits)."""
+    a = np.abs(np.asarray(w, np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 2.0**-133)))
+    return 2.0 ** (np.maximum(e, -133) - 7)
+
+
+@pytest.mark.parametrize("case", sorted(TC.CASES))
+def test_train_step_matches_golden(hip, case):
+    z = np.load(os.path.join(HERE, f"transformer_{case}.npz"))
+    meta = json.loads(str(z["meta"]))
+    cfg = TC.CASES[case]
+    assert meta["config"] == cfg.__dict__, "the fixture was made for another shape: regenerate it"
+    model, opt, weights, ids, targets = TC.setup(cfg)
+    assert TC.input_digest(weights, ids) == meta["digest"], "seeded inputs differ from the fixture's"
+    f = L.compile(TC.step_with_grads, device="hip")
+    outs = f(model, opt, L.from_numpy(ids), L.from_numpy(targets))
+    kinds = {s["kind"] for s in f.plan.describe()}
+    assert {"dot", "flash_fwd", "flash_bwd", "row"} <= kinds, kinds
+
+    loss, want_loss = float(L.to_numpy(outs[0])), float(z["loss"])
+    assert abs(loss - want_loss) <= 1e-2 * abs(want_loss), (loss, want_loss)
+    params = dict(model.named_parameters())
+    worst = []
+    for j, name in enumerate(meta["params"]):
+        idx = z[f"idx/{name}"]
+        g_full = np.asarray(L.to_numpy(outs[1 + j]), np.float64).ravel()
+        g, want = g_full[idx], z[f"grad/{name}"].astype(np.float64)
+        gmax = float(z[f"grad_max/{name}"])
+        bound = 2e-2 * np.abs(want) + 1e-2 * gmax
+        err = np.abs(g - want)
+        worst.append((float((err / bound).max()), name))
+        assert np.all(err <= bound), (name, float(err.max()), gmax)
+        norm, want_norm = np.linalg.norm(g_full), float(z[f"grad_norm/{name}"])
+        assert abs(norm - want_norm) <= 2e-2 * want_norm, (name, norm, want_norm)
+        new = D.bf16_to_f32(params[name]._placed("hip:0").raw()).astype(np.float64).ravel()[idx]
+        want_new = D.bf16_to_f32(z[f"new/{name}"]).astype(np.float64)
+        limit = _bf16_step(want_new) + TC.LR * bound
+        assert np.all(np.abs(new - want_new) <= limit), (name, float(np.abs(new - want_new).max()))
+    worst.sort(reverse=True)
+    print(f"{case}: loss {loss:.6f} vs {want_loss:.6f}; largest error / bound: {worst[:3]}")
