@@ -159,6 +159,13 @@ int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, con
 int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
                    const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace);
 int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes);
+/* nhip_flash_bwd without a workspace argument and without allocating: its scratch (delta and LSE, 8 bytes a
+ * query row) is a 16 MiB array in the library's device memory, one per GPU, held until the process ends.
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Fails for batch * heads * sq > 2^21 rows. Calls that overlap on
+ * one GPU (several host threads or streams) share the array and race. */
+int nhip_flash_bwd_noalloc(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
+                           const void *d_o, const float *lse, void *dq, void *dk, void *dv);
 
 /* ---- linear cross entropy (Primitive::LinearCrossEntropy, lumen/reference/mod.rs:1092-1120; the Triton kernel
  * lumen/codegen/dot_general/triton/linear_cross_entropy_kernel.py; the pass that emits it,
