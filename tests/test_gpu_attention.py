@@ -126,7 +126,9 @@ def test_flash_backward_config3_throughput(hip):
     lse = Dev(nbytes=b * n * s * 4)
     desc = attn_desc(b, s, s, n, n, d, True, 1 / math.sqrt(d))
     nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
-    gq, gk, gv, ws = Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=b * n * s * 4)
+    ws_bytes = C.c_size_t()
+    nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
+    gq, gk, gv, ws = Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=ws_bytes.value)
     args = (C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, g.ptr, lse.ptr, gq.ptr, gk.ptr, gv.ptr, ws.ptr)
     nv.call("nhip_flash_bwd", *args)
     nv.sync()
