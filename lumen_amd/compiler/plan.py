@@ -166,8 +166,8 @@ def compile_graph(graph: Graph, packable=()) -> tuple[Graph, list]:
     packs = []
     if config.compiler.merge_dots and packable:
         g, packs = merge.merge_dots(g, set(packable))
-        if packs:
-            g = passes.frontend(g)
+    # after every pattern match: the structural rewrites too (``pipeline.rs``: simplify follows the matchers)
+    g = passes.frontend(g, matched=config.compiler.simplify_structural)
     return g, packs
 
 

@@ -17,6 +17,8 @@ class CompilerFlags:
     autotune: bool = True             # time GEMM tile candidates before a plan's first run
     deterministic: bool = True        # attention backward without atomics
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
+    # simplify's structural rewrites after pattern matching (swapped/folded dots, ops moved across layouts)
+    simplify_structural: bool = True
     # a cross entropy over h . w^T logits nothing else reads becomes one linear_cross_entropy step
     # (graph_compiler/config/mod.rs:115, on by default)
     fused_linear_cross_entropy: bool = True

@@ -187,3 +187,47 @@ def test_linear_cross_entropy_through_the_pipeline():
     with L.config.compiler.patch(fused_linear_cross_entropy=False):
         p = Plan(L.make_graph(_eval_ce)(h, w, t), build_kernels=False)
     assert "linear_cross_entropy" not in [s.kind for s in p.steps]
+
+
+def _prims(g):
+    return [n.prim for n in g.nodes]
+
+
+REWRITES = {
+    # name: (program, input shapes, check of the simplified graph) — identities and compositions
+    "mul_one": (lambda x: (x * 1.0) * (1.0 * x), [((4, 5), "float32")],
+                lambda g: _prims(g).count("mul") == 1),
+    "add_sub_div": (lambda x: ((x + 0.0) - 0.0) / 1.0 + (0.0 + x), [((3, 7), "bfloat16")],
+                    lambda g: _prims(g) == ["add"]),
+    "double_neg": (lambda x: -(-x) * 3.0, [((6,), "float32")], lambda g: "neg" not in _prims(g)),
+    "select_same": (lambda x, y: F.where(x > y, x, x), [((4, 4), "float32"), ((4, 4), "float32")],
+                    lambda g: "select" not in _prims(g)),
+    "broadcasts": (lambda x: x.reshape(4, 1).expand(4, 6).reshape(1, 4, 6).expand(3, 4, 6) * 2.0,
+                   [((4,), "float32")], lambda g: True),
+    # structural (after matching): a transposed dot, transposed operands, moved casts and elementwise ops
+    "dot_transposed": (lambda x, w: F.matmul(x, w, "float32", "float32").t() + 1.0,
+                       [((8, 16), "float32"), ((16, 4), "float32")],
+                       lambda g: "transpose" not in _prims(g)),
+    "dot_operand_transposed": (lambda x, w: F.matmul(x.t(), w.t(), "float32", "float32"),
+                               [((16, 8), "float32"), ((4, 16), "float32")],
+                               lambda g: "transpose" not in _prims(g)),
+    "widening_cast_after_layout": (lambda x: x.float().t().reshape(20) * 2.0, [((4, 5), "bfloat16")],
+                                   lambda g: _prims(g).index("cast") > _prims(g).index("reshape")),
+    "narrowing_cast_before_layout": (lambda x: (x * 3.0).t().bfloat16(), [((4, 5), "float32")],
+                                     lambda g: _prims(g).index("cast") < _prims(g).index("transpose")),
+    "elementwise_before_reshape": (lambda x, y: F.exp(x.reshape(10, 2) * y.reshape(10, 2)),
+                                   [((4, 5), "float32"), ((4, 5), "float32")],
+                                   lambda g: _prims(g)[-1] == "reshape"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(REWRITES))
+def test_simplify_rewrites_keep_values_bit_for_bit(name):
+    """Each rewrite of simplify (``passes/simplify.rs``) on a program that exercises it: the rewritten graph
+    has the expected structure and the oracle computes the same bits from both (random inputs, twice)."""
+    fn, shapes, check = REWRITES[name]
+    g = L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in shapes])
+    s = passes.frontend(g, matched=True)
+    assert check(s), str(s)
+    for seed in (0, 1):
+        _same(g, s, seed)
