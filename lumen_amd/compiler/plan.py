@@ -17,7 +17,7 @@ from dataclasses import dataclass
 
 from lumen_amd import dtypes as D
 from lumen_amd.compiler import attention as attn_pass
-from lumen_amd.compiler import codegen, fusion, kcache, merge, passes
+from lumen_amd.compiler import codegen, fusion, kcache, merge, passes, remat, schedule
 from lumen_amd.config import config
 from lumen_amd.graph.ir import Graph
 
@@ -174,10 +174,31 @@ def compile_graph(graph: Graph, packable=()) -> tuple[Graph, list]:
 class Plan:
     """A graph compiled for ``device`` (``"hip:0"``): steps, workspace layout and native step list."""
 
-    def __init__(self, graph: Graph, device="hip:0", build_kernels=True, packable=()):
+    def __init__(self, graph: Graph, device="hip:0", build_kernels=True, packable=(), compiled=None):
         self.device = device
         self.source_graph = graph
-        self.graph, self.packs = compile_graph(graph, packable)
+        self.graph, self.packs = compiled if compiled is not None else compile_graph(graph, packable)
+        self._lay_out()
+        limit = config.compiler.memory_limit
+        if limit and compiled is None and self.workspace_bytes > limit:
+            # remat.rs via plan/compile.rs:37-44: recompute values past the live-bytes peak
+            def plan_of(g):
+                return Plan(graph, device, build_kernels=False, compiled=(g, self.packs))
+
+            g = remat.rematerialize(self.graph, limit, plan_of)
+            if g is not self.graph:
+                self.graph = g
+                self._lay_out()
+        self.kernels = {}
+        self.sources = {}
+        self._native = None
+        if compiled is None or build_kernels:
+            self._gen_kernels()
+        if build_kernels:
+            self.build()
+
+    def _lay_out(self):
+        """Steps, schedule and placement of ``self.graph``."""
         # concatenations of a pack's weights: views of the first weight's memory (the caller stores a pack's
         # weights back to back, in order)
         self.packed = set()
@@ -186,15 +207,9 @@ class Plan:
             if n.prim == "concatenate" and n.params["dimension"] == 0 and tuple(n.inputs) in packed_inputs:
                 self.packed.add(n.output)
         self.steps = self._fuse()
-        self._place()
+        self._schedule()
         if config.compiler.fuse and config.compiler.epilogue_fusion and self._fuse_epilogues():
             self._place()
-        self.kernels = {}
-        self.sources = {}
-        self._native = None
-        self._gen_kernels()
-        if build_kernels:
-            self.build()
 
     # ---- fusion with fallback: groups the generator rejects are split
     def _fuse(self):
@@ -205,6 +220,25 @@ class Plan:
         if config.compiler.fuse and config.compiler.horizontal_fusion:
             steps = fusion.horizontal(self.graph, steps)
         return steps
+
+    # ---- schedule (plan/compile.rs:19-47): the step order whose placement needs the least workspace
+    def _schedule(self):
+        """Places the steps in their fused order and in each schedule of ``schedule.SCHEDULES``, keeping the
+        order with the smallest workspace (the fused order on ties); ``self.schedule`` names it."""
+        fused = list(self.steps)
+        self._place()
+        best = (self.workspace_bytes, "fused", fused)
+        self.schedule_bytes = {"fused": self.workspace_bytes}
+        if config.compiler.schedules:
+            for name, order_of in schedule.SCHEDULES.items():
+                self.steps = order_of(self.graph, fused)
+                self._place()
+                self.schedule_bytes[name] = self.workspace_bytes
+                if self.workspace_bytes < best[0]:
+                    best = (self.workspace_bytes, name, list(self.steps))
+        self.schedule = best[1]
+        self.steps = best[2]
+        self._place()
 
     # ---- placement
     def _place(self):

@@ -19,6 +19,11 @@ class CompilerFlags:
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
     # simplify's structural rewrites after pattern matching (swapped/folded dots, ops moved across layouts)
     simplify_structural: bool = True
+    # try the list and depth-first step schedules and keep the order needing the least workspace
+    schedules: bool = True
+    # workspace bytes a plan should fit in (0: no limit); above it values are rematerialized
+    # (graph_compiler/config/mod.rs:90 memory_limit)
+    memory_limit: int = 0
     # a cross entropy over h . w^T logits nothing else reads becomes one linear_cross_entropy step
     # (graph_compiler/config/mod.rs:115, on by default)
     fused_linear_cross_entropy: bool = True

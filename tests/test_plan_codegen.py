@@ -215,3 +215,48 @@ def test_row_statistics_are_read_only_at_their_own_row():
     for si, st in enumerate(p.steps):
         if st.kind == "row":
             assert si in p.sources  # the generated source exists: no statistic read at another row
+
+
+def _remat_program(x, w, w3, w4):
+    a = F.exp(x)                                               # elementwise of an input: cheap to recompute
+    h = F.relu(F.matmul(a, w, "float32", "float32"))           # a dot reads it before the peak
+    big = F.matmul(h, w3, "float32", "float32")                # the peak: a wide intermediate
+    scale = big.sum()                                          # the late dot needs the peak's result ...
+    late = F.matmul(a, w4 * scale, "float32", "float32")       # ... and reads `a` again after it
+    return late.sum(0)
+
+
+# `a` and `big` are both 16 MiB: with `a` recomputed, `big` reuses its memory
+REMAT_METAS = (((2048, 2048), "float32"), ((2048, 64), "float32"), ((64, 2048), "float32"), ((2048, 64), "float32"))
+
+
+def test_schedules_keep_the_smallest_workspace():
+    """The plan places its steps in the fused order and in the list and depth-first schedules and keeps the
+    order needing the least workspace (plan/compile.rs:19-47)."""
+
+    p = _plan(_remat_program, *REMAT_METAS)
+    assert set(p.schedule_bytes) == {"fused", "traced", "list", "dfs"}
+    assert p.workspace_bytes == min(p.schedule_bytes.values()) or p.schedule == "fused"
+    with L.config.compiler.patch(schedules=False):
+        q = _plan(_remat_program, *REMAT_METAS)
+    assert q.schedule == "fused"
+
+
+def test_memory_limit_rematerializes_values_without_changing_them():
+    """Above ``memory_limit`` a value written before the live-bytes peak and read after it is recomputed
+    before its late reader: the workspace shrinks and the oracle computes the same bits from the rewritten
+    graph. No schedule helps here: the late dot needs the peak's result."""
+    from oracle import oracle
+
+    # horizontal fusion would launch the small recomputation together with the first exp (it groups members
+    # of up to 2^20 elements)
+    with L.config.compiler.patch(horizontal_fusion=False):
+        p0 = _plan(_remat_program, *REMAT_METAS)
+        with L.config.compiler.patch(memory_limit=p0.workspace_bytes // 2):
+            p1 = _plan(_remat_program, *REMAT_METAS)
+    assert p1.workspace_bytes < p0.workspace_bytes
+    assert sum(n.prim == "exp" for n in p1.graph.nodes) == 2  # exp(x) computed twice
+    rng = np.random.default_rng(0)
+    xs = [(rng.standard_normal(s) * 0.1).astype(np.float32) for s, _ in REMAT_METAS]
+    for a, b in zip(oracle.run(p0.graph, xs), oracle.run(p1.graph, xs)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
