@@ -153,6 +153,10 @@ typedef struct {
 /* O = softmax(scale Q K^T [causal]) V, P rounded to the inputs' dtype before P V; writes LSE = m + log l
  * (kernel.py:99-102). */
 int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, void *o, float *lse);
+/* Number of forward tile configs nhip_attn_desc.config accepts (0: 128 queries a workgroup, the default for -1;
+ * 1: 256; 2: 64) for autotuning and forced configs (the CUDA attention `Config`,
+ * lumen/codegen/attention/cuda/mod.rs:312-420). */
+int nhip_attn_config_count(int *count);
 /* FlashAttention-2 backward (kernel.py:107-256): delta = rowsum(dO * O) (float32 [B, N, Sq]), then dK, dV
  * per key block and dQ per query block (deterministic: no atomics). `workspace` needs
  * nhip_flash_bwd_workspace bytes. */

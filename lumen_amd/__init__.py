@@ -5,7 +5,7 @@ pass pipeline over it and executes it as one static plan in one device workspace
 CDNA4 kernels (``libnhip.so``, C ABI in ``include/nhip.h``) and generated fused loop kernels.
 """
 
-from lumen_amd import autograd, functional, nn
+from lumen_amd import autograd, autotune, functional, nn
 from lumen_amd.autograd import grad, value_and_grad, vjp
 from lumen_amd.config import config
 from lumen_amd.graph import prims
@@ -19,6 +19,6 @@ int8, int16, int32, int64 = "int8", "int16", "int32", "int64"
 float16, bfloat16, float32, float64 = "float16", "bfloat16", "float32", "float64"
 
 __all__ = [
-    "Compiled", "Tensor", "autograd", "compile", "config", "empty", "from_numpy", "full", "functional", "grad",
+    "Compiled", "Tensor", "autograd", "autotune", "compile", "config", "empty", "from_numpy", "full", "functional", "grad",
     "make_graph", "nn", "ones", "prims", "tensor", "to_numpy", "value_and_grad", "vjp", "zeros",
 ]

@@ -498,7 +498,8 @@ def lower(plan, step):
     body = p["body"]
     loc = plan.loc
     a = nv.AttnDesc()
-    a.scale, a.causal, a.config = p["scale"], int(p["causal"]), -1
+    a.scale, a.causal = p["scale"], int(p["causal"])
+    a.config = getattr(step, "config", -1) if p["name"] == FWD else -1  # the forward's tile (autotuned or forced)
     if p["name"] == FWD:
         q, k, v = n.inputs
         (qb, qs, qd), (kb, ks, kd), (vb, vs, vd) = p["q_dims"], p["k_dims"], p["v_dims"]

@@ -818,14 +818,71 @@ class Plan:
     AUTOTUNE_MARGIN = 0.03
     _tuned: dict = {}
 
+    def _apply_forced(self):
+        """Configs of ``lumen_amd.autotune.use`` blocks: every plain GEMM step (any size) and every flash
+        forward step takes its family's forced config, untimed (``autotune/forced.rs``)."""
+        from lumen_amd import autotune
+
+        gemm, attn = autotune.forced(autotune.HipGemmConfig), autotune.forced(autotune.HipAttentionConfig)
+        for st in self.steps:
+            if gemm is not None and st.kind == "dot" and getattr(st, "splits", 1) == 1 \
+                    and getattr(st, "epi", None) is None:
+                st.config, st.forced = gemm.index, True
+            if attn is not None and st.kind == "flash_fwd":
+                st.config, st.forced = attn.index, True
+
     def _autotune(self, workspace_ptr, input_ptrs):
+        self._autotune_gemms(workspace_ptr, input_ptrs)
+        self._autotune_attention(workspace_ptr, input_ptrs)
+
+    ATTN_AUTOTUNE_FLOPS = 1 << 32  # flash forwards of fewer FLOPs keep the default tile
+
+    def _autotune_attention(self, workspace_ptr, input_ptrs):
+        """Times each forward tile config on a flash forward step's own operands (HIP events, 3 runs after a
+        warm-up) and keeps the fastest (a later one must win by ``AUTOTUNE_MARGIN``); picks are shared by
+        steps of the same shape, layout and dtype."""
+        from lumen_amd import native as nv
+
+        n_cfg = C.c_int()
+        nv.call("nhip_attn_config_count", C.byref(n_cfg))
+        ev0, ev1 = nv.Event(), nv.Event()
+        for si, st in enumerate(self.steps):
+            if st.kind != "flash_fwd" or getattr(st, "forced", False):
+                continue
+            flops, _ = self.cost(si)
+            if flops < self.ATTN_AUTOTUNE_FLOPS:
+                continue
+            kind, desc, ops = attn_pass.lower(self, st)
+            key = ("attn", desc.batch, desc.heads, desc.kv_heads, desc.sq, desc.sk, desc.head_dim, desc.dtype,
+                   desc.causal, desc.q_s, desc.k_s, desc.v_s, desc.o_s)
+            if key not in Plan._tuned:
+                ptrs = []
+                for loc in ops:
+                    base = workspace_ptr if loc.base[0] == "ws" else input_ptrs[loc.base[1]]
+                    ptrs.append(base + loc.offset * D.size_of(loc.dtype))
+                best, best_ms = 0, float("inf")
+                for cfg in range(n_cfg.value):
+                    desc.config = cfg
+                    nv.call("nhip_flash_fwd", C.byref(desc), *ptrs)  # warm-up
+                    ev0.record()
+                    for _ in range(3):
+                        nv.call("nhip_flash_fwd", C.byref(desc), *ptrs)
+                    ev1.record()
+                    ms = ev0.elapsed_ms(ev1) / 3
+                    if ms < best_ms * (1.0 - self.AUTOTUNE_MARGIN):
+                        best, best_ms = cfg, ms
+                Plan._tuned[key] = best
+            st.config = Plan._tuned[key]
+
+    def _autotune_gemms(self, workspace_ptr, input_ptrs):
         from lumen_amd import native as nv
 
         n_cfg = C.c_int()
         nv.call("nhip_gemm_config_count", C.byref(n_cfg))
         ev0, ev1 = nv.Event(), nv.Event()
         for st in self.steps:
-            if st.kind != "dot" or getattr(st, "splits", 1) > 1 or getattr(st, "epi", None) is not None:
+            if st.kind != "dot" or getattr(st, "splits", 1) > 1 or getattr(st, "epi", None) is not None \
+                    or getattr(st, "forced", False):
                 continue
             try:
                 d, ops = self._gemm_desc(st.nodes[0])
@@ -894,8 +951,10 @@ class Plan:
         autotunes the plan's large GEMMs on its own buffers (when ``config.compiler.autotune``)."""
         from lumen_amd import native as nv
 
-        if self._native is None and config.compiler.autotune:
-            self._autotune(workspace_ptr, input_ptrs)
+        if self._native is None:
+            self._apply_forced()
+            if config.compiler.autotune:
+                self._autotune(workspace_ptr, input_ptrs)
         plan = self._native_plan()
         arr = (C.c_void_p * max(1, len(input_ptrs)))(*input_ptrs)
         nv.call("nhip_plan_run", plan, C.c_void_p(workspace_ptr), arr, len(input_ptrs))

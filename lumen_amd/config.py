@@ -48,7 +48,10 @@ class CompilerFlags:
                 setattr(self, k, v)
 
     def key(self):
-        return tuple((f.name, getattr(self, f.name)) for f in dataclasses.fields(self) if f.name != "_version")
+        from lumen_amd import autotune
+
+        flags = tuple((f.name, getattr(self, f.name)) for f in dataclasses.fields(self) if f.name != "_version")
+        return flags + (("forced", autotune.forced_key()),)
 
 
 @dataclasses.dataclass

@@ -127,7 +127,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // the swizzled tile `dst`. When the operand spans less than 2^31 bytes the loads are buffer loads (the row
 // offset a uniform operand, the lane's offset fixed) and rows past `rows` read zeros; otherwise 64-bit global
 // loads with rows past `rows` clamped to the last row. Either way those rows' scores are masked.
-template <int D>
+template <int D, int NW = 4>
 __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs, int64_t k0, int64_t rows,
                                                 uint16_t *dst, int wave, int lane) {
     constexpr int RPS = 1024 / (D * 2);  // rows a wave instruction covers
@@ -137,7 +137,7 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, int(bytes), 0x00020000);
         const uint32_t so = uint32_t(k0 * rs * 2);
 #pragma unroll
-        for (int seg = wave; seg < SEGS; seg += 4) {
+        for (int seg = wave; seg < SEGS; seg += NW) {
             const int r = seg * RPS + lane / (D / 8);
             const int c = lane % (D / 8);
             const uint32_t vo = uint32_t((r * rs + ((c ^ kv_swz<D>(r)) << 3)) * 2);
@@ -146,7 +146,7 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
         return;
     }
 #pragma unroll
-    for (int seg = wave; seg < SEGS; seg += 4) {
+    for (int seg = wave; seg < SEGS; seg += NW) {
         const int r = seg * RPS + lane / (D / 8);
         const int c = lane % (D / 8);
         int64_t row = k0 + r;
@@ -156,8 +156,15 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
     }
 }
 
-template <int D, bool F16, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
+// Workgroup sizes of the forward kernel (the attention tile configs): NW waves of 32 queries each share every
+// K/V tile a workgroup streams through LDS. More waves read K and V fewer times per query; fewer fill the CUs
+// when there are few query blocks. Two workgroups a CU hold the 64 KiB (D = 128) double-buffered tiles, so
+// each wave keeps 256 VGPRs at 4 waves a workgroup and 8 (one workgroup a CU at 8).
+template <int NW> struct FwdOccupancy { static constexpr int kBlocks = NW >= 8 ? 1 : (NW >= 4 ? 2 : 4); };
+
+template <int D, bool F16, bool CAUSAL, int NW = 4>
+__global__ __launch_bounds__(64 * NW, FwdOccupancy<NW>::kBlocks) void flash_fwd_kernel(AttnParams p) {
+    constexpr int QB = 32 * NW;  // queries a workgroup
     constexpr int BN = 64;
     constexpr int DS = D / 16, DT = D / 32;
     constexpr int TILE = BN * D;  // elements
@@ -165,13 +172,13 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
-    const int64_t nqb = (p.sq + 127) / 128;
+    const int64_t nqb = (p.sq + QB - 1) / QB;
     int64_t unit, qblk;
     xcd_order(int64_t(gridDim.x) / nqb, nqb, unit, qblk);
     if (CAUSAL) qblk = nqb - 1 - qblk;  // longest rows first
     const int64_t b = unit / p.heads, n = unit % p.heads;
     const int64_t nkv = n / (p.heads / p.kv_heads);
-    const int64_t q0 = qblk * 128;
+    const int64_t q0 = qblk * QB;
     const int64_t qi = q0 + wave * 32 + l32;
     const bool qvalid = qi < p.sq;
     const int64_t wq_last = q0 + wave * 32 + 31;  // the wave's last query
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
 
     const int64_t shift = p.sk - p.sq;  // key j is visible to query i when j <= i + shift
     int64_t kend = p.sk;
-    if (CAUSAL) kend = min(p.sk, q0 + 128 + shift);
+    if (CAUSAL) kend = min(p.sk, q0 + QB + shift);
     const int ntiles = kend > 0 ? int((kend + BN - 1) / BN) : 0;
     // tiles before `nfull` need no mask for any query of the workgroup
     int64_t full_end = p.sk;
@@ -190,8 +197,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
     const int nfull = full_end > 0 ? int(full_end / BN) : 0;
 
     if (ntiles > 0) {
-        load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane);
-        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
+        load_tile_async<D, NW>(kp, p.k_s, 0, p.sk, smem, wave, lane);
+        load_tile_async<D, NW>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
     }
 
     uint4 qf[DS];
@@ -215,8 +222,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_kernel(AttnParams p) {
         __syncthreads();                // ... and every thread's; tile kt-1's buffer is free
         if (kt + 1 < ntiles) {
             uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
-            load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
-            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
+            load_tile_async<D, NW>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
+            load_tile_async<D, NW>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
         }
         if (CAUSAL && k0 > wq_last + shift) continue;  // every key of the tile is masked for this wave
         const char *Kb = reinterpret_cast<const char *>(Ks);
@@ -746,23 +753,38 @@ inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
     return p;
 }
 
+// The forward's tile configs (nhip_attn_desc.config; -1 is config 0): 0 = 4 waves (128 queries) a
+// workgroup, 1 = 8 waves (256 queries), 2 = 2 waves (64 queries). The backward kernels have one tile each.
+constexpr int kNumAttnConfigs = 3;
+
 inline int check_attn(const nhip_attn_desc *d, const char *what) {
     if (d->head_dim != 64 && d->head_dim != 128)
         return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
+    if (d->config >= kNumAttnConfigs)
+        return fail(std::string(what) + ": no attention tile config " + std::to_string(d->config));
     if (d->causal && d->sk < d->sq)
         return fail(std::string(what) + ": causal with fewer keys than queries (rows without keys) has no kernel");
-    if ((d->sq + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31) || (d->sk + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31))
+    if ((d->sq + 63) / 64 * d->heads * d->batch >= (int64_t(1) << 31) || (d->sk + 127) / 128 * d->heads * d->batch >= (int64_t(1) << 31))
         return fail(std::string(what) + ": more than 2^31 workgroups");
     return 0;
 }
 
+template <int D, bool F16, bool CAUSAL, int NW>
+int launch_fwd_nw(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
+    dim3 grid(unsigned((d->sq + 32 * NW - 1) / (32 * NW) * d->heads * d->batch));
+    hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL, NW>), grid, dim3(64 * NW), 0, s, p);
+    return check(hipGetLastError(), "flash_fwd launch");
+}
+
 template <int D, bool F16, bool CAUSAL>
 int launch_fwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
-    dim3 grid(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
-    hipLaunchKernelGGL((nhipk::flash_fwd_kernel<D, F16, CAUSAL>), grid, dim3(256), 0, s, p);
-    return check(hipGetLastError(), "flash_fwd launch");
+    switch (d->config < 0 ? 0 : d->config) {
+        case 1: return launch_fwd_nw<D, F16, CAUSAL, 8>(s, p, d);
+        case 2: return launch_fwd_nw<D, F16, CAUSAL, 2>(s, p, d);
+        default: return launch_fwd_nw<D, F16, CAUSAL, 4>(s, p, d);
+    }
 }
 
 int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v, void *o,

@@ -53,6 +53,11 @@ int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, con
     return flash_bwd_on(s, desc, q, k, v, o, d_o, lse, dq, dk, dv, workspace);
 }
 
+int nhip_attn_config_count(int *count) {
+    *count = kNumAttnConfigs;
+    return 0;
+}
+
 int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes) {
     *bytes = flash_bwd_workspace_bytes(desc);
     return 0;

@@ -129,6 +129,7 @@ SIGNATURES = {
         C.c_int,
     ),
     "nhip_flash_bwd_workspace": ([C.POINTER(AttnDesc), C.POINTER(C.c_size_t)], C.c_int),
+    "nhip_attn_config_count": ([C.POINTER(C.c_int)], C.c_int),
     "nhip_flash_bwd_noalloc": ([C.POINTER(AttnDesc)] + [C.c_void_p] * 9, C.c_int),
     "nhip_plan_create": ([C.POINTER(C.c_void_p)], C.c_int),
     "nhip_plan_destroy": ([C.c_void_p], C.c_int),

@@ -73,16 +73,18 @@ def test_flash_forward_config3_throughput(hip):
     o = Dev(nbytes=q.nbytes)
     lse = Dev(nbytes=b * n * s * 4)
     desc = attn_desc(b, s, s, n, n, d, True, 1 / math.sqrt(d))
-    nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
-    nv.sync()
-    e0, e1 = nv.Event(), nv.Event()
-    e0.record()
-    for _ in range(10):
-        nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
-    e1.record()
-    ms = e0.elapsed_ms(e1) / 10
     flops = 2 * b * n * s * s * d  # causal half of 4 B N S^2 D
-    print(f"flash fwd config3: {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s")
+    for cfg, waves in enumerate((4, 8, 2)):
+        desc.config = cfg
+        nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
+        nv.sync()
+        e0, e1 = nv.Event(), nv.Event()
+        e0.record()
+        for _ in range(10):
+            nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
+        e1.record()
+        ms = e0.elapsed_ms(e1) / 10
+        print(f"flash fwd config3, {waves} waves a workgroup: {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s")
     out = D.bf16_to_f32(o.get(q.shape, np.uint16))
     assert np.isfinite(out).all()
 
@@ -141,3 +143,48 @@ def test_flash_backward_config3_throughput(hip):
     flops = 2.5 * 2 * b * n * s * s * d
     print(f"flash bwd config3: {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s (algorithmic 2.5x fwd)")
     assert np.isfinite(D.bf16_to_f32(gq.get(q.shape, np.uint16))).all()
+
+
+@pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", [CASES[1], CASES[2], CASES[3], CASES[5]])
+def test_forward_tile_configs_agree_bit_for_bit(hip, b, sq, sk, n, nkv, d, causal):
+    """Every forward tile config (4, 8 or 2 waves a workgroup) gives the same bits: each query is one lane's,
+    its keys visited in the same tiles and order whatever the workgroup size."""
+    q, k, v = _inputs(b, sq, sk, n, nkv, d, seed=3)
+    dq, dk, dv = Dev(q), Dev(k), Dev(v)
+    count = C.c_int()
+    nv.call("nhip_attn_config_count", C.byref(count))
+    assert count.value == 3
+    outs = []
+    for cfg in range(count.value):
+        desc = attn_desc(b, sq, sk, n, nkv, d, causal, 1.0 / math.sqrt(d))
+        desc.config = cfg
+        o, lse = Dev(nbytes=q.nbytes), Dev(nbytes=b * n * sq * 4)
+        nv.call("nhip_flash_fwd", C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr)
+        outs.append((o.get(q.shape, np.uint16), lse.get((b, n, sq), np.float32)))
+    for o, lse in outs[1:]:
+        assert np.array_equal(o, outs[0][0])
+        assert np.array_equal(lse.view(np.uint32), outs[0][1].view(np.uint32))
+
+
+def test_forced_configs_reach_the_plan(hip):
+    """``autotune.use`` forces the GEMM and attention configs of a compiled plan, untimed; the results equal
+    the autotuned plan's within the bf16 tolerance (and the attention bit for bit)."""
+    from lumen_amd import autotune as A
+
+    rng = np.random.default_rng(4)
+    shapes = [(2, 256, 4, 64), (2, 256, 4, 64), (2, 256, 4, 64), (256, 256)]
+    ts = [L.tensor(rng.standard_normal(s).astype(np.float32), "bfloat16") for s in shapes]
+
+    def fn(q, k, v, w):
+        o = F.flash_attention(q, k, v, is_causal=True)
+        return F.matmul(o.reshape(512, 256), w, "float32", "bfloat16")
+
+    free = L.compile(fn, device="hip")
+    want = L.to_numpy(free(*ts))
+    with A.use(A.HipGemmConfig(3), A.HipAttentionConfig(waves=2)):
+        f = L.compile(fn, device="hip")
+        got = L.to_numpy(f(*ts))
+        steps = f.plan.steps
+    assert [getattr(s, "config", None) for s in steps if s.kind == "flash_fwd"] == [2]
+    assert [getattr(s, "config", None) for s in steps if s.kind == "dot"] == [3]
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
