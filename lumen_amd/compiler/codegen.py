@@ -62,18 +62,19 @@ DEV float ro_f32(double x) {
 // sign(x) (1 - 2 / (2^(2|x| log2 e) + 1)) on the hardware exp2 and reciprocal (2^... overflows to inf past
 // |x| = 44, giving +-1; NaN propagates). Within 2 ulp of the exact value with correctly rounded exp2 and
 // division (checked over [2^-31, 12] on the host).
+// Both branches are evaluated and one selected: lanes of a wave straddle 0.55, so a branch would run both
+// anyway, plus the exec-mask bookkeeping.
 DEV float tanh_f32(float x) {
   const float ax = fabsf(x);
-  if (ax < 0.55f) {
-    const float x2 = x * x;
-    float p = fmaf(x2, -6.349337287e-03f, 2.112270333e-02f);
-    p = fmaf(x2, p, -5.386411399e-02f);
-    p = fmaf(x2, p, 1.333269179e-01f);
-    p = fmaf(x2, p, -3.333331943e-01f);
-    return copysignf(fmaf(x * x2, p, x), x);  // keeps the sign of -0
-  }
+  const float x2 = x * x;
+  float p = fmaf(x2, -6.349337287e-03f, 2.112270333e-02f);
+  p = fmaf(x2, p, -5.386411399e-02f);
+  p = fmaf(x2, p, 1.333269179e-01f);
+  p = fmaf(x2, p, -3.333331943e-01f);
+  const float small = fmaf(x * x2, p, x);
   const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * ax);
-  return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), x);
+  const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+  return copysignf(ax < 0.55f ? small : big, x);  // keeps the sign of -0; NaN propagates through big
 }
 // exp in float32: x log2 e split into the rounded product hi and its error lo (fma residual plus x times
 // the low part of log2 e), then 2^hi on the hardware exp2 times (1 + lo ln 2). Within 2 ulp of the exact
@@ -85,6 +86,21 @@ DEV float exp_f32(float x) {
   lo = __builtin_isinf(x) ? 0.0f : lo;
   const float r = __builtin_amdgcn_exp2f(hi);
   return r * fmaf(lo, 0.6931471805599453f, 1.0f);
+}
+// a / b in float32 within 1 ulp (Markstein): the hardware reciprocal refined by one Newton step, the quotient
+// a * r corrected once by its residual a - b q. The reciprocal depends on b alone, so a divisor shared by many
+// quotients (a row's sum or deviation) is refined once. Divisors near the ends of the exponent range, zero,
+// infinities and NaN take the IEEE division (a branch uniform across a row's lanes).
+DEV float fdiv_f32(float a, float b) {
+  const float ab = fabsf(b);
+  if (!(ab > 0x1p-125f && ab < 0x1p+125f)) return a / b;
+  float r = __builtin_amdgcn_rcpf(b);
+  r = fmaf(fmaf(-b, r, 1.0f), r, r);
+  const float q = a * r;
+  const float q2 = fmaf(fmaf(-b, q, a), r, q);
+  // a zero quotient keeps a's sign (the correction would give +0 for -0 / b); an infinite or NaN dividend,
+  // or a quotient past the float range, is a * r's (inf, NaN, or the overflow) instead of the correction's NaN
+  return (q2 == 0.0f || !__builtin_isfinite(q2)) ? q : q2;
 }
 DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
@@ -191,6 +207,10 @@ class View:
 
 class Emitter:
     """Evaluates graph values of one kernel at index expressions, writing C statements."""
+
+    # float32 division as a refined reciprocal and one quotient correction (fdiv_f32, within 1 ulp) instead of
+    # the correctly rounded division sequence; the reciprocal of a row statistic is then computed once a row
+    FAST_DIV = True
 
     def __init__(self, graph: Graph, nodes, inputs: dict, rows=None):
         self.graph = graph
@@ -342,7 +362,9 @@ class Emitter:
                     self.emit(f"const {ct} {out} = ({a} > {b} ? {a} : {b});")
             else:
                 op = {"add": "+", "sub": "-", "mul": "*", "div": "/"}[p]
-                if D.is_float(dt):
+                if D.is_float(dt) and p == "div" and ct == "float" and Emitter.FAST_DIV:
+                    self.emit(f"const {ct} {out} = {self.round(f'fdiv_f32({a}, {b})', dt)};")
+                elif D.is_float(dt):
                     self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
                 elif p == "div":
                     # truncating; x / 0 = -1 and int64 min / -1 wraps to itself (the reference divides in i128
@@ -661,6 +683,8 @@ class LoopKernel:
     # another; at 512 threads two rows share a CU and overlap (0.51 -> 0.37 ms for the [8192, 32000]
     # cross-entropy row on MI355X)
     ROW_MAX_THREADS = 512
+    ROW_WAVE_CHUNKS = 64  # rows of at most this many vector chunks run one wavefront a row (4 rows a workgroup)
+    ROW_CHUNKS_PER_THREAD = 2
     # sums over leading axes: rows a workgroup sums before its atomic adds, and loads a thread keeps in flight
     LEAD_CHUNK = 128
     LEAD_UNROLL = 8
@@ -806,10 +830,13 @@ class LoopKernel:
                 V = cand
                 break
         chunks = -(-C // V)
-        if chunks <= 64:
+        if chunks <= self.ROW_WAVE_CHUNKS:
             T, rows_per_block = 64, 4
         else:
-            T = min(self.ROW_MAX_THREADS, -(-chunks // 64) * 64)
+            # at least ROW_CHUNKS_PER_THREAD chunks a thread: fewer, fuller waves spend less of the row's time
+            # in the block-wide reductions (config 2's 4096-wide rows: 69 us at 256 threads, 77-80 at 512)
+            per = -(-chunks // self.ROW_CHUNKS_PER_THREAD)
+            T = min(self.ROW_MAX_THREADS, max(64, -(-per // 64) * 64))
             rows_per_block = 1
         J = -(-chunks // T)
         exact = C % (T * V) == 0

@@ -313,3 +313,29 @@ def test_gemm_epilogue_column_sums_match_oracle(hip, m, n, k, monkeypatch):
     assert np.all(np.abs(got[0] - want[0]) <= 1e-4 * scale + 1e-6)
     assert np.all(np.abs(got[0] - ref[0]) <= 1e-4 * scale + 1e-6)
     np.testing.assert_allclose(got[1], want[1], rtol=2e-2, atol=1e-2 * np.abs(want[1]).max())
+
+
+def test_float32_division_is_within_1_ulp(hip):
+    """Generated float32 division (refined hardware reciprocal plus one quotient correction) against the
+    correctly rounded quotient: within 1 ulp everywhere, exact on at least 99% of random operands; zero,
+    infinite and NaN operands and divisors near the ends of the exponent range follow IEEE division
+    (signed zeros included)."""
+    rng = np.random.default_rng(21)
+    n = 1 << 20
+    a = (rng.standard_normal(n) * np.exp2(rng.integers(-60, 60, n))).astype(np.float32)
+    b = (rng.standard_normal(n) * np.exp2(rng.integers(-60, 60, n))).astype(np.float32)
+    sa = np.float32([1.0, -0.0, 0.0, 3.0, -3.0, np.inf, 1.0, np.nan, 1.0, 1e-40, 5.0, 1.0, 2.0, -0.0])
+    sb = np.float32([0.0, 2.0, -2.0, np.inf, -np.inf, 2.0, np.nan, 1.0, 1e-39, 3.0, 3e38, 1e-38, 2.0, -5.0])
+    x, y = np.concatenate([a, sa]), np.concatenate([b, sb])
+    f = L.compile(lambda x, y: x / y, device="hip")
+    got = np.asarray(L.to_numpy(f(L.from_numpy(x), L.from_numpy(y))), np.float32)
+    with np.errstate(all="ignore"):
+        want = x / y  # NumPy float32 division: correctly rounded
+    fin = np.isfinite(want[:n]) & (np.abs(want[:n]) >= np.float32(2.0 ** -126))
+    ulp = np.spacing(np.abs(want[:n][fin])).astype(np.float64)
+    err = np.abs(got[:n][fin].astype(np.float64) - want[:n][fin]) / ulp
+    assert err.max() <= 1.0, (err.max(), x[:n][fin][err.argmax()], y[:n][fin][err.argmax()])
+    assert (got[:n][fin] == want[:n][fin]).mean() >= 0.99
+    tail_g, tail_w = got[n:], want[n:]
+    same = (tail_g.view(np.uint32) == tail_w.view(np.uint32)) | (np.isnan(tail_g) & np.isnan(tail_w))
+    assert same.all(), (tail_g, tail_w)
