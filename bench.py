@@ -27,41 +27,55 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
-def cpu_baseline(cfg, budget_s=12.0):
-    """The oracle (1 thread) on a bounded sample: the first layer's QKV projection dot for a slice of the
-    tokens, scaled by the step's FLOPs (the step is dot-dominated)."""
+def cpu_baseline(cfg, seq=None, threads=None):
+    """The CPU oracle (the C restatement of lumen/reference/mod.rs) timed on a bounded sample of the workload:
+    one whole training step (forward, autograd backward, SGD update) of a one-layer model at the config's
+    widths (d, heads, FFN, vocab) on one sequence of ``seq`` tokens, scaled to the configured step by
+    algorithmic FLOPs (the step is dot-dominated). Its dots fold each output row in the reference's
+    sequential k order, rows split over ``threads`` host threads."""
+    import dataclasses
+
     import numpy as np
 
-    import lumen_amd as L
-    import lumen_amd.functional as F
-    from lumen_amd import dtypes as D
+    from lumen_amd import workloads as W
+    from lumen_amd.graph.trace import trace
     from oracle import oracle
 
-    d = cfg.dim
-    rows = 8
-    rng = np.random.default_rng(0)
-    total, flops = 0.0, 0
-    while total < budget_s / 4:
-        g = L.make_graph(lambda x, w: F.matmul(x, w.t(), "float32", "bfloat16"))(
-            L.empty([rows, d], "bfloat16", "meta"), L.empty([3 * d, d], "bfloat16", "meta")
-        )
-        x = D.bf16_bits(rng.standard_normal((rows, d)).astype(np.float32))
-        w = D.bf16_bits((0.02 * rng.standard_normal((3 * d, d))).astype(np.float32))
-        t = time.perf_counter()
-        oracle.run(g, [x, w])
-        total = time.perf_counter() - t
-        flops = 2 * rows * d * 3 * d
-        rows *= 2
-    rate = flops / total
-    step_s = cfg.step_flops() / rate
+    threads = threads or min(16, os.cpu_count() or 1)
+    seq = seq or min(cfg.seq, 256)
+    sample = dataclasses.replace(cfg, batch=1, layers=1, seq=seq)
+    model, opt = W.build(sample, lr=1e-2)
+    weights = W.init_weights(model)
+    W.load(model, weights)
+    ids, targets = W.batch(sample)
+    import lumen_amd as L
+
+    args = (model, opt, L.from_numpy(ids), L.from_numpy(targets))
+    traced = trace(W.train_step, args)
+    names = {id(p): n for n, p in model.named_parameters()}
+    ins = []
+    for kind, k in traced.layout:
+        if kind == "arg":
+            ins.append([ids, targets][k])
+        elif kind == "scalar":
+            ins.append(np.array(1e-2, np.float64))
+        else:
+            ins.append(weights[names[id(traced.weights[k])]])
+    oracle.set_threads(threads)
+    t = time.perf_counter()
+    oracle.run(traced.graph, ins)
+    total = time.perf_counter() - t
+    oracle.set_threads(1)
+    rate = sample.step_flops() / total
     return {
-        "value": round(step_s * 1e3, 1),
+        "value": round(cfg.step_flops() / rate * 1e3, 1),
         "unit": "ms/step",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"oracle (C restatement of lumen/reference/mod.rs) on the QKV dot [{rows // 2},{d}]x[{d},{3 * d}] "
-        f"bf16 ({flops / 1e9:.2f} GFLOP in {total:.2f} s, {rate / 1e9:.3f} GFLOP/s), scaled to the step's "
-        f"{cfg.step_flops() / 1e12:.1f} TFLOP; nproc={os.cpu_count()}",
+        "sample": f"oracle (C restatement of lumen/reference/mod.rs, dots' output rows over {threads} threads) on one "
+        f"whole train step of 1 layer at d={cfg.dim}, ffn={cfg.ffn}, vocab={cfg.vocab}, batch 1 x seq {seq} "
+        f"({sample.step_flops() / 1e9:.1f} GFLOP in {total:.2f} s, {rate / 1e9:.2f} GFLOP/s), scaled by FLOPs to "
+        f"the {cfg.step_flops() / 1e12:.1f} TFLOP step; nproc={os.cpu_count()}",
     }
 
 

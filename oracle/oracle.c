@@ -20,6 +20,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 typedef __int128 i128;
 
@@ -490,35 +491,45 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
     size_t n = numel(out);
 #define IS(s) (!strcmp(p, s))
     if (IS("add") || IS("sub") || IS("mul") || IS("div") || IS("max") || IS("eq") || IS("lt")) {
+        /* the operation is picked once; elements are independent, so large arrays split over threads */
+        enum { ADD, SUB, MUL, DIV, MAX, EQ, LT } op = IS("add") ? ADD : IS("sub") ? SUB : IS("mul") ? MUL
+                                                  : IS("div") ? DIV : IS("max") ? MAX : IS("eq") ? EQ : LT;
         const Values *x = args[0], *y = args[1];
         if (!x->is_float) {
             Values v = vnew(0, n);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
             for (size_t k = 0; k < n; ++k) {
                 i128 a = x->i[k], b = y->i[k], r;
-                if (IS("add")) r = a + b;
-                else if (IS("sub")) r = a - b;
-                else if (IS("mul")) r = (i128)((unsigned __int128)a * (unsigned __int128)b);
-                else if (IS("div")) r = b == 0 ? -1 : a / b;
-                else if (IS("max")) r = a > b ? a : b;
-                else if (IS("eq")) r = a == b;
-                else r = a < b;
+                switch (op) {
+                    case ADD: r = a + b; break;
+                    case SUB: r = a - b; break;
+                    case MUL: r = (i128)((unsigned __int128)a * (unsigned __int128)b); break;
+                    case DIV: r = b == 0 ? -1 : a / b; break;
+                    case MAX: r = a > b ? a : b; break;
+                    case EQ: r = a == b; break;
+                    default: r = a < b;
+                }
                 v.i[k] = wrap(r, dt);
             }
             return v;
         }
-        if (IS("eq") || IS("lt")) {
+        if (op == EQ || op == LT) {
             Values v = vnew(0, n);
-            for (size_t k = 0; k < n; ++k) v.i[k] = IS("eq") ? x->f[k] == y->f[k] : x->f[k] < y->f[k];
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
+            for (size_t k = 0; k < n; ++k) v.i[k] = op == EQ ? x->f[k] == y->f[k] : x->f[k] < y->f[k];
             return v;
         }
         Values v = vnew(1, n);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
         for (size_t k = 0; k < n; ++k) {
             double a = x->f[k], b = y->f[k], r;
-            if (IS("add")) r = a + b;
-            else if (IS("sub")) r = a - b;
-            else if (IS("mul")) r = a * b;
-            else if (IS("div")) r = a / b;
-            else r = fmax_nan(a, b);
+            switch (op) {
+                case ADD: r = a + b; break;
+                case SUB: r = a - b; break;
+                case MUL: r = a * b; break;
+                case DIV: r = a / b; break;
+                default: r = fmax_nan(a, b);
+            }
             v.f[k] = round_to(r, dt);
         }
         return v;
@@ -532,14 +543,19 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
         return v;
     }
     if (IS("exp") || IS("log") || IS("sqrt") || IS("tanh") || IS("logistic")) {
+        enum { EXP, LOG, SQRT, TANH, LOGISTIC } op = IS("exp") ? EXP : IS("log") ? LOG : IS("sqrt") ? SQRT
+                                                   : IS("tanh") ? TANH : LOGISTIC;
         Values v = vnew(1, n);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
         for (size_t k = 0; k < n; ++k) {
             double a = args[0]->f[k], r;
-            if (IS("exp")) r = exp(a);
-            else if (IS("log")) r = log(a);
-            else if (IS("sqrt")) r = sqrt(a);
-            else if (IS("tanh")) r = tanh(a);
-            else r = 1.0 / (1.0 + exp(-a));
+            switch (op) {
+                case EXP: r = exp(a); break;
+                case LOG: r = log(a); break;
+                case SQRT: r = sqrt(a); break;
+                case TANH: r = tanh(a); break;
+                default: r = 1.0 / (1.0 + exp(-a));
+            }
             v.f[k] = round_to(r, dt);
         }
         return v;
@@ -547,6 +563,7 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
     if (IS("cast")) {
         const Values *x = args[0];
         Values v = vnew(is_float(dt), n);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
         for (size_t k = 0; k < n; ++k) {
             if (!x->is_float && is_float(dt)) {
                 i128 a = x->i[k];
@@ -563,6 +580,7 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
     }
     if (IS("select")) {
         Values v = vnew(args[1]->is_float, n);
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
         for (size_t k = 0; k < n; ++k) {
             int c = args[0]->i[k] != 0;
             if (v.is_float) v.f[k] = c ? args[1]->f[k] : args[2]->f[k];
@@ -664,43 +682,72 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
                 roff[j] = o2;
                 step_index(ridx, rsh, nrf);
             }
-            int64_t osh[8];
-            int orank = lb->nints + nlf;
-            for (int i = 0; i < orank; ++i) osh[i] = out->shape[i];
             const double *xf = args[0]->f, *yf = args[1]->f;
             const int64_t sl = cl[0], sr = cr[0], K = cshape[0];
             int unit = 1; /* rhs free elements consecutive in memory */
             for (size_t j = 0; j < nr; ++j) unit &= roff[j] == (int64_t)j;
-            /* output rows are independent: threads split them (each row's fold is unchanged) */
-#pragma omp parallel
-            {
-                float *acc = (float *)malloc((nr ? nr : 1) * sizeof(float));
-#pragma omp for schedule(dynamic, 4)
-                for (size_t o = 0; o < nouter; ++o) {
-                    int64_t oi[8], rem = (int64_t)o;
-                    for (int i = orank - 1; i >= 0; --i) {
-                        oi[i] = rem % osh[i];
-                        rem /= osh[i];
-                    }
-                    int64_t lo = 0, ro = 0, pos = 0;
-                    for (int i = 0; i < lb->nints; ++i, ++pos) {
-                        lo += oi[pos] * lst[lb->ints[i]];
-                        ro += oi[pos] * rst[rb->ints[i]];
-                    }
-                    for (int i = 0; i < nlf; ++i, ++pos) lo += oi[pos] * lst[lfree[i]];
-                    for (size_t j = 0; j < nr; ++j) acc[j] = 0.0f;
-                    for (int64_t c = 0; c < K; ++c) {
-                        const double x = xf[lo + c * sl];
-                        const double *yb = yf + ro + c * sr;
-                        if (unit)
-                            for (size_t j = 0; j < nr; ++j) acc[j] = acc[j] + (float)(x * yb[j]);
-                        else
-                            for (size_t j = 0; j < nr; ++j) acc[j] = acc[j] + (float)(x * yb[roff[j]]);
-                    }
-                    for (size_t j = 0; j < nr; ++j) v.f[o * nr + j] = round_to((double)acc[j], dt);
+            /* a rhs whose free elements are not consecutive ([n, k] row-major, say) is first copied per batch
+               into a [k][n] block, so the accumulator row sweeps memory in order */
+            size_t nlrows = 1;
+            for (int i = 0; i < nlf; ++i) nlrows *= (size_t)l->shape[lfree[i]];
+            const size_t nbatch = nlrows ? nouter / nlrows : 0;
+            double *packed = unit ? NULL : (double *)malloc((size_t)(K ? K : 1) * (nr ? nr : 1) * sizeof(double));
+            for (size_t z = 0; z < nbatch; ++z) {
+                int64_t bi[8], rem = (int64_t)z, lob = 0, rob = 0;
+                for (int i = lb->nints - 1; i >= 0; --i) {
+                    bi[i] = rem % out->shape[i];
+                    rem /= out->shape[i];
                 }
-                free(acc);
+                for (int i = 0; i < lb->nints; ++i) {
+                    lob += bi[i] * lst[lb->ints[i]];
+                    rob += bi[i] * rst[rb->ints[i]];
+                }
+                const double *yrow = yf + rob; /* element (c, j) at yrow[c * ystep + j] */
+                int64_t ystep = sr;
+                if (!unit) {
+#pragma omp parallel for schedule(static)
+                    for (int64_t c = 0; c < K; ++c)
+                        for (size_t j = 0; j < nr; ++j) packed[(size_t)c * nr + j] = yf[rob + c * sr + roff[j]];
+                    yrow = packed;
+                    ystep = (int64_t)nr;
+                }
+                /* output rows are independent: threads split them (each row's fold is unchanged) */
+                /* blocks of RB rows share each pass over a rhs row (RB times less rhs traffic) */
+                enum { RB = 8 };
+                const size_t nblocks = (nlrows + RB - 1) / RB;
+#pragma omp parallel
+                {
+                    float *acc = (float *)malloc((size_t)RB * (nr ? nr : 1) * sizeof(float));
+#pragma omp for schedule(dynamic, 1)
+                    for (size_t blk = 0; blk < nblocks; ++blk) {
+                        const size_t r0 = blk * RB, rows = nlrows - r0 < RB ? nlrows - r0 : RB;
+                        int64_t lo[RB];
+                        for (size_t q = 0; q < rows; ++q) {
+                            int64_t off = lob, rem2 = (int64_t)(r0 + q);
+                            for (int i = nlf - 1; i >= 0; --i) {
+                                off += (rem2 % l->shape[lfree[i]]) * lst[lfree[i]];
+                                rem2 /= l->shape[lfree[i]];
+                            }
+                            lo[q] = off;
+                        }
+                        for (size_t j = 0; j < rows * nr; ++j) acc[j] = 0.0f;
+                        for (int64_t c = 0; c < K; ++c) {
+                            const double *yb = yrow + c * ystep;
+                            for (size_t q = 0; q < rows; ++q) {
+                                const double x = xf[lo[q] + c * sl];
+                                float *a = acc + q * nr;
+                                for (size_t j = 0; j < nr; ++j) a[j] = a[j] + (float)(x * yb[j]);
+                            }
+                        }
+                        for (size_t q = 0; q < rows; ++q) {
+                            const size_t o = z * nlrows + r0 + q;
+                            for (size_t j = 0; j < nr; ++j) v.f[o * nr + j] = round_to((double)acc[q * nr + j], dt);
+                        }
+                    }
+                    free(acc);
+                }
             }
+            free(packed);
             free(roff);
             return v;
         }
@@ -747,29 +794,44 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
     if (IS("reshape") || IS("host_wait") || IS("device_wait") || IS("to_host") || IS("to_device"))
         return vclone(args[0]);
     if (IS("broadcast_in_dim") || IS("transpose") || IS("slice") || IS("swap_pairs")) {
+        /* each output element reads one input element; per output dim, how far the input offset moves when
+           that index steps (0 along a broadcast dim), plus a base (a slice's start) */
         const Type *x = types[0];
-        int64_t xst[8], idx[8] = {0};
+        int64_t xst[8], step[8] = {0}, base = 0;
         strides_of(x, xst);
-        int64_t *src = (int64_t *)malloc((n ? n : 1) * sizeof(int64_t));
-        for (size_t k = 0; k < n; ++k) {
-            int64_t s = 0;
-            if (IS("broadcast_in_dim")) {
-                const Param *bd = need(nd, "broadcast_dimensions");
-                for (int i = 0; i < bd->nints; ++i) s += (x->shape[i] == 1 ? 0 : idx[bd->ints[i]]) * xst[i];
-            } else if (IS("transpose")) {
-                const Param *pm = need(nd, "permutation");
-                for (int i = 0; i < pm->nints; ++i) s += idx[i] * xst[pm->ints[i]];
-            } else if (IS("slice")) {
+        int swap = IS("swap_pairs");
+        if (IS("broadcast_in_dim")) {
+            const Param *bd = need(nd, "broadcast_dimensions");
+            for (int i = 0; i < bd->nints; ++i)
+                if (x->shape[i] != 1) step[bd->ints[i]] += xst[i];
+        } else if (IS("transpose")) {
+            const Param *pm = need(nd, "permutation");
+            for (int i = 0; i < pm->nints; ++i) step[i] = xst[pm->ints[i]];
+        } else {
+            for (int i = 0; i < x->rank; ++i) step[i] = xst[i];
+            if (IS("slice")) {
                 const Param *st = need(nd, "start_indices");
-                for (int i = 0; i < x->rank; ++i) s += (idx[i] + st->ints[i]) * xst[i];
-            } else {
-                for (int i = 0; i < x->rank; ++i) s += (i == x->rank - 1 ? (idx[i] ^ 1) : idx[i]) * xst[i];
+                for (int i = 0; i < x->rank; ++i) base += st->ints[i] * xst[i];
             }
-            src[k] = s;
-            step_index(idx, out->shape, out->rank);
         }
-        Values v = gather_by(args[0], n, src);
-        free(src);
+        Values v = vnew(args[0]->is_float, n);
+        const int r = out->rank;
+        const int64_t inner = r ? out->shape[r - 1] : 1, istep = r ? step[r - 1] : 0;
+        const size_t rows = inner ? n / (size_t)inner : 0;
+#pragma omp parallel for schedule(static) if (n > (1 << 16))
+        for (size_t row = 0; row < rows; ++row) {
+            int64_t off = base, rem = (int64_t)row;
+            for (int d = r - 2; d >= 0; --d) {
+                off += (rem % out->shape[d]) * step[d];
+                rem /= out->shape[d];
+            }
+            const size_t o = row * (size_t)inner;
+            for (int64_t c = 0; c < inner; ++c) {
+                const int64_t src = off + (swap ? (c ^ 1) : c) * istep;
+                if (v.is_float) v.f[o + c] = args[0]->f[src];
+                else v.i[o + c] = args[0]->i[src];
+            }
+        }
         return v;
     }
     if (IS("concatenate")) {
@@ -793,10 +855,11 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
     if (IS("full")) {
         const Param *fv = need(nd, "fill_value");
         Values v = vnew(is_float(dt), n);
+        const double f = is_float(dt) ? round_to(fv->kind == 'f' ? fv->fval : (double)fv->ival, dt) : 0.0;
+        const i128 i = is_float(dt) ? 0 : fv->kind == 'f' ? saturate(fv->fval, dt) : wrap(fv->ival, dt);
         for (size_t k = 0; k < n; ++k) {
-            if (is_float(dt)) v.f[k] = round_to(fv->kind == 'f' ? fv->fval : (double)fv->ival, dt);
-            else if (fv->kind == 'f') v.i[k] = saturate(fv->fval, dt);
-            else v.i[k] = wrap(fv->ival, dt);
+            if (is_float(dt)) v.f[k] = f;
+            else v.i[k] = i;
         }
         return v;
     }
@@ -1046,7 +1109,26 @@ static Values eval_node(const Node *nd, Values **args, const Type **types, const
 #undef IS
 }
 
+/* Optional time per primitive (ORACLE_PROFILE set in the environment): where the interpreter spends its
+   time, printed to stderr after each run. */
+static int prof_on = -1;
+static char prof_names[64][32];
+static double prof_secs[64];
+static int prof_n = 0;
+static void prof_add(const char *name, double secs) {
+    for (int i = 0; i < prof_n; ++i)
+        if (!strcmp(prof_names[i], name)) {
+            prof_secs[i] += secs;
+            return;
+        }
+    if (prof_n < 64) {
+        snprintf(prof_names[prof_n], 32, "%s", name);
+        prof_secs[prof_n++] = secs;
+    }
+}
+
 static Values *eval_graph(const Graph *g, Values *inputs) {
+    if (prof_on < 0) prof_on = getenv("ORACLE_PROFILE") != NULL;
     Values *env = (Values *)calloc(g->ntypes ? g->ntypes : 1, sizeof(Values));
     char *have = (char *)calloc(g->ntypes ? g->ntypes : 1, 1);
     /* extra outputs of multi-output fusions, read by fusion_output */
@@ -1085,7 +1167,13 @@ static Values *eval_graph(const Graph *g, Values *inputs) {
             int index = (int)need(nd, "index")->ival;
             env[nd->out] = vclone(&extra[nd->ins[0]][index]);
         } else {
+            struct timespec t0, t1;
+            if (prof_on) clock_gettime(CLOCK_MONOTONIC, &t0);
             env[nd->out] = eval_node(nd, args, types, &g->types[nd->out]);
+            if (prof_on) {
+                clock_gettime(CLOCK_MONOTONIC, &t1);
+                prof_add(nd->name, (t1.tv_sec - t0.tv_sec) + 1e-9 * (t1.tv_nsec - t0.tv_nsec));
+            }
         }
         have[nd->out] = 1;
         for (int k = 0; k < nd->nin; ++k) {
@@ -1172,6 +1260,12 @@ const char *oracle_error(void) { return g_err; }
 /* Threads the dot fold may split its independent output rows over (1 = the reference's single thread). */
 void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 
+static void prof_print(void) {
+    if (!prof_on) return;
+    for (int i = 0; i < prof_n; ++i) fprintf(stderr, "oracle %-24s %8.3f s\n", prof_names[i], prof_secs[i]);
+    prof_n = 0;
+}
+
 int oracle_run(const char *text, const void *const *inputs, void *const *outputs) {
     g_err[0] = 0;
     Cursor c = {text};
@@ -1187,6 +1281,7 @@ int oracle_run(const char *text, const void *const *inputs, void *const *outputs
     free(ins);
     free(outs);
     free_graph(g);
+    prof_print();
     return g_err[0] ? 1 : 0;
 }
 
