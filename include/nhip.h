@@ -148,6 +148,9 @@ typedef struct {
     int64_t dq_b, dq_s, dq_n;    /* backward only */
     int64_t dk_b, dk_s, dk_n;    /* backward only */
     int64_t dv_b, dv_s, dv_n;    /* backward only */
+    int32_t deterministic;       /* backward only: 1 = dQ by its own kernel (same bits every run); 0 = dQ added
+                                    atomically by the dK/dV kernel into a float32 buffer (the reference's
+                                    default, lumen/graph_compiler/config/mod.rs:117) */
 } nhip_attn_desc;
 
 /* O = softmax(scale Q K^T [causal]) V, P rounded to the inputs' dtype before P V; writes LSE = m + log l
@@ -158,8 +161,9 @@ int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, con
  * lumen/codegen/attention/cuda/mod.rs:312-420). */
 int nhip_attn_config_count(int *count);
 /* FlashAttention-2 backward (kernel.py:107-256): delta = rowsum(dO * O) (float32 [B, N, Sq]), then dK, dV
- * per key block and dQ per query block (deterministic: no atomics). `workspace` needs
- * nhip_flash_bwd_workspace bytes. */
+ * per key block, and dQ either per query block by a second kernel (desc->deterministic) or added atomically by
+ * the dK/dV kernel into a float32 [B, N, Sq, D] buffer in the workspace, then rounded into dq. `workspace`
+ * needs nhip_flash_bwd_workspace bytes (more when not deterministic). */
 int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
                    const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace);
 int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes);

@@ -500,6 +500,9 @@ def lower(plan, step):
     a = nv.AttnDesc()
     a.scale, a.causal = p["scale"], int(p["causal"])
     a.config = getattr(step, "config", -1) if p["name"] == FWD else -1  # the forward's tile (autotuned or forced)
+    from lumen_amd.config import config
+
+    a.deterministic = int(bool(config.compiler.deterministic))  # backward: dQ by its own kernel, or atomically
     if p["name"] == FWD:
         q, k, v = n.inputs
         (qb, qs, qd), (kb, ks, kd), (vb, vs, vd) = p["q_dims"], p["k_dims"], p["v_dims"]

@@ -15,7 +15,9 @@ class CompilerFlags:
     horizontal_fusion: bool = True    # merge small independent loop kernels into one launch
     epilogue_fusion: bool = True      # fuse elementwise consumers into GEMM stores
     autotune: bool = True             # time GEMM tile candidates before a plan's first run
-    deterministic: bool = True        # attention backward without atomics
+    # attention backward without atomics: dQ by a kernel of its own (same bits every run); off, as in the
+    # reference (graph_compiler/config/mod.rs:117), the dK/dV kernel adds dQ atomically
+    deterministic: bool = True
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
     # simplify's structural rewrites after pattern matching (swapped/folded dots, ops moved across layouts)
     simplify_structural: bool = True

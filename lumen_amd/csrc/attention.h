@@ -67,7 +67,8 @@ struct AttnParams {
     float *lse;
     const float *lse_in;
     float *delta;
-    int64_t sq, sk, heads, kv_heads;
+    float *dqacc;  // float32 [B, N, Sq, D] dQ accumulated atomically by the dK/dV kernel (null: deterministic)
+    int64_t sq, sk, heads, kv_heads, batch;
     int64_t q_b, q_s, q_n, k_b, k_s, k_n, v_b, v_s, v_n, o_b, o_s, o_n;
     int64_t do_b, do_s, do_n, dq_b, dq_s, dq_n, dk_b, dk_s, dk_n, dv_b, dv_s, dv_n;
     float scale;
@@ -339,6 +340,8 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *ls
     for (int d = lane; d < D; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
     acc = wave_sum(acc);
     const int64_t i = (b * p.heads + n) * p.sq + q;
+    if (p.dqacc)  // the row of the atomic dQ accumulator starts at zero
+        for (int d = lane; d < D; d += 64) p.dqacc[i * D + d] = 0.0f;
     if (lane == 0) {
         p.delta[i] = acc * p.scale;  // delta times the softmax scale: dS = P (dP scale - delta scale)
         lse2[i] = p.lse_in[i] * 1.4426950408889634f;
@@ -371,6 +374,11 @@ __global__ __launch_bounds__(256) void flash_prep_vec_kernel(AttnParams p, float
     }
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (live && p.dqacc) {  // the row of the atomic dQ accumulator starts at zero
+        float4 *z = reinterpret_cast<float4 *>(p.dqacc + ((b * p.heads + n) * p.sq + q) * D + 8 * sub);
+        z[0] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        z[1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     if (live && sub == 0) {
         const int64_t i = (b * p.heads + n) * p.sq + q;
         p.delta[i] = acc * p.scale;
@@ -390,14 +398,33 @@ __device__ __forceinline__ void load_row64_async(const float *src, int64_t k0, i
 
 // dK and dV for 128 keys (32 a wavefront, one key a lane of the C layout), looping over 64-query tiles of
 // every query head sharing the key/value head.
-template <int D, bool F16, bool CAUSAL>
+//
+// ATOMIC_DQ (the non-deterministic mode): the workgroup also adds each tile's dQ = dS K into the float32
+// accumulator p.dqacc, so no second kernel recomputes S and dP. The 128 keys' K rows stay in LDS for the
+// whole loop; each wave writes its dS (one key a lane) into a [query][key] LDS tile, and after a barrier each
+// wave computes dQ for its share of the 64 x D tile (32 head-dim columns, both query halves at D = 128; one
+// half at D = 64) over all 128 keys: A = dS rows (one query a lane), B = K read transposed (one head-dim
+// column a lane). Its adds are issued at the start of the next tile, so the wait for that tile's loads does
+// not also wait for adds just issued.
+template <int D> struct DkdvLds {
+    static constexpr int kTile = 64 * D;              // a Q or dO tile, elements
+    static constexpr int kDsPitch = 128 + 8;          // dS row pitch (elements): rows on distinct banks
+    static constexpr int kBase = 4 * kTile;           // Q0 dO0 Q1 dO1
+    static constexpr int kAtomic = kBase + 128 * D + 64 * kDsPitch;  // + K (128 keys) + dS
+};
+
+template <int D, bool F16, bool CAUSAL, bool ATOMIC_DQ = false>
 __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const float *lse2) {
     constexpr int BM = 64;
     constexpr int DS = D / 16, DT = D / 32;
     constexpr int TILE = BM * D;
-    __shared__ __align__(1024) uint16_t smem[4 * TILE];  // Q0 dO0 Q1 dO1
+    __shared__ __align__(1024) uint16_t smem[ATOMIC_DQ ? DkdvLds<D>::kAtomic : DkdvLds<D>::kBase];
     __shared__ __align__(16) float Ls[2][BM];
     __shared__ __align__(16) float Dl[2][BM];
+    uint16_t *const Ks = smem + DkdvLds<D>::kBase;    // ATOMIC_DQ: K rows [128][D], swizzled like a Q tile
+    uint16_t *const dSb = Ks + 128 * D;               // ATOMIC_DQ: dS [64 queries][kDsPitch]
+    (void)Ks;
+    (void)dSb;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
@@ -440,7 +467,33 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         if (wave == 0) load_row64_async(ls, q0, p.sq, Ls[j & 1], lane);
         if (wave == 1) load_row64_async(dl, q0, p.sq, Dl[j & 1], lane);
     };
+    if constexpr (ATOMIC_DQ) {  // waited for with the first tile's loads
+        load_tile_async<D>(kp, p.k_s, kb0, p.sk, Ks, wave, lane);
+        load_tile_async<D>(kp, p.k_s, kb0 + 64, p.sk, Ks + 64 * D, wave, lane);
+    }
     if (total > 0) issue(0);
+
+    // ATOMIC_DQ: this wave's dQ share of the previous tile, waiting to be added: NQ accumulators of 32 queries
+    // x 32 head-dim columns (query half qh0 + c, columns 32 * dblk ...)
+    constexpr int NQ = D == 128 ? 2 : 1;
+    const int dblk = D == 128 ? wave : (wave & 1), qh0 = D == 128 ? 0 : (wave >> 1);
+    f32x16_t adq[NQ];
+    float *dq_rows = nullptr;  // the previous tile's first dQ accumulator row (query q0, head n)
+    int64_t dq_left = 0;       // rows of that tile inside the queries
+    (void)qh0;
+    auto flush_dq = [&]() {
+        if constexpr (ATOMIC_DQ) {
+            if (!dq_rows) return;
+#pragma unroll
+            for (int c = 0; c < NQ; ++c)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 32 * (qh0 + c) + 8 * (e / 4) + 4 * h + (e % 4);
+                    if (r < dq_left) unsafeAtomicAdd(dq_rows + int64_t(r) * D + 32 * dblk + l32, adq[c][e]);
+                }
+            dq_rows = nullptr;
+        }
+    };
 
     uint4 kf[DS], vf[DS];
 #pragma unroll
@@ -464,6 +517,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        flush_dq();  // the previous tile's dQ adds, ahead of this iteration's loads
         if (j + 1 < total) issue(j + 1);
         const char *Qb = reinterpret_cast<const char *>(smem + (j & 1) * 2 * TILE);
         const char *Gb = Qb + TILE * 2;
@@ -534,6 +588,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                             const float dr = f4_at(d4[(jj + u) / 4], (jj + u) % 4);
                             float pe = fast_exp2(fmaf(sv[qs][e], c2, -lr));
                             if constexpr (MASKED) pe = ((r >= rmin) & (r < rmax)) ? pe : 0.0f;
+                            if constexpr (ATOMIC_DQ) pe = kvalid ? pe : 0.0f;  // keys past sk add nothing to dQ
                             pv[u] = pe;
                             dv2[u] = pe * fmaf(dp[qs][e], p.scale, -dr);
                         }
@@ -584,7 +639,60 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         mfma_then_ds<6 * DT, 2, 2>();
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * DT, 2);
         __builtin_amdgcn_sched_barrier(0);
+
+        if constexpr (ATOMIC_DQ) {
+            // dS (16-bit, as packed for dK) into the [query][key] tile: this lane's key, its 32 queries
+            const int key = 32 * wave + l32;
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t w[4] = {sb[qs][half].x, sb[qs][half].y, sb[qs][half].z, sb[qs][half].w};
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int e = 8 * half + jj;
+                        const int r = 32 * qs + 8 * (e / 4) + 4 * h + (e % 4);
+                        dSb[r * DkdvLds<D>::kDsPitch + key] = uint16_t(jj & 1 ? w[jj / 2] >> 16 : w[jj / 2] & 0xffffu);
+                    }
+                }
+            __syncthreads();
+            // dQ[q, d] = sum over the 128 keys of dS[q, key] K[key, d]: A = dS (one query a lane), B = K read
+            // transposed (one head-dim column a lane). The transposed read gives lane half h the keys
+            // k0 + 4 h + {0..3, 8..11} of a 16-key step, so the dS fragment takes the same keys.
+#pragma unroll
+            for (int c = 0; c < NQ; ++c)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) adq[c][e] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const int k0 = 16 * ks;
+                const int krow = k0 + 4 * h + s16 / 4;
+                const int col = 32 * dblk + 16 * (g & 1) + 4 * (s16 & 3);
+                v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(reinterpret_cast<char *>(Ks) + kv_off<D>(krow, col)));
+                v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(reinterpret_cast<char *>(Ks) + kv_off<D>(krow + 8, col)));
+                const uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                const uint4 kb = make_uint4(xa.x, xa.y, ya.x, ya.y);
+#pragma unroll
+                for (int c = 0; c < NQ; ++c) {
+                    const int q = 32 * (qh0 + c) + l32;
+                    const uint16_t *row = dSb + q * DkdvLds<D>::kDsPitch + k0 + 4 * h;
+                    const uint2 lo = *reinterpret_cast<const uint2 *>(row), hi = *reinterpret_cast<const uint2 *>(row + 8);
+                    const uint4 da = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    adq[c] = mfma32<F16>(da, kb, adq[c]);
+                }
+            }
+            {
+                const uint16_t *qp_, *gp_;
+                const float *ls_, *dl_;
+                int64_t q0_;
+                tile_src(j, qp_, gp_, ls_, dl_, q0_);
+                const int64_t n_ = nkv * group + j / per_head;
+                dq_rows = p.dqacc + ((b * p.heads + n_) * p.sq + q0_) * D;
+                dq_left = p.sq - q0_;
+            }
+        }
     }
+    if constexpr (ATOMIC_DQ) flush_dq();
     if (!kvalid) return;
     uint16_t *dkp = p.dk + b * p.dk_b + nkv * p.dk_n + kj * p.dk_s;
     uint16_t *dvp = p.dv + b * p.dv_b + nkv * p.dv_n + kj * p.dv_s;
@@ -598,6 +706,31 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
             *reinterpret_cast<uint2 *>(dvp + d) =
                 make_uint2(pack2<F16>(adv[dt][4 * e4], adv[dt][4 * e4 + 1]), pack2<F16>(adv[dt][4 * e4 + 2], adv[dt][4 * e4 + 3]));
         }
+}
+
+// The atomic dQ accumulator (float32 [B, N, Sq, D]) rounded into dq (its strides): eight head-dim elements a
+// thread, a 16-byte store when dq's rows allow it.
+template <int D, bool F16>
+__global__ __launch_bounds__(256) void flash_dq_round_kernel(AttnParams p) {
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t row = t / (D / 8), c = (t % (D / 8)) * 8;
+    const int64_t rows_all = p.heads * p.sq;
+    if (row >= p.batch * rows_all) return;
+    const int64_t b = row / rows_all, rem = row % rows_all, n = rem / p.sq, q = rem % p.sq;
+    const float4 x = *reinterpret_cast<const float4 *>(p.dqacc + row * D + c);
+    const float4 y = *reinterpret_cast<const float4 *>(p.dqacc + row * D + c + 4);
+    uint16_t *dst = p.dq + b * p.dq_b + n * p.dq_n + q * p.dq_s + c;
+    const uint4 v = make_uint4(pack2<F16>(x.x, x.y), pack2<F16>(x.z, x.w), pack2<F16>(y.x, y.y), pack2<F16>(y.z, y.w));
+    if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<uint4 *>(dst) = v;
+    } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dst[2 * i] = uint16_t(w[i] & 0xffffu);
+            dst[2 * i + 1] = uint16_t(w[i] >> 16);
+        }
+    }
 }
 
 // dQ for 128 queries (32 a wavefront), looping over 64-key tiles: S^T and dP^T one query a lane, dQ^T
@@ -731,8 +864,14 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
 namespace nhip {
 
 // delta and the base-2 LSE, float32 [B, N, Sq] each.
+// delta and the base-2 LSE (float32 [B, N, Sq] each), then, when not deterministic, the float32 dQ
+// accumulator [B, N, Sq, D], 16-byte aligned after them.
+inline size_t flash_bwd_dq_offset(const nhip_attn_desc *d) {
+    return (2 * size_t(d->batch) * d->heads * d->sq * sizeof(float) + 15) / 16 * 16;
+}
 inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
-    return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
+    if (d->deterministic) return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
+    return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * d->head_dim * sizeof(float);
 }
 
 inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
@@ -741,6 +880,7 @@ inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
     p.sk = d->sk;
     p.heads = d->heads;
     p.kv_heads = d->kv_heads;
+    p.batch = d->batch;
     p.q_b = d->q_b, p.q_s = d->q_s, p.q_n = d->q_n;
     p.k_b = d->k_b, p.k_s = d->k_s, p.k_n = d->k_n;
     p.v_b = d->v_b, p.v_s = d->v_s, p.v_n = d->v_n;
@@ -812,6 +952,7 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
 
 template <int D, bool F16, bool CAUSAL>
 int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
+    const bool atomic = p.dqacc != nullptr;
     dim3 gd(unsigned((d->heads * d->sq + 3) / 4), unsigned(d->batch));
     dim3 gk(unsigned((d->sk + 127) / 128 * d->kv_heads * d->batch));
     dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
@@ -832,6 +973,14 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
         hipLaunchKernelGGL((nhipk::flash_prep_kernel<D, F16>), gd, dim3(256), 0, s, p, lse2);
     }
     if (check(hipGetLastError(), "flash delta launch")) return 1;
+    if (atomic) {
+        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL, true>), gk, dim3(256), 0, s, p, lse2);
+        if (check(hipGetLastError(), "flash dkdv+dq launch")) return 1;
+        const int64_t rows = d->batch * d->heads * d->sq;
+        dim3 gc(unsigned((rows * (D / 8) + 255) / 256));
+        hipLaunchKernelGGL((nhipk::flash_dq_round_kernel<D, F16>), gc, dim3(256), 0, s, p);
+        return check(hipGetLastError(), "flash dq rounding launch");
+    }
     hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p, lse2);
     if (check(hipGetLastError(), "flash dkdv launch")) return 1;
     hipLaunchKernelGGL((nhipk::flash_dq_kernel<D, F16, CAUSAL>), gq, dim3(256), 0, s, p, lse2);
@@ -853,6 +1002,7 @@ int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.dk = static_cast<uint16_t *>(dk);
     p.dv = static_cast<uint16_t *>(dv);
     p.delta = static_cast<float *>(ws);
+    p.dqacc = d->deterministic ? nullptr : reinterpret_cast<float *>(static_cast<char *>(ws) + flash_bwd_dq_offset(d));
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_BWD(DD, FF, CC) return launch_bwd<DD, FF, CC>(s, p, d)
     if (d->head_dim == 128) {

@@ -78,7 +78,9 @@ class AttnDesc(C.Structure):
         ("causal", C.c_int32),
         ("scale", C.c_float),
         ("config", C.c_int32),
-    ] + [(f"{t}_{a}", C.c_int64) for t in ("q", "k", "v", "o", "do", "dq", "dk", "dv") for a in ("b", "s", "n")]
+    ] + [(f"{t}_{a}", C.c_int64) for t in ("q", "k", "v", "o", "do", "dq", "dk", "dv") for a in ("b", "s", "n")] + [
+        ("deterministic", C.c_int32),
+    ]
 
 
 class Reloc(C.Structure):

@@ -30,11 +30,12 @@ class Dev:
             pass
 
 
-def attn_desc(b, sq, sk, n, nkv, d, causal, scale, dtype=1):
+def attn_desc(b, sq, sk, n, nkv, d, causal, scale, dtype=1, deterministic=1):
     """Descriptor for contiguous [B, S, N, D] q/o/do/dq and [B, S, Nkv, D] k/v/dk/dv."""
     a = nv.AttnDesc()
     a.batch, a.heads, a.kv_heads, a.sq, a.sk, a.head_dim = b, n, nkv, sq, sk, d
     a.dtype, a.causal, a.scale, a.config = dtype, int(causal), scale, -1
+    a.deterministic = int(deterministic)
     for t in ("q", "o", "do", "dq"):
         setattr(a, f"{t}_b", sq * n * d)
         setattr(a, f"{t}_s", n * d)

@@ -89,15 +89,17 @@ def test_flash_forward_config3_throughput(hip):
     assert np.isfinite(out).all()
 
 
+@pytest.mark.parametrize("deterministic", [1, 0])
 @pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", CASES)
-def test_flash_backward_matches_unfused_graph(hip, b, sq, sk, n, nkv, d, causal):
-    """dQ, dK, dV from the three backward kernels against the oracle running the traced FlashAttention-2
-    backward (recomputed probabilities from the saved log-sum-exp), bf16 tolerance."""
+def test_flash_backward_matches_unfused_graph(hip, b, sq, sk, n, nkv, d, causal, deterministic):
+    """dQ, dK, dV from the backward kernels against the oracle running the traced FlashAttention-2 backward
+    (recomputed probabilities from the saved log-sum-exp), bf16 tolerance; dQ by its own kernel
+    (deterministic) or added atomically by the dK/dV kernel."""
     q, k, v = _inputs(b, sq, sk, n, nkv, d, seed=1)
     rng = np.random.default_rng(2)
     g = D.bf16_bits(rng.standard_normal((b, sq, n, d)).astype(np.float32))
     scale = 1.0 / math.sqrt(d)
-    desc = attn_desc(b, sq, sk, n, nkv, d, causal, scale)
+    desc = attn_desc(b, sq, sk, n, nkv, d, causal, scale, deterministic=deterministic)
     dq_, dk_, dv_, dg = Dev(q), Dev(k), Dev(v), Dev(g)
     o, lse = Dev(nbytes=q.nbytes), Dev(nbytes=b * n * sq * 4)
     nv.call("nhip_flash_fwd", C.byref(desc), dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr)
@@ -131,17 +133,22 @@ def test_flash_backward_config3_throughput(hip):
     ws_bytes = C.c_size_t()
     nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
     gq, gk, gv, ws = Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=ws_bytes.value)
-    args = (C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, g.ptr, lse.ptr, gq.ptr, gk.ptr, gv.ptr, ws.ptr)
-    nv.call("nhip_flash_bwd", *args)
-    nv.sync()
-    e0, e1 = nv.Event(), nv.Event()
-    e0.record()
-    for _ in range(5):
-        nv.call("nhip_flash_bwd", *args)
-    e1.record()
-    ms = e0.elapsed_ms(e1) / 5
     flops = 2.5 * 2 * b * n * s * s * d
-    print(f"flash bwd config3: {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s (algorithmic 2.5x fwd)")
+    for det in (1, 0):
+        desc.deterministic = det
+        nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
+        ws = Dev(nbytes=ws_bytes.value)
+        args = (C.byref(desc), dq.ptr, dk.ptr, dv.ptr, o.ptr, g.ptr, lse.ptr, gq.ptr, gk.ptr, gv.ptr, ws.ptr)
+        nv.call("nhip_flash_bwd", *args)
+        nv.sync()
+        e0, e1 = nv.Event(), nv.Event()
+        e0.record()
+        for _ in range(5):
+            nv.call("nhip_flash_bwd", *args)
+        e1.record()
+        ms = e0.elapsed_ms(e1) / 5
+        mode = "deterministic" if det else "atomic dQ"
+        print(f"flash bwd config3 ({mode}): {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s (algorithmic 2.5x fwd)")
     assert np.isfinite(D.bf16_to_f32(gq.get(q.shape, np.uint16))).all()
 
 
