@@ -45,6 +45,12 @@ DEV float lb_bf16(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 // that integer rounding on all 2^32 float32 inputs (checked on MI355X)
 DEV uint16_t sb_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 DEV float r_bf16(float f) { return lb_bf16(sb_bf16(f)); }
+typedef float lk_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 lk_bf16x2 __attribute__((ext_vector_type(2)));
+// two float32 -> bfloat16 (a in the low half) in one v_cvt_pk_bf16_f32
+DEV uint32_t sb2_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((lk_f32x2){a, b}, lk_bf16x2));
+}
 DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
 DEV float r_f16(float f) { return lb_f16(sb_f16(f)); }
@@ -87,20 +93,30 @@ DEV float exp_f32(float x) {
   const float r = __builtin_amdgcn_exp2f(hi);
   return r * fmaf(lo, 0.6931471805599453f, 1.0f);
 }
-// a / b in float32 within 1 ulp (Markstein): the hardware reciprocal refined by one Newton step, the quotient
-// a * r corrected once by its residual a - b q. The reciprocal depends on b alone, so a divisor shared by many
-// quotients (a row's sum or deviation) is refined once. Divisors near the ends of the exponent range, zero,
-// infinities and NaN take the IEEE division (a branch uniform across a row's lanes).
-DEV float fdiv_f32(float a, float b) {
+// a / b in float32 within 1 ulp (Markstein): the hardware reciprocal refined by one Newton step (rcp_f32), the
+// quotient a * r corrected once by its residual a - b q. A zero quotient keeps a's sign (the correction would
+// give +0 for -0 / b); an infinite or NaN dividend, or a quotient past the float range, is a * r's (inf, NaN,
+// or the overflow) instead of the correction's NaN: one class test (NaN, +-inf, +-0) picks q. Divisors near
+// the ends of the exponent range, zero, infinities and NaN take the IEEE division.
+DEV float rcp_f32(float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  return fmaf(fmaf(-b, r, 1.0f), r, r);
+}
+DEV int fdiv_ok(float b) {
   const float ab = fabsf(b);
-  if (!(ab > 0x1p-125f && ab < 0x1p+125f)) return a / b;
-  float r = __builtin_amdgcn_rcpf(b);
-  r = fmaf(fmaf(-b, r, 1.0f), r, r);
+  return ab > 0x1p-125f && ab < 0x1p+125f;
+}
+DEV float fdiv_q(float a, float b, float r) {
   const float q = a * r;
   const float q2 = fmaf(fmaf(-b, q, a), r, q);
-  // a zero quotient keeps a's sign (the correction would give +0 for -0 / b); an infinite or NaN dividend,
-  // or a quotient past the float range, is a * r's (inf, NaN, or the overflow) instead of the correction's NaN
-  return (q2 == 0.0f || !__builtin_isfinite(q2)) ? q : q2;
+  return __builtin_amdgcn_classf(q2, 0x267) ? q : q2;
+}
+DEV float fdiv_f32(float a, float b) { return fdiv_ok(b) ? fdiv_q(a, b, rcp_f32(b)) : a / b; }
+// the same quotient for a divisor shared by a row's lanes (a row's sum or deviation): its reciprocal r and
+// range flag computed once, the flag wave-uniform so the IEEE fallback is a scalar branch
+DEV float fdiv_row(float a, float b, float r, int ok) {
+  if (!ok) return a / b;
+  return fdiv_q(a, b, r);
 }
 DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
@@ -115,9 +131,34 @@ template <typename T> DEV T sat_cast(double x, double lo, double hi) {
   if (x >= hi) return hi < 9.2233720368547758e18 ? T(hi) : (T(0) < T(-1) ? T(~T(0)) : T(~(T(1) << (8 * sizeof(T) - 1))));
   return T(x);
 }
-DEV float wsum(float v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
+// float wave reductions on DPP moves, every lane of the wave active: lanes exchanged within quads (xor 1, xor 2),
+// half rows and rows (mirrors), then rows 0+1 and 2+3 joined by the row broadcasts of lanes 15 and 31, so lane
+// 63 holds the total, read back as a wave-uniform value. Disabled rows of a broadcast read the identity.
+#define LK_DPP(v, ctrl, rows, id) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, (float)(id)), \
+                                                        __builtin_bit_cast(int, v), ctrl, rows, 0xF, false))
+DEV float lane63(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63)); }
+DEV float wsum(float v) {
+  v += LK_DPP(v, 0xB1, 0xF, 0.0f);
+  v += LK_DPP(v, 0x4E, 0xF, 0.0f);
+  v += LK_DPP(v, 0x141, 0xF, 0.0f);
+  v += LK_DPP(v, 0x140, 0xF, 0.0f);
+  v += LK_DPP(v, 0x142, 0xA, 0.0f);
+  v += LK_DPP(v, 0x143, 0xC, 0.0f);
+  return lane63(v);
+}
+// the maximum propagates NaN: fmaxf skips it, so a NaN on any lane (a ballot) gives NaN
+DEV float wmax(float v) {
+  const bool nan = __builtin_amdgcn_ballot_w64(v != v) != 0;
+  v = fmaxf(v, LK_DPP(v, 0xB1, 0xF, -INFINITY));
+  v = fmaxf(v, LK_DPP(v, 0x4E, 0xF, -INFINITY));
+  v = fmaxf(v, LK_DPP(v, 0x141, 0xF, -INFINITY));
+  v = fmaxf(v, LK_DPP(v, 0x140, 0xF, -INFINITY));
+  v = fmaxf(v, LK_DPP(v, 0x142, 0xA, -INFINITY));
+  v = fmaxf(v, LK_DPP(v, 0x143, 0xC, -INFINITY));
+  return nan ? __builtin_nanf("") : lane63(v);
+}
 DEV double wsum(double v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
-DEV float wmax(float v) { for (int o = 32; o > 0; o >>= 1) v = fmax_n(v, __shfl_xor(v, o, 64)); return v; }
 DEV double wmax(double v) { for (int o = 32; o > 0; o >>= 1) v = dmax_n(v, __shfl_xor(v, o, 64)); return v; }
 // integer wavefront sums wrap (unsigned adds, two's complement: any order gives the same bits) and maxima;
 // 64-bit values cross lanes as two 32-bit halves
@@ -224,13 +265,38 @@ class Emitter:
         self.flat_loads: dict = {}    # (arg, fbase) -> element names (vectorized loads)
         self.vec = 1
         self.given: dict = {}         # var -> fn(idx) -> C name: values the caller computes (a GEMM's sums)
+        self.uniform: set = set()     # C names of per-row values (the same on every lane of a row's wave)
+        self.recips: dict = {}        # uniform divisor name -> (reciprocal name, range-flag name)
+        self.rounded: dict = {}       # name of a bf16-rounded float -> the name it was rounded from
 
     def tmp(self, prefix="t"):
         self.count += 1
         return f"{prefix}{self.count}"
 
+    _ROUNDED = re.compile(r"const float (\w+) = r_bf16\((\w+)\);$")
+
     def emit(self, line):
+        m = self._ROUNDED.match(line)
+        if m:
+            self.rounded[m.group(1)] = m.group(2)
         self.lines.append(line)
+
+    def unrounded(self, name):
+        """The float that ``name`` was rounded to bf16 from, when it was (storing that float as bf16 gives the
+        same bits, rounding being idempotent), else ``name``."""
+        return self.rounded.get(name, name)
+
+    def quotient(self, a, b):
+        """``a / b`` in float32 (within 1 ulp): a per-row divisor's reciprocal and range flag are computed once."""
+        if b in self.uniform and a not in self.uniform:
+            if b not in self.recips:
+                r, ok = self.tmp("rcp"), self.tmp("dok")
+                self.emit(f"const float {r} = rcp_f32({b});")
+                self.emit(f"const int {ok} = __builtin_amdgcn_readfirstlane(fdiv_ok({b}));")
+                self.recips[b] = (r, ok)
+            r, ok = self.recips[b]
+            return f"fdiv_row({a}, {b}, {r}, {ok})"
+        return f"fdiv_f32({a}, {b})"
 
     # ---- indices
     def multi(self, idx, shape):
@@ -272,6 +338,8 @@ class Emitter:
             return self.memo[key]
         name = self._compute(var, idx, ty)
         self.memo[key] = name
+        if idx[0] == "r" and self.rows is not None:
+            self.uniform.add(name)
         return name
 
     def _key(self, idx, shape):
@@ -363,7 +431,7 @@ class Emitter:
             else:
                 op = {"add": "+", "sub": "-", "mul": "*", "div": "/"}[p]
                 if D.is_float(dt) and p == "div" and ct == "float" and Emitter.FAST_DIV:
-                    self.emit(f"const {ct} {out} = {self.round(f'fdiv_f32({a}, {b})', dt)};")
+                    self.emit(f"const {ct} {out} = {self.round(self.quotient(a, b), dt)};")
                 elif D.is_float(dt):
                     self.emit(f"const {ct} {out} = {self.round(f'{a} {op} {b}', dt)};")
                 elif p == "div":
@@ -749,7 +817,7 @@ class LoopKernel:
         for k, v in enumerate(st.outputs):
             dt = g.types[v].dtype
             if V > 1 and self.out_views[v].contiguous():
-                stores.append(self._vec_store(f"out{k}", "base", [per_v[l][k] for l in range(V)], dt, V))
+                stores.append(self._vec_store(f"out{k}", "base", [per_v[l][k] for l in range(V)], dt, V, em))
             else:
                 view = self.out_views[v]
                 for lane in range(V):
@@ -802,13 +870,22 @@ class LoopKernel:
                     lines.append(f"const {STORE_T[dt]} {nm} = __builtin_bit_cast({STORE_T[dt]}, ({ct}){tmp}.e[{lane}]);")
         return lines
 
-    def _vec_store(self, ptr, base, names, dt, V):
+    def _vec_store(self, ptr, base, names, dt, V, em=None):
         esz = D.size_of(dt)
+        if em is not None and dt == "bfloat16":
+            names = [em.unrounded(n) for n in names]
         vt = {2: "u16v", 4: "u32v", 8: "u64v"}.get(esz)
         if vt is None or V * esz not in (4, 8, 16):
             return " ".join(f"{ptr}[{base} + {l}] = {_store(n, dt)};" for l, n in enumerate(names))
-        ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
         t = f"S{abs(hash((ptr, base))) % 100000}"
+        if dt == "bfloat16" and V % 2 == 0:
+            # pairs converted together, stored as V / 2 words
+            parts = [f"{{ u32v<{V // 2}> {t};"]
+            for l in range(0, V, 2):
+                parts.append(f"{t}.e[{l // 2}] = sb2_bf16({names[l]}, {names[l + 1]});")
+            parts.append(f"*reinterpret_cast<u32v<{V // 2}>*>({ptr} + {base}) = {t}; }}")
+            return " ".join(parts)
+        ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
         parts = [f"{{ {vt}<{V}> {t};"]
         for l, n in enumerate(names):
             parts.append(f"{t}.e[{l}] = __builtin_bit_cast({ct}, ({STORE_T[dt]}){_store(n, dt)});")
@@ -858,6 +935,11 @@ class LoopKernel:
             isf = D.is_float(acc_dt)
             accn = em.tmp("acc")
             em.emit(f"{act} {accn} = {_red_identity(red.prim, acc_dt)};")
+            # a float32 maximum: fmaxf (which skips NaN) and a NaN flag kept as a lane mask, NaN restored after
+            # the row's lanes are folded; one vector compare an element instead of fmax_n's three operations
+            nanf = em.tmp("anynan") if red.prim == "reduce_max" and acc_dt == "float32" else None
+            if nanf:
+                em.emit(f"bool {nanf} = false;")
             for j in range(J):
                 for lane in range(V):
                     cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
@@ -868,7 +950,12 @@ class LoopKernel:
                     idx = ("rc", "r", cidx, vbase(j), lane)
                     val = em.value(red.inputs[0], idx)
                     guard = "" if exact else f"if ({cexpr} < {C}LL) "
-                    em.emit(f"{guard}{accn} = {_red_update(em, red.prim, acc_dt, accn, val)};")
+                    if nanf:
+                        em.emit(f"{guard}{{ {accn} = fmaxf({accn}, {val}); {nanf} |= ({val} != {val}); }}")
+                    else:
+                        em.emit(f"{guard}{accn} = {_red_update(em, red.prim, acc_dt, accn, val)};")
+            if nanf:
+                em.emit(f"if ({nanf}) {accn} = __builtin_nanf(\"\");")
             total = em.tmp("red")
             op = "wsum" if red.prim == "reduce_sum" else "wmax"
             em.emit(f"{act} {total} = {op}(({act}){accn});")
@@ -900,7 +987,7 @@ class LoopKernel:
                 dt = g.types[v].dtype
                 base = f"(r * {C}LL + ({j} * {T} + tid) * {V})"
                 if V > 1 and self.out_views[v].contiguous():
-                    s = self._vec_store(f"out{oi}", base, [lanes[l][k] for l in range(V)], dt, V)
+                    s = self._vec_store(f"out{oi}", base, [lanes[l][k] for l in range(V)], dt, V, em)
                 else:
                     s = " ".join(
                         f"out{oi}[{self._out_addr(self.out_views[v], g.types[v].shape, f'({base} + {l})')}] = "
@@ -1205,7 +1292,7 @@ class GemmEpilogueKernel:
             names = dnames if (self.store_dot and k == 0) else [per_lane[l][k - (1 if self.store_dot else 0)] for l in range(4)]
             view = self.out_views[v]
             if view.contiguous():
-                stores.append(lk._vec_store(f"out{k}", "base", names, dt, 4))
+                stores.append(lk._vec_store(f"out{k}", "base", names, dt, 4, em))
             else:
                 for lane in range(4):
                     addr = lk._out_addr(view, g.types[v].shape, f"(base + {lane})")
