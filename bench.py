@@ -250,6 +250,21 @@ def _op_line(args, metric, ms, unit_value, unit, config, roof, cpu, dtype, extra
     return out
 
 
+def _probe_copies(replay, kernel):
+    """``--probe``: the dominant kernel's replays, then three device copies of 1 GiB (1 GiB read + 1 GiB written
+    each), whose counter readings calibrate FETCH_SIZE and WRITE_SIZE."""
+    from lumen_amd import native
+    from lumen_amd.tensor import DeviceBuffer
+
+    replay()
+    native.sync()
+    buf = DeviceBuffer(0, 2 << 30)
+    for _ in range(3):
+        native.d2d(buf.ptr, buf.ptr + (1 << 30), 1 << 30)
+    native.sync()
+    print(f"[probe] {kernel} x3, then a 1 GiB copy x3", file=sys.stderr, flush=True)
+
+
 def _time_calls(fn, steps, warmup):
     from lumen_amd import native
     for _ in range(warmup):
@@ -355,6 +370,9 @@ def _config2(args):
     roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s", "frac": round(gbs / 8000.0, 4),
             "traffic": None, "kernel": f"{f.plan.steps[dom].kind} step {dom}: {f.plan.steps[dom].label()}",
             "per_launch": {"flops": 0, "bytes": nbytes, "ms": round(per[dom], 4)}}
+    roof["traffic"] = _traffic(roof["kernel"], args.config)
+    if args.probe:
+        _probe_copies(lambda: [call() for _ in range(3)], roof["kernel"])
     cpu = None
     if not args.no_cpu:
         r = 64
@@ -397,6 +415,7 @@ def _config3(args):
     desc = nv.AttnDesc()
     desc.batch, desc.heads, desc.kv_heads, desc.sq, desc.sk, desc.head_dim = b, n, n, s, s, d
     desc.dtype, desc.causal, desc.scale, desc.config = 1, 1, 1.0 / math.sqrt(d), -1
+    desc.deterministic = 1  # dQ by its own kernel (the plans' default; faster here than atomic adds)
     desc.q_b, desc.q_s, desc.q_n = s * n * d, n * d, d
     for nm in ("k", "v", "o", "do", "dq", "dk", "dv"):
         setattr(desc, f"{nm}_b", s * n * d)

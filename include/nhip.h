@@ -148,9 +148,11 @@ typedef struct {
     int64_t dq_b, dq_s, dq_n;    /* backward only */
     int64_t dk_b, dk_s, dk_n;    /* backward only */
     int64_t dv_b, dv_s, dv_n;    /* backward only */
-    int32_t deterministic;       /* backward only: 1 = dQ by its own kernel (same bits every run); 0 = dQ added
-                                    atomically by the dK/dV kernel into a float32 buffer (the reference's
-                                    default, lumen/graph_compiler/config/mod.rs:117) */
+    int32_t deterministic;       /* backward only, dQ's mode: 0 = added atomically by the dK/dV kernel into a
+                                    float32 buffer (the reference's default, lumen/graph_compiler/config/mod.rs:117);
+                                    1 = dQ = dS K from the 16-bit dS tiles the dK/dV kernel stores in the workspace
+                                    (same bits every run); 2 = by a kernel recomputing S and dP (same bits every
+                                    run, no dS workspace) */
 } nhip_attn_desc;
 
 /* O = softmax(scale Q K^T [causal]) V, P rounded to the inputs' dtype before P V; writes LSE = m + log l
@@ -161,17 +163,20 @@ int nhip_flash_fwd(const nhip_attn_desc *desc, const void *q, const void *k, con
  * lumen/codegen/attention/cuda/mod.rs:312-420). */
 int nhip_attn_config_count(int *count);
 /* FlashAttention-2 backward (kernel.py:107-256): delta = rowsum(dO * O) (float32 [B, N, Sq]), then dK, dV
- * per key block, and dQ either per query block by a second kernel (desc->deterministic) or added atomically by
- * the dK/dV kernel into a float32 [B, N, Sq, D] buffer in the workspace, then rounded into dq. `workspace`
- * needs nhip_flash_bwd_workspace bytes (more when not deterministic). */
+ * per key block, and dQ by desc->deterministic's mode: from the dS tiles the dK/dV kernel stored (1), per query
+ * block by a kernel recomputing S and dP (2), or added atomically by the dK/dV kernel into a float32
+ * [B, N, Sq, D] buffer in the workspace, then rounded into dq (0). `workspace` needs nhip_flash_bwd_workspace
+ * bytes (mode 1: 2 B N Sk Sq bytes of dS tiles, rounded up to 128 keys x 64 queries). */
 int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
                    const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace);
 int nhip_flash_bwd_workspace(const nhip_attn_desc *desc, size_t *bytes);
-/* nhip_flash_bwd without a workspace argument and without allocating: its scratch (delta and LSE, 8 bytes a
- * query row) is a 16 MiB array in the library's device memory, one per GPU, held until the process ends.
- * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, serving
- * loops, harnesses that forbid hipMalloc). Fails for batch * heads * sq > 2^21 rows. Calls that overlap on
- * one GPU (several host threads or streams) share the array and race. */
+/* nhip_flash_bwd without a workspace argument and without allocating: its scratch (what
+ * nhip_flash_bwd_workspace reports for the same desc) is a 16 MiB array in the library's device memory, one
+ * per GPU, held until the process ends. No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). Fails when the workspace
+ * exceeds 16 MiB: mode 2 (8 bytes a query row) takes up to batch * heads * sq = 2^21 rows; modes 1 and 0 much
+ * fewer (dS tiles, the float32 dQ accumulator). Calls that overlap on one GPU (several host threads or
+ * streams) share the array and race. */
 int nhip_flash_bwd_noalloc(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
                            const void *d_o, const float *lse, void *dq, void *dk, void *dv);
 

@@ -502,7 +502,7 @@ def lower(plan, step):
     a.config = getattr(step, "config", -1) if p["name"] == FWD else -1  # the forward's tile (autotuned or forced)
     from lumen_amd.config import config
 
-    a.deterministic = int(bool(config.compiler.deterministic))  # backward: dQ by its own kernel, or atomically
+    a.deterministic = backward_mode()
     if p["name"] == FWD:
         q, k, v = n.inputs
         (qb, qs, qd), (kb, ks, kd), (vb, vs, vd) = p["q_dims"], p["k_dims"], p["v_dims"]
@@ -552,3 +552,26 @@ def _need_unit(*pairs):
 
 
 _ = (Node, TensorType)
+
+
+def backward_mode() -> int:
+    """The flash backward's dQ mode (nhip_attn_desc.deterministic): 0 added atomically by the dK/dV kernel,
+    1 from the dS tiles the dK/dV kernel stores, 2 by a kernel recomputing S and dP."""
+    from lumen_amd.config import config
+
+    if not config.compiler.deterministic:
+        return 0
+    return 1 if config.compiler.attention_store_ds else 2
+
+
+def backward_workspace_bytes(b, nh, sq, sk, hd, mode) -> int:
+    """Workspace bytes of nhip_flash_bwd (its nhip_flash_bwd_workspace): delta and the base-2 LSE (two floats
+    a query row), then 256-byte aligned the float32 dQ accumulator (mode 0) or the 16-bit dS tiles, 128 keys x
+    64 queries each (mode 1)."""
+    rows = 2 * b * nh * sq * 4
+    if mode == 2:
+        return rows
+    base = -(-rows // 256) * 256
+    if mode == 1:
+        return base + b * nh * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2
+    return base + b * nh * sq * hd * 4

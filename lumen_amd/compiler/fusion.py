@@ -267,14 +267,11 @@ def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
             if kind in ("flash_fwd", "flash_bwd"):
                 q = graph.types[node.inputs[0]]
                 if kind == "flash_bwd":
-                    from lumen_amd.config import config
+                    from lumen_amd.compiler.attention import backward_mode, backward_workspace_bytes
 
                     b, sq, nh, hd = q.shape
-                    # delta and base-2 LSE, then (not deterministic) the float32 dQ accumulator, 16-byte
-                    # aligned (nhip_flash_bwd_workspace)
-                    st.scratch = 2 * b * nh * sq * 4
-                    if not config.compiler.deterministic:
-                        st.scratch = -(-st.scratch // 16) * 16 + b * nh * sq * hd * 4
+                    sk = graph.types[node.inputs[1]].shape[1]
+                    st.scratch = backward_workspace_bytes(b, nh, sq, sk, hd, backward_mode())
                 elif len(outs) == 1:
                     st.scratch = graph.types[outs[0]].numel() // graph.types[outs[0]].shape[-1] * 4
         elif kinds[k] in ("view", "reduce"):

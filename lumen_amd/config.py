@@ -18,6 +18,9 @@ class CompilerFlags:
     # attention backward without atomics: dQ by a kernel of its own (same bits every run); off, as in the
     # reference (graph_compiler/config/mod.rs:117), the dK/dV kernel adds dQ atomically
     deterministic: bool = True
+    # deterministic attention backward: the dK/dV kernel stores dS (16-bit, B x N x Sk x Sq / 2 bytes causal) and
+    # dQ = dS K reads it back, instead of a second kernel recomputing S and dP (off: no dS workspace)
+    attention_store_ds: bool = True
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
     # simplify's structural rewrites after pattern matching (swapped/folded dots, ops moved across layouts)
     simplify_structural: bool = True

@@ -68,6 +68,7 @@ struct AttnParams {
     const float *lse_in;
     float *delta;
     float *dqacc;  // float32 [B, N, Sq, D] dQ accumulated atomically by the dK/dV kernel (null: deterministic)
+    uint16_t *ds;  // dS tiles [B, N, Sk / 128, Sq / 64][128 keys][64 queries] the dK/dV kernel stores (or null)
     int64_t sq, sk, heads, kv_heads, batch;
     int64_t q_b, q_s, q_n, k_b, k_s, k_n, v_b, v_s, v_n, o_b, o_s, o_n;
     int64_t do_b, do_s, do_n, dq_b, dq_s, dq_n, dk_b, dk_s, dk_n, dv_b, dv_s, dv_n;
@@ -411,14 +412,18 @@ template <int D> struct DkdvLds {
     static constexpr int kDsPitch = 128 + 8;          // dS row pitch (elements): rows on distinct banks
     static constexpr int kBase = 4 * kTile;           // Q0 dO0 Q1 dO1
     static constexpr int kAtomic = kBase + 128 * D + 64 * kDsPitch;  // + K (128 keys) + dS
+    static constexpr int kStagePitch = 72;                           // STORE_DS staging row pitch (elements)
+    static constexpr int kStore = kBase + 4 * 32 * kStagePitch;      // + each wave's [32 keys][64 queries] dS
 };
 
-template <int D, bool F16, bool CAUSAL, bool ATOMIC_DQ = false>
+// STORE_DS (the deterministic mode's default): each tile's dS (rounded as for dK) is stored to p.ds for the
+// dQ = dS K kernel, instead of a second kernel recomputing S and dP.
+template <int D, bool F16, bool CAUSAL, bool ATOMIC_DQ = false, bool STORE_DS = false>
 __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const float *lse2) {
     constexpr int BM = 64;
     constexpr int DS = D / 16, DT = D / 32;
     constexpr int TILE = BM * D;
-    __shared__ __align__(1024) uint16_t smem[ATOMIC_DQ ? DkdvLds<D>::kAtomic : DkdvLds<D>::kBase];
+    __shared__ __align__(1024) uint16_t smem[ATOMIC_DQ ? DkdvLds<D>::kAtomic : STORE_DS ? DkdvLds<D>::kStore : DkdvLds<D>::kBase];
     __shared__ __align__(16) float Ls[2][BM];
     __shared__ __align__(16) float Dl[2][BM];
     uint16_t *const Ks = smem + DkdvLds<D>::kBase;    // ATOMIC_DQ: K rows [128][D], swizzled like a Q tile
@@ -515,7 +520,10 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
             const float *ls, *dl;
             tile_src(j, qp, gp, ls, dl, q0);
         }
-        __builtin_amdgcn_s_waitcnt(0);
+        // this thread's loads of tile j have landed; with STORE_DS the previous tile's 4 dS stores, issued after
+        // them, may stay in flight (vector memory operations complete in order: vmcnt <= 4)
+        if (STORE_DS && j > 0) __builtin_amdgcn_s_waitcnt(4 | (7 << 4));
+        else __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         flush_dq();  // the previous tile's dQ adds, ahead of this iteration's loads
         if (j + 1 < total) issue(j + 1);
@@ -588,7 +596,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                             const float dr = f4_at(d4[(jj + u) / 4], (jj + u) % 4);
                             float pe = fast_exp2(fmaf(sv[qs][e], c2, -lr));
                             if constexpr (MASKED) pe = ((r >= rmin) & (r < rmax)) ? pe : 0.0f;
-                            if constexpr (ATOMIC_DQ) pe = kvalid ? pe : 0.0f;  // keys past sk add nothing to dQ
+                            if constexpr (ATOMIC_DQ || STORE_DS) pe = kvalid ? pe : 0.0f;  // keys past sk add nothing to dQ
                             pv[u] = pe;
                             dv2[u] = pe * fmaf(dp[qs][e], p.scale, -dr);
                         }
@@ -602,6 +610,41 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         if (masked) probs(std::true_type{});
         else probs(std::false_type{});
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (STORE_DS) {
+            // The tile's dS goes out in the dQ kernel's operand order (flash_dq_ds_kernel): for each 16-key step
+            // ks and 32-query half qb of the tile, 64 lanes x 8 values, lane (q = lane & 31, h = lane >> 5)
+            // holding dS[q][16 ks + 4 h + {0..3}] and dS[q][16 ks + 8 + 4 h + {0..3}] (1 KiB a fragment, 16 a
+            // tile). sb[qs][half] holds the lane's key's queries r0 .. r0 + 3 and r0 + 8 .. r0 + 11 (r0 = 32 qs
+            // + 16 half + 4 h); written into the wave's own LDS rows [32 keys][64 queries], they are read back
+            // transposed (the B-operand read), each wave's two key steps x two query halves, and stored 16 bytes
+            // a lane, 1 KiB contiguous an instruction. Masked rows and keys past sk hold zeros.
+            uint16_t *stg = smem + DkdvLds<D>::kBase + wave * (32 * DkdvLds<D>::kStagePitch);
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    uint16_t *row = stg + l32 * DkdvLds<D>::kStagePitch + 32 * qs + 16 * half + 4 * h;
+                    *reinterpret_cast<uint2 *>(row) = make_uint2(sb[qs][half].x, sb[qs][half].y);
+                    *reinterpret_cast<uint2 *>(row + 8) = make_uint2(sb[qs][half].z, sb[qs][half].w);
+                }
+            const int64_t n_ = nkv * group + j / per_head;
+            uint16_t *blk = p.ds + (((b * p.heads + n_) * nkb + kblk) * ((p.sq + 63) / 64) + q0 / 64) * (128 * 64);
+            const char *sg = reinterpret_cast<const char *>(stg);
+#pragma unroll
+            for (int ksl = 0; ksl < 2; ++ksl)
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    const int krow = 16 * ksl + 4 * h + s16 / 4;
+                    const int col = 32 * qb + 16 * (g & 1) + 4 * (s16 & 3);
+                    v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4i16_t *)(sg + (krow * DkdvLds<D>::kStagePitch + col) * 2));
+                    v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_v4i16_t *)(sg + ((krow + 8) * DkdvLds<D>::kStagePitch + col) * 2));
+                    const uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                    const int f = (2 * wave + ksl) * 2 + qb;
+                    *reinterpret_cast<uint4 *>(blk + f * 512 + lane * 8) = make_uint4(xa.x, xa.y, ya.x, ya.y);
+                }
+        }
 
         // phase 3: dV^T += dO^T P and dK^T += Q^T dS (8 independent chains), transposed fragments read one step
         // ahead
@@ -730,6 +773,123 @@ __global__ __launch_bounds__(256) void flash_dq_round_kernel(AttnParams p) {
             dst[2 * i] = uint16_t(w[i] & 0xffffu);
             dst[2 * i + 1] = uint16_t(w[i] >> 16);
         }
+    }
+}
+
+// dQ = dS K from the dS tiles the dK/dV kernel stored (deterministic, nothing recomputed): 256 queries of one
+// head a workgroup of 4 wavefronts, 64 keys a step; wave w owns the 64 queries of dS tile q0 / 64 + w and the
+// whole head dim: C[d][q] += K^T dS^T (2 x D / 32 MFMA tiles), keys the k dimension. The dS operand comes from
+// HBM straight into registers (the tiles are stored in operand order: 16 bytes a lane, 1 KiB a fragment, each
+// read by one wave once); the K rows stream into LDS for the transposed reads, shared by the 4 waves. Both
+// run two steps ahead (three LDS stages, three register sets; every wave issues every load, so the wait
+// counts are uniform). Steps a wave's queries do not reach (causal) are skipped; so are key blocks whose dS
+// tile the dK/dV kernel never wrote (all its keys after the tile's queries). dS is read once from HBM: 128
+// bf16 products a byte at D = 128, so the kernel is HBM-bound below ~1 PFLOP/s.
+template <int D, bool F16, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void flash_dq_ds_kernel(AttnParams p) {
+    constexpr int KT = 64, QB = 256, KS = KT / 16;
+    constexpr int DSB = 128 * 64;                                     // one dS tile, elements
+    constexpr int FN = D / 32;                                        // 32-column MFMA tiles of the head dim
+    constexpr int KSTAGE = KT * D;                                    // K rows of a step in LDS, elements
+    constexpr int KOPS = (64 / (1024 / (D * 2))) / 4;                 // K-row loads a lane a step
+    __shared__ __align__(1024) uint16_t smem[3 * KSTAGE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+    const int g = lane >> 4, s16 = lane & 15;
+    const int64_t nqb = (p.sq + QB - 1) / QB;
+    const int64_t units = int64_t(gridDim.x) / nqb;  // batch x heads
+    const int64_t unit = blockIdx.x % units;
+    const int64_t qb = nqb - 1 - blockIdx.x / units;  // causal: the last query blocks see the most keys; issued first
+    const int64_t b = unit / p.heads, n = unit % p.heads;
+    const int64_t nkv = n / (p.heads / p.kv_heads);
+    const int64_t q0 = qb * QB;
+    const int64_t nkb = (p.sk + 127) / 128, nqt = (p.sq + 63) / 64;
+    const int64_t shift = p.sk - p.sq;
+    int nk = int((p.sk + KT - 1) / KT);
+    if (CAUSAL) nk = int(min<int64_t>(nk, (q0 + QB - 1 + shift) / KT + 1));
+    const uint16_t *kp = p.k + b * p.k_b + nkv * p.k_n;
+    const int64_t qt = q0 / 64 + wave;  // this wave's dS tile (64 queries)
+    const int64_t qtc = qt < nqt ? qt : nqt - 1;
+    const uint16_t *dsw = p.ds + ((b * p.heads + n) * nkb * nqt + qtc) * DSB + lane * 8;
+    uint4 fs[2][KS][2];
+    // K rows of step kt into LDS stage B (three stages: issued two steps ahead)
+    auto issue_k = [&](auto bufc, int kt) {
+        constexpr int B = decltype(bufc)::value;
+        load_tile_async<D, 4>(kp, p.k_s, int64_t(kt) * KT, p.sk, smem + B * KSTAGE, wave, lane);
+    };
+    // dS fragments of step kt into register set B (two sets: issued one step ahead): 16-key steps 4 (kt & 1) + kk
+    // and query halves qh of the 128-key block kt / 2
+    auto issue_ds = [&](auto bufc, int kt) {
+        constexpr int B = decltype(bufc)::value;
+        const uint16_t *src = dsw + int64_t(kt / 2) * nqt * DSB + (kt & 1) * 4 * 2 * 512;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) fs[B][kk][qh] = *reinterpret_cast<const uint4 *>(src + (2 * kk + qh) * 512);
+    };
+    f32x16_t acc[2][FN];
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[qh][j][e] = 0.0f;
+    // step kt: its K rows were issued two steps ago and its dS one step ago, before the K rows of step kt + 1,
+    // which alone may stay in flight (vmcnt <= the K loads of one step)
+    auto step = [&](auto bdc, auto bkc, int kt) {
+        constexpr int BD = decltype(bdc)::value, BK = decltype(bkc)::value;
+        if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt((KOPS & 15) | ((KOPS >> 4) << 14) | (7 << 4));
+        else __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // every wave's K rows of step kt are in LDS; the stage of step kt - 1 is free
+        if (kt + 1 < nk) issue_ds(std::integral_constant<int, 1 - BD>{}, kt + 1);
+        if (kt + 2 < nk) issue_k(std::integral_constant<int, (BK + 2) % 3>{}, kt + 2);
+        const bool live = qt < nqt && (!CAUSAL || (int64_t(kt) * KT <= qt * 64 + 63 + shift &&
+                                                   qt >= max<int64_t>(0, int64_t(kt / 2) * 128 - shift) / 64));
+        if (!live) return;
+        const char *ks_ = reinterpret_cast<const char *>(smem + BK * KSTAGE);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const int krow = 16 * kk + 4 * h + s16 / 4;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int cold = 32 * j + 16 * (g & 1) + 4 * (s16 & 3);
+                v4i16_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(ks_ + kv_off<D>(krow, cold)));
+                v4i16_t y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(ks_ + kv_off<D>(krow + 8, cold)));
+                const uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
+                const uint4 kf = make_uint4(xa.x, xa.y, ya.x, ya.y);
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) acc[qh][j] = mfma32<F16>(kf, fs[BD][kk][qh], acc[qh][j]);
+            }
+        }
+    };
+    if (nk > 0) {
+        issue_k(std::integral_constant<int, 0>{}, 0);
+        issue_ds(std::integral_constant<int, 0>{}, 0);
+    }
+    if (nk > 1) issue_k(std::integral_constant<int, 1>{}, 1);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int kt = 0; kt < nk; kt += 6) {
+        step(I0{}, I0{}, kt);
+        if (kt + 1 < nk) step(I1{}, I1{}, kt + 1);
+        if (kt + 2 < nk) step(I0{}, I2{}, kt + 2);
+        if (kt + 3 < nk) step(I1{}, I0{}, kt + 3);
+        if (kt + 4 < nk) step(I0{}, I1{}, kt + 4);
+        if (kt + 5 < nk) step(I1{}, I2{}, kt + 5);
+    }
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+        const int64_t q = qt * 64 + 32 * qh + l32;
+        if (q >= p.sq) continue;
+        uint16_t *dqp = p.dq + b * p.dq_b + n * p.dq_n + q * p.dq_s;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int d = 32 * j + 8 * e4 + 4 * h;
+                *reinterpret_cast<uint2 *>(dqp + d) = make_uint2(pack2<F16>(acc[qh][j][4 * e4], acc[qh][j][4 * e4 + 1]),
+                                                                 pack2<F16>(acc[qh][j][4 * e4 + 2], acc[qh][j][4 * e4 + 3]));
+            }
     }
 }
 
@@ -866,11 +1026,18 @@ namespace nhip {
 // delta and the base-2 LSE, float32 [B, N, Sq] each.
 // delta and the base-2 LSE (float32 [B, N, Sq] each), then, when not deterministic, the float32 dQ
 // accumulator [B, N, Sq, D], 16-byte aligned after them.
+// Backward workspace: delta and the base-2 LSE (2 floats a query row), then by mode (nhip_attn_desc.deterministic)
+// 0: the float32 dQ accumulator [B, N, Sq, D]; 1: the dS tiles [B, N, ceil(Sk/128), ceil(Sq/64)][128][64] (16-bit);
+// 2: nothing (dQ recomputes S and dP).
 inline size_t flash_bwd_dq_offset(const nhip_attn_desc *d) {
-    return (2 * size_t(d->batch) * d->heads * d->sq * sizeof(float) + 15) / 16 * 16;
+    return (2 * size_t(d->batch) * d->heads * d->sq * sizeof(float) + 255) / 256 * 256;
+}
+inline size_t flash_bwd_ds_bytes(const nhip_attn_desc *d) {
+    return size_t(d->batch) * d->heads * size_t((d->sk + 127) / 128) * size_t((d->sq + 63) / 64) * 128 * 64 * 2;
 }
 inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
-    if (d->deterministic) return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
+    if (d->deterministic == 2) return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
+    if (d->deterministic == 1) return flash_bwd_dq_offset(d) + flash_bwd_ds_bytes(d);
     return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * d->head_dim * sizeof(float);
 }
 
@@ -902,6 +1069,9 @@ inline int check_attn(const nhip_attn_desc *d, const char *what) {
         return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
+    if (d->deterministic < 0 || d->deterministic > 2)
+        return fail(std::string(what) + ": backward mode (deterministic) " + std::to_string(d->deterministic) +
+                    " (0 atomic dQ, 1 stored dS, 2 recomputed dQ)");
     if (d->config >= kNumAttnConfigs)
         return fail(std::string(what) + ": no attention tile config " + std::to_string(d->config));
     if (d->causal && d->sk < d->sq)
@@ -981,6 +1151,13 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
         hipLaunchKernelGGL((nhipk::flash_dq_round_kernel<D, F16>), gc, dim3(256), 0, s, p);
         return check(hipGetLastError(), "flash dq rounding launch");
     }
+    if (p.ds) {
+        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL, false, true>), gk, dim3(256), 0, s, p, lse2);
+        if (check(hipGetLastError(), "flash dkdv+dS launch")) return 1;
+        dim3 gs(unsigned((d->sq + 255) / 256 * d->heads * d->batch));
+        hipLaunchKernelGGL((nhipk::flash_dq_ds_kernel<D, F16, CAUSAL>), gs, dim3(256), 0, s, p);
+        return check(hipGetLastError(), "flash dq from dS launch");
+    }
     hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL>), gk, dim3(256), 0, s, p, lse2);
     if (check(hipGetLastError(), "flash dkdv launch")) return 1;
     hipLaunchKernelGGL((nhipk::flash_dq_kernel<D, F16, CAUSAL>), gq, dim3(256), 0, s, p, lse2);
@@ -1003,6 +1180,7 @@ int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.dv = static_cast<uint16_t *>(dv);
     p.delta = static_cast<float *>(ws);
     p.dqacc = d->deterministic ? nullptr : reinterpret_cast<float *>(static_cast<char *>(ws) + flash_bwd_dq_offset(d));
+    p.ds = d->deterministic == 1 ? reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + flash_bwd_dq_offset(d)) : nullptr;
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_BWD(DD, FF, CC) return launch_bwd<DD, FF, CC>(s, p, d)
     if (d->head_dim == 128) {

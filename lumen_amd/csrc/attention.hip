@@ -11,9 +11,10 @@ using namespace nhip;
 
 namespace {
 
-// Scratch of nhip_flash_bwd_noalloc: the backward's delta and base-2 LSE (2 floats a query row), for callers
-// that cannot allocate. One copy per GPU, held until the process ends; 16 MiB covers 2^21 query rows
-// (batch x heads x sq), e.g. [4, 4096, 16, 128] uses 2 MiB.
+// Scratch of nhip_flash_bwd_noalloc: the backward's workspace (delta and base-2 LSE, 2 floats a query row, then
+// the mode's dS tiles or dQ accumulator), for callers that cannot allocate. One copy per GPU, held until the
+// process ends; 16 MiB covers 2^21 query rows (batch x heads x sq) in mode 2, e.g. [4, 4096, 16, 128] uses
+// 2 MiB there.
 constexpr size_t kFlashScratchBytes = size_t(16) << 20;
 __device__ __align__(256) unsigned char scratch[kFlashScratchBytes];
 
@@ -71,8 +72,8 @@ int nhip_flash_bwd_noalloc(const nhip_attn_desc *desc, const void *q, const void
     if (need > kFlashScratchBytes)
         return fail("nhip_flash_bwd_noalloc: " + std::to_string(desc->batch * desc->heads * desc->sq) +
                     " query rows need " + std::to_string(need) + " bytes of scratch, above its " +
-                    std::to_string(kFlashScratchBytes) + " (" + std::to_string(kFlashScratchBytes / 8) +
-                    " rows); use nhip_flash_bwd with a workspace");
+                    std::to_string(kFlashScratchBytes) + " (mode 2 takes " + std::to_string(kFlashScratchBytes / 8) +
+                    " rows); use nhip_flash_bwd with a workspace, or deterministic = 2");
     void *ws = nullptr;
     if (scratch_of_current(&ws)) return 1;
     // every scratch word the kernels read is written first in the same call (delta and LSE by the prep

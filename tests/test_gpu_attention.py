@@ -89,12 +89,12 @@ def test_flash_forward_config3_throughput(hip):
     assert np.isfinite(out).all()
 
 
-@pytest.mark.parametrize("deterministic", [1, 0])
+@pytest.mark.parametrize("deterministic", [1, 2, 0])
 @pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", CASES)
 def test_flash_backward_matches_unfused_graph(hip, b, sq, sk, n, nkv, d, causal, deterministic):
     """dQ, dK, dV from the backward kernels against the oracle running the traced FlashAttention-2 backward
-    (recomputed probabilities from the saved log-sum-exp), bf16 tolerance; dQ by its own kernel
-    (deterministic) or added atomically by the dK/dV kernel."""
+    (recomputed probabilities from the saved log-sum-exp), bf16 tolerance; dQ from the stored dS tiles (1), by a
+    kernel recomputing S and dP (2), or added atomically by the dK/dV kernel (0)."""
     q, k, v = _inputs(b, sq, sk, n, nkv, d, seed=1)
     rng = np.random.default_rng(2)
     g = D.bf16_bits(rng.standard_normal((b, sq, n, d)).astype(np.float32))
@@ -134,7 +134,7 @@ def test_flash_backward_config3_throughput(hip):
     nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
     gq, gk, gv, ws = Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=q.nbytes), Dev(nbytes=ws_bytes.value)
     flops = 2.5 * 2 * b * n * s * s * d
-    for det in (1, 0):
+    for det in (1, 2, 0):
         desc.deterministic = det
         nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
         ws = Dev(nbytes=ws_bytes.value)
@@ -147,7 +147,7 @@ def test_flash_backward_config3_throughput(hip):
             nv.call("nhip_flash_bwd", *args)
         e1.record()
         ms = e0.elapsed_ms(e1) / 5
-        mode = "deterministic" if det else "atomic dQ"
+        mode = {1: "dQ from stored dS", 2: "dQ recomputing S and dP", 0: "atomic dQ"}[det]
         print(f"flash bwd config3 ({mode}): {ms * 1e3:.1f} us, {flops / ms / 1e9:.1f} TFLOP/s (algorithmic 2.5x fwd)")
     assert np.isfinite(D.bf16_to_f32(gq.get(q.shape, np.uint16))).all()
 

@@ -88,13 +88,14 @@ def test_flash_attention_cases(hip, case, dtype):
         assert "flash_fwd" not in kinds
 
 
-@pytest.mark.parametrize("deterministic", [True, False])
+@pytest.mark.parametrize("deterministic,store_ds", [(True, True), (True, False), (False, True)])
 @pytest.mark.parametrize("case", BACKWARD_CASES, ids=_ids(BACKWARD_CASES))
-def test_attention_backward_cases(hip, case, deterministic):
+def test_attention_backward_cases(hip, case, deterministic, store_ds):
     """The gradient of a weighted sum of flash attention's output with respect to q, k and v, in bf16,
     against the oracle on the same traced program, with the reference's tolerance: rtol 2e-2 and atol
     2e-2 times the largest magnitude of each gradient (test_attention.py:413-416); deterministic (the same
-    bits every run) or with dQ added atomically (the reference's default)."""
+    bits every run: dQ from the stored dS, or recomputing S and dP) or with dQ added atomically (the
+    reference's default)."""
     (b, sq, sk, n, nkv, h, hv), causal = case
     shapes = (b, sq, n, h), (b, sk, nkv, h), (b, sk, nkv, hv), (b, sq, n, hv)
     ts, _ = _tensors("bfloat16", *shapes)
@@ -103,7 +104,7 @@ def test_attention_backward_cases(hip, case, deterministic):
         return F.sum((F.flash_attention(q, k, v, is_causal=causal) * w).float())
 
     grad = L.grad(loss, (0, 1, 2))
-    with L.config.compiler.patch(deterministic=deterministic):
+    with L.config.compiler.patch(deterministic=deterministic, attention_store_ds=store_ds):
         c = L.compile(grad, device="hip")
         got = [L.to_numpy(t).astype(np.float32) for t in c(*ts)]
         again = [L.to_numpy(t).astype(np.float32) for t in c(*ts)]
