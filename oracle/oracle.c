@@ -11,6 +11,11 @@
  * saturate with NaN -> 0 (mod.rs:226-243).
  *
  * Graphs arrive in a line-oriented text format written by oracle/oracle.py (`serialize`).
+ *
+ * Parity unpinned: the last bit of float64 transcendentals (exp, log, tanh, pow, ... from glibc's libm
+ * here, Rust's platform libm in the reference); the tests pin them only against NumPy's float64 results
+ * rounded once to the output dtype, so a one-ulp libm difference can flip a float rounding (inside every
+ * test's tolerance).
  */
 #include <ctype.h>
 #include <math.h>
