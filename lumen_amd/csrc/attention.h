@@ -531,7 +531,9 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         const char *Gb = Qb + TILE * 2;
         const float *Lt = Ls[j & 1], *Dt = Dl[j & 1];
         // rows q with q > sq - 1 or (causal) kj > q + shift are masked: tile row r is kept when rmin <= r < rmax
-        const bool masked = q0 + BM > p.sq || (CAUSAL && q0 + shift < kb0 + 127);
+        // (with ATOMIC_DQ or STORE_DS also the key block past sk: its keys' P is zeroed)
+        const bool masked = q0 + BM > p.sq || (CAUSAL && q0 + shift < kb0 + 127) ||
+                            ((ATOMIC_DQ || STORE_DS) && kb0 + 128 > p.sk);
         const int rmin = CAUSAL ? int(min<int64_t>(max<int64_t>(kj - shift - q0, 0), BM)) : 0;
         const int rmax = int(min<int64_t>(p.sq - q0, BM));
 
@@ -596,7 +598,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                             const float dr = f4_at(d4[(jj + u) / 4], (jj + u) % 4);
                             float pe = fast_exp2(fmaf(sv[qs][e], c2, -lr));
                             if constexpr (MASKED) pe = ((r >= rmin) & (r < rmax)) ? pe : 0.0f;
-                            if constexpr (ATOMIC_DQ || STORE_DS) pe = kvalid ? pe : 0.0f;  // keys past sk add nothing to dQ
+                            if constexpr (MASKED && (ATOMIC_DQ || STORE_DS)) pe = kvalid ? pe : 0.0f;  // keys past sk add nothing to dQ
                             pv[u] = pe;
                             dv2[u] = pe * fmaf(dp[qs][e], p.scale, -dr);
                         }
