@@ -37,14 +37,33 @@ def hipcc():
     return "hipcc"
 
 
-@functools.lru_cache(maxsize=None)
-def hipcc_version() -> str:
-    """The compiler's own version text (part of every key: a new compiler makes new objects)."""
+VERSION_FILE = os.path.join(CACHE, "HIPCC_VERSION")
+
+
+def query_hipcc_version() -> str:
+    """Runs ``hipcc --version`` (a child process: only before the GPU is initialised) and records the text in
+    the cache directory, where later processes read it instead of running the compiler."""
     try:
         r = subprocess.run([hipcc(), "--version"], capture_output=True, text=True, timeout=120)
-        return "\n".join(r.stdout.splitlines()[:2])
+        text = "\n".join(r.stdout.splitlines()[:2])
     except (OSError, subprocess.SubprocessError):
         return "unknown"
+    os.makedirs(CACHE, exist_ok=True)
+    with open(VERSION_FILE + ".tmp", "w") as f:
+        f.write(text)
+    os.replace(VERSION_FILE + ".tmp", VERSION_FILE)
+    return text
+
+
+@functools.lru_cache(maxsize=None)
+def hipcc_version() -> str:
+    """The compiler's own version text (part of every key: a new compiler makes new objects). Read from the
+    file the build wrote, so that a process that has initialised the GPU starts no child process for it."""
+    try:
+        with open(VERSION_FILE) as f:
+            return f.read()
+    except OSError:
+        return query_hipcc_version()
 
 
 def includes(text: str, csrc: str = CSRC) -> list:
@@ -98,7 +117,7 @@ def prune(csrc: str = CSRC, cache: str = CACHE) -> int:
     keep, removed = live_dirs(csrc), 0
     for name in os.listdir(cache):
         p = os.path.join(cache, name)
-        if os.path.isdir(p) and name in keep:
+        if (os.path.isdir(p) and name in keep) or p == VERSION_FILE:
             continue
         removed += 1
         if os.path.isdir(p):
