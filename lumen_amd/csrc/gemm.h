@@ -430,7 +430,9 @@ __device__ __forceinline__ void stage_acc(const f32x16_t (&acc)[FM][FN], int hal
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
 // functor called as out(row, col, float4, pre) with the float32 sums of four consecutive columns (col a
 // multiple of 4, within m x n) and pre = out.load(row, col), its other operands read ahead. `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256>
+// XPF (three or more stages, buffer loads): the k loop reads the next k tile's first fragments during the last
+// k step of the current one instead of after a barrier at the top of each tile.
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256, bool XPF = false>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
     constexpr int NW = 2 * WN;       // wavefronts (2 x WN)
@@ -548,6 +550,72 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
+    if constexpr (XPF) {
+        // Fragments run ahead across k tiles: the last k step of tile kt waits for tile kt + 1's loads (issued
+        // STAGES - 1 tiles earlier), meets the other waves at the barrier (which also frees tile kt's stage:
+        // every wave's reads of it have completed) and reads tile kt + 1's first fragments under its own MFMAs,
+        // so the MFMA stream has no gap at tile boundaries. Tile kt + STAGES - 1's loads are issued during the
+        // first k step of tile kt, into the stage the previous barrier freed.
+        static_assert(STAGES >= 3, "cross-tile fragment prefetch needs a tile of loads in flight");
+        constexpr int NSTEP = BK / 16;
+        uint4 fa[2][FM], fb[2][FN];
+        auto read = [&](const char *ta, int buf, int kk) {
+            const char *tb = ta + TA::bytes;
+            fa[buf][0] = frag(ta, wm * WR, kk, std::integral_constant<bool, AT>{});
+#pragma unroll
+            for (int j = 0; j < FN; ++j) fb[buf][j] = frag(tb, wn * WCOLS + 32 * j, kk, std::integral_constant<bool, BT>{});
+#pragma unroll
+            for (int i = 1; i < FM; ++i) fa[buf][i] = frag(ta, wm * WR + 32 * i, kk, std::integral_constant<bool, AT>{});
+        };
+        // waits until at most `later` tiles' loads of this thread are in flight (vector memory completes in order)
+        auto wait_tiles = [&](int later) {
+            if (later <= 0) __builtin_amdgcn_s_waitcnt(0x0070);
+            else if (later == 1) __builtin_amdgcn_s_waitcnt((LPS & 15) | ((LPS >> 4) << 14) | 0x0070);
+            else if (later == 2) __builtin_amdgcn_s_waitcnt(((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | 0x0070);
+            else __builtin_amdgcn_s_waitcnt(((3 * LPS) & 15) | (((3 * LPS) >> 4) << 14) | 0x0070);
+        };
+#pragma unroll
+        for (int st = 0; st < STAGES - 1; ++st)
+            if (st < ktiles) issue(st, st, 0, LPS);
+        wait_tiles(min(STAGES - 2, ktiles - 1));
+        __syncthreads();
+        read(smem, 0, 0);
+        for (int kt = 0; kt < ktiles; ++kt) {
+            const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+            const char *tn = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
+            const bool more = kt + STAGES - 1 < ktiles;
+            const bool next = kt + 1 < ktiles;
+            auto step = [&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                constexpr int cur = i & 1;
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (i + 1 < NSTEP) {
+                    read(ta, cur ^ 1, 16 * (i + 1));
+                } else {
+                    if (next) {
+                        wait_tiles(min(STAGES - 2, ktiles - 2 - kt));  // tile kt + 1 landed (this thread)
+                        asm volatile("s_barrier" ::: "memory");           // ... every thread's; stage kt is free
+                        read(tn, cur ^ 1, 0);
+                    }
+                }
+                if constexpr (i == 0) {
+                    if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+                }
+#pragma unroll
+                for (int ii = 0; ii < FM; ++ii)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[ii][j] = Mfma<F16>::run(fb[cur][j], fa[cur][ii], acc[ii][j]);
+                mfma_ds_interleave<0, FM * FN, NRD, i + 1>();
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+            if constexpr (NSTEP > 2) {
+                step(std::integral_constant<int, 2>{});
+                step(std::integral_constant<int, 3>{});
+            }
+        }
+    } else {
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
         if (st < ktiles) issue(st, st, 0, LPS);
@@ -591,6 +659,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             step(std::integral_constant<int, 32>{});
             step(std::integral_constant<int, 48>{});
         }
+    }
     }
 
     // acc[i][j][e]: row m0 + wm*WR + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
@@ -900,11 +969,11 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     gemm_stream_persist_run<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, bool XPF = false>
 __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
     extern __shared__ __align__(1024) char smem[];
-    gemm_stream_tile<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
+    gemm_stream_tile<F16, BK, WN, AT, BT, BUF, AnyStore, 256, XPF>(s, a, b, out, smem);
 }
 
 // The 128 x 128 tile: 4 wavefronts of 64 x 64, two 32 KiB stages, two workgroups a CU (dots with too few
