@@ -1227,8 +1227,14 @@ class GemmEpilogueKernel:
     (mn-contiguous operands), as nhip_gemm takes them."""
 
 
-    def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None):
+    # The k loops a generated epilogue kernel can instantiate: (k tile, cross-tile fragment prefetch). Variant 0
+    # is gemm_stream's config 7 body; variant 1 its config 11 body (k tile 32, four stages, buffer loads only).
+    VARIANTS = ((64, False), (32, True))
+
+    def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None,
+                 variant=0):
         self.graph, self.dot, self.loop = graph, dot_step, loop_step
+        self.variant = variant
         self.desc, self.at, self.bt, self.f16, self.store_dot = desc, at, bt, f16, store_dot
         # (value, sum): a float32 loop output summed over the rows into `sum` [n] (atomically, into zeros)
         # instead of being stored
@@ -1240,6 +1246,11 @@ class GemmEpilogueKernel:
         self.block = (512, 1, 1)
         self.lds = 0
         self.args = []
+
+    def variant_ok(self, variant):
+        """Whether k loop ``variant`` can run this dot (its k tile divides k; XPF needs the buffer-load path)."""
+        bk, xpf = self.VARIANTS[variant]
+        return self.desc.k % bk == 0 and (not xpf or self.buffer_ok())
 
     def buffer_ok(self):
         """gemm.h's stream_buffer_ok: the operand bytes a 256 x 256 tile spans fit 32-bit buffer offsets."""
@@ -1327,6 +1338,9 @@ class GemmEpilogueKernel:
                 pre_uses.append(f"const {m.group(1)} {m.group(2)} = pre.{m.group(2)};")
             else:
                 rest.append(l)
+        bk, xpf = self.VARIANTS[self.variant]
+        if not self.variant_ok(self.variant):
+            raise Unfusable(dv, f"GEMM epilogue k loop variant {self.variant} does not fit k = {d.k}")
         # chunks read ahead at a time: at most 64 VGPRs of 16-byte loads
         ahead = 16
         while ahead > 1 and ahead * len(pre_fields) > 16:
@@ -1351,11 +1365,12 @@ class GemmEpilogueKernel:
             "};",
             f'extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) '
             f'void KNAME({", ".join(params)}) {{',
-            "  __shared__ __align__(1024) char smem[nhipk::gemm_stream_lds_bytes<64, 4>()];",
+            f"  __shared__ __align__(1024) char smem[nhipk::gemm_stream_lds_bytes<{bk}, 4>()];",
             "  nhipk::GemmShape s;",
             f"  {shape}",
-            f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, 64, 4, {'true' if self.at else 'false'}, "
-            f"{'true' if self.bt else 'false'}, {'true' if self.buffer_ok() else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
+            f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, {bk}, 4, {'true' if self.at else 'false'}, "
+            f"{'true' if self.bt else 'false'}, {'true' if self.buffer_ok() else 'false'}, EpiKNAME, 256, "
+            f"{'true' if xpf else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
             "}",
         ]
         return "\n".join(lines)

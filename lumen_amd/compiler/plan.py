@@ -191,6 +191,7 @@ class Plan:
                 self._lay_out()
         self.kernels = {}
         self.sources = {}
+        self.epi_alts = {}  # epilogue GEMM step -> [(k loop variant, kernel, source)] for the autotuner
         self._native = None
         if compiled is None or build_kernels:
             self._gen_kernels()
@@ -596,6 +597,17 @@ class Plan:
                 k.name = st.name = name
                 self.kernels[si] = k
                 self.sources[si] = codegen.HEADER + body.replace("KNAME", name)
+                # the other k loops, for the autotuner to time against this one (large dots whose operands and
+                # outputs do not overlap, so a timed run changes nothing the plan reads)
+                if config.compiler.autotune and d.m * d.n * d.k >= self.AUTOTUNE_MACS and not self._epi_overlaps(st):
+                    for var in range(1, len(codegen.GemmEpilogueKernel.VARIANTS)):
+                        if not k.variant_ok(var):
+                            continue
+                        kv = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
+                                                        colsum=getattr(st, "epi_colsum", None), variant=var)
+                        bv = kv.source()
+                        kv.name = f"gemm_epi_{hashlib.sha1(bv.encode()).hexdigest()[:10]}"
+                        self.epi_alts.setdefault(si, []).append((var, kv, codegen.HEADER + bv.replace("KNAME", kv.name)))
                 continue
             if st.kind not in ("loop", "row", "reduce", "scatter_add"):
                 continue
@@ -627,10 +639,31 @@ class Plan:
         return ("copy", self.loc[n.inputs[0]])
 
     def build(self):
-        """Compiles every generated kernel (hipcc, cached)."""
+        """Compiles every generated kernel (hipcc, cached), the epilogue GEMMs' alternative k loops too."""
         keys = list(self.sources)
-        paths = kcache.compile_many([self.sources[k] for k in keys])
-        self.objects = dict(zip(keys, paths))
+        alts = [(si, i) for si, lst in self.epi_alts.items() for i in range(len(lst))]
+        paths = kcache.compile_many([self.sources[k] for k in keys] + [self.epi_alts[si][i][2] for si, i in alts])
+        self.objects = dict(zip(keys, paths[: len(keys)]))
+        self.alt_objects = {key: p for key, p in zip(alts, paths[len(keys):])}
+
+    def _epi_overlaps(self, st):
+        """Whether an epilogue GEMM step writes memory it also reads (then it is never run for timing alone)."""
+        ins = [self.loc[v] for v in st.nodes[0].inputs if v in self.loc] + \
+              [self.loc[v] for v in st.epi.inputs if v != st.nodes[0].output and v in self.loc]
+        outs = [self.loc[v] for v in st.outputs if v in self.loc]
+
+        def span(loc):
+            lo = loc.offset * D.size_of(loc.dtype)
+            hi = lo + max(1, sum((n - 1) * abs(stv) for n, stv in zip(loc.shape, loc.strides)) + 1) * D.size_of(loc.dtype)
+            return loc.base, lo, hi
+
+        for o in outs:
+            bo, lo_o, hi_o = span(o)
+            for i in ins:
+                bi, lo_i, hi_i = span(i)
+                if bi == bo and lo_i < hi_o and lo_o < hi_i:
+                    return True
+        return False
 
     # ---- native
     def _native_plan(self):
@@ -833,7 +866,55 @@ class Plan:
 
     def _autotune(self, workspace_ptr, input_ptrs):
         self._autotune_gemms(workspace_ptr, input_ptrs)
+        self._autotune_epilogues(workspace_ptr, input_ptrs)
         self._autotune_attention(workspace_ptr, input_ptrs)
+
+    def _autotune_epilogues(self, workspace_ptr, input_ptrs):
+        """Each epilogue GEMM with alternative k loops runs every one of them (a warm-up, then three timed runs
+        with HIP events, on the step's own buffers); the fastest (by more than the margin) replaces the kernel
+        the plan launches. Kept per generated source for the process."""
+        from lumen_amd import native as nv
+
+        if not self.epi_alts:
+            return
+        if not hasattr(self, "objects"):
+            self.build()
+        ev0, ev1 = nv.Event(), nv.Event()
+        for si, alts in self.epi_alts.items():
+            st = self.steps[si]
+            key = ("epi", self.sources[si])
+            if key not in Plan._tuned:
+                k0 = self.kernels[si]
+                ptrs = []
+                for _, v in k0.args:
+                    loc = self.loc[v]
+                    base = workspace_ptr if loc.base[0] == "ws" else input_ptrs[loc.base[1]]
+                    ptrs.append(base + loc.offset * D.size_of(loc.dtype))
+                args = (C.c_uint64 * max(1, len(ptrs)))(*ptrs)
+                cands = [(0, k0, self.objects[si])] + [(var, kv, self.alt_objects[(si, i)])
+                                                       for i, (var, kv, _) in enumerate(alts)]
+                best, best_ms = 0, float("inf")
+                for var, kv, obj in cands:
+                    fn = nv.module_function(obj, kv.name)
+                    grid = (C.c_uint32 * 3)(*kv.grid)
+                    block = (C.c_uint32 * 3)(*kv.block)
+                    nv.call("nhip_launch", fn, grid, block, kv.lds, args, C.sizeof(args))
+                    ev0.record()
+                    for _ in range(3):
+                        nv.call("nhip_launch", fn, grid, block, kv.lds, args, C.sizeof(args))
+                    ev1.record()
+                    ms = ev0.elapsed_ms(ev1) / 3
+                    if ms < best_ms * (1.0 - self.AUTOTUNE_MARGIN):
+                        best, best_ms = var, ms
+                Plan._tuned[key] = best
+            var = Plan._tuned[key]
+            if var:
+                i = [a[0] for a in alts].index(var)
+                _, kv, _ = alts[i]
+                self.kernels[si] = kv
+                self.objects[si] = self.alt_objects[(si, i)]
+                st.name = kv.name
+            st.epi_variant = var
 
     ATTN_AUTOTUNE_FLOPS = 1 << 32  # flash forwards of fewer FLOPs keep the default tile
 

@@ -186,6 +186,49 @@ def test_gemm_epilogue_matches_oracle_and_unfused_plan(hip, fn, m, n, k, monkeyp
         assert np.array_equal(g_, r_)
 
 
+def _epi_colsum_fn(x, w, h, b):
+    z = F.matmul(x, w, "float32", "float32") * h
+    return F.sum(z, dim=(0,)), (z + b).bfloat16()
+
+
+@pytest.mark.parametrize("fn", [_epi_fn_keep, _epi_colsum_fn])
+def test_gemm_epilogue_k_loops_agree_and_autotune_keeps_values(hip, fn, monkeypatch):
+    """The generated epilogue GEMM's two k loops (k tile 64; k tile 32 with fragments read ahead across k
+    tiles) give the same bits, ragged m and n included; and a plan whose autotuner times both on its own
+    buffers before the first run (column sums added atomically into zeros among them) still gives those
+    bits."""
+    from lumen_amd.compiler import codegen
+    from lumen_amd.compiler.plan import Plan
+
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
+    m, n, k = 1000, 776, 320
+    rng = np.random.default_rng(23)
+    x = _bf16(rng.standard_normal((m, k)) * 0.25)
+    w = _bf16(rng.standard_normal((k, n)) * 0.25)
+    h = rng.standard_normal((m, n)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    args = [L.tensor(D.bf16_to_f32(x), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(h),
+            L.from_numpy(b)]
+
+    def run(**patch):
+        with L.config.compiler.patch(horizontal_fusion=False, **patch):
+            f = L.compile(fn, device="hip")
+            out = [np.asarray(L.to_numpy(t), np.float32) for t in f(*args)]
+            assert any(s["name"].startswith("gemm_epi_") for s in f.plan.describe())
+            return out, f.plan
+
+    first, _ = run(autotune=False)
+    monkeypatch.setattr(codegen.GemmEpilogueKernel, "VARIANTS", tuple(reversed(codegen.GemmEpilogueKernel.VARIANTS)))
+    second, _ = run(autotune=False)
+    monkeypatch.undo()
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
+    monkeypatch.setattr(Plan, "AUTOTUNE_MACS", 1)
+    tuned, plan = run(autotune=True)
+    assert plan.epi_alts and all(hasattr(plan.steps[si], "epi_variant") for si in plan.epi_alts)
+    for a, b_, c in zip(first, second, tuned):
+        assert np.array_equal(a, b_) and np.array_equal(a, c)
+
+
 @pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,))])
 def test_leading_axis_sums_match_oracle(hip, shape, axes):
     """float32 sums over leading axes (the vectorized reduce kernel: four columns a thread, 64-row chunks
