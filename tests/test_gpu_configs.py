@@ -195,8 +195,8 @@ def _epi_colsum_fn(x, w, h, b):
 def test_gemm_epilogue_k_loops_agree_and_autotune_keeps_values(hip, fn, monkeypatch):
     """The generated epilogue GEMM's two k loops (k tile 64; k tile 32 with fragments read ahead across k
     tiles) give the same bits, ragged m and n included; and a plan whose autotuner times both on its own
-    buffers before the first run (column sums added atomically into zeros among them) still gives those
-    bits."""
+    buffers before the first run still gives those bits. Column sums, added atomically into zeros in no fixed
+    order, agree within float32 reassociation (1e-5 of the sum of magnitudes)."""
     from lumen_amd.compiler import codegen
     from lumen_amd.compiler.plan import Plan
 
@@ -225,8 +225,14 @@ def test_gemm_epilogue_k_loops_agree_and_autotune_keeps_values(hip, fn, monkeypa
     monkeypatch.setattr(Plan, "AUTOTUNE_MACS", 1)
     tuned, plan = run(autotune=True)
     assert plan.epi_alts and all(hasattr(plan.steps[si], "epi_variant") for si in plan.epi_alts)
-    for a, b_, c in zip(first, second, tuned):
-        assert np.array_equal(a, b_) and np.array_equal(a, c)
+    summed = fn is _epi_colsum_fn  # its first output: column sums added atomically, in no fixed order
+    for i, (a, b_, c) in enumerate(zip(first, second, tuned)):
+        if summed and i == 0:
+            y = D.bf16_to_f32(x).astype(np.float64) @ D.bf16_to_f32(w).astype(np.float64)
+            scale = np.abs(y * h).sum(axis=0)
+            assert np.all(np.abs(a - b_) <= 1e-5 * scale) and np.all(np.abs(a - c) <= 1e-5 * scale)
+        else:
+            assert np.array_equal(a, b_) and np.array_equal(a, c)
 
 
 @pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,))])
