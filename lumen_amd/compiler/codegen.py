@@ -899,7 +899,11 @@ class LoopKernel:
         reds = [n for n in st.nodes if n.prim in ("reduce_sum", "reduce_max")]
         outs_elem = [v for v in st.outputs if g.types[v].numel() == R * C and R * C != R]
         outs_row = [v for v in st.outputs if v not in outs_elem]
-        dts = [g.types[v].dtype for v in st.outputs] + [g.types[v].dtype for v in st.inputs]
+        # the vector width follows the operands read or written along the columns; per-row values (a row's
+        # target class, its statistics) are loaded once a row and do not narrow it
+        per_row = {R, 1} if C > 1 else set()
+        dts = [g.types[v].dtype for v in outs_elem] + \
+              [g.types[v].dtype for v in st.inputs if g.types[v].numel() not in per_row]
         esz = max([D.size_of(d) for d in dts] + [2])
         V = 1
         for cand in (8, 4, 2):
