@@ -347,6 +347,10 @@ struct StreamTile {
     static constexpr int segs = bytes / 1024;
 };
 
+// The persistent kernel's LDS: two operand stages plus one wave's 32 staging rows (the other waves stage in the
+// stage the tile's last k step has read).
+constexpr int gemm_stream_persist_lds_bytes() { return 2 * 2 * 256 * 64 * 2 + 32 * (64 * 4 + 16); }
+
 // Stages: 128 KiB of operand tiles for the 256 x 256 tile (one workgroup a CU); two stages (64 KiB, two
 // workgroups a CU) for the 128 x 128 tile.
 template <int BK, int TM = 256>
@@ -362,10 +366,10 @@ constexpr int gemm_stream_lds_bytes() {
     return ops > epi ? ops : epi;
 }
 
-// Writes rows [rbase, rbase + 64) x columns [cbase, cbase + WCOLS) of D from a wave's float32 staging rows
+// Writes rows [rbase, rbase + ROWS) x columns [cbase, cbase + WCOLS) of D from a wave's float32 staging rows
 // (`PITCH` bytes apart): 16-byte stores when D is row-contiguous and aligned, else element by element through
 // the strided store.
-template <int WCOLS, int PITCH>
+template <int WCOLS, int PITCH, int ROWS = 64>
 __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyStore &out, int64_t od, const char *stage,
                                                   int64_t rbase, int64_t cbase, int lane) {
     const int esize = out.dtype == 0 ? 4 : 2;
@@ -375,7 +379,7 @@ __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyS
     if (vec) {
         const int epc = 16 / esize;            // output elements a 16-byte chunk
         const int cpr = WCOLS / epc;           // chunks a row
-        for (int idx = lane; idx < 64 * cpr; idx += 64) {
+        for (int idx = lane; idx < ROWS * cpr; idx += 64) {
             const int r = idx / cpr, ch = idx % cpr;
             const int64_t gr = rbase + r, gc = cbase + ch * epc;
             if (gr >= s.m || gc >= s.n) continue;
@@ -401,7 +405,7 @@ __device__ __forceinline__ void stream_store_rows(const GemmShape &s, const AnyS
         }
     } else {
         out.visit([&](auto stf) {
-            for (int idx = lane; idx < 64 * WCOLS; idx += 64) {
+            for (int idx = lane; idx < ROWS * WCOLS; idx += 64) {
                 const int r = idx / WCOLS, c = idx % WCOLS;
                 const int64_t gr = rbase + r, gc = cbase + c;
                 if (gr < s.m && gc < s.n) stf(s, od, gr, gc, *reinterpret_cast<const float *>(stage + r * PITCH + c * 4));
@@ -738,53 +742,11 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     }
 }
 
-// Writes a wave's sums straight from the MFMA accumulators: acc[i][j][4 e4 .. 4 e4 + 3] are four consecutive
-// columns of one row, a 16-byte (float32) or 8-byte (16-bit) store when D is row-major with rows a multiple
-// of 4 elements; the L2 merges the 32-byte pieces of a row the wave writes into whole lines. LDS is not used,
-// so the next tile's operands can stream into it meanwhile.
-template <int FM, int FN>
-__device__ __forceinline__ void stream_store_direct(const GemmShape &s, const AnyStore &out, int64_t od,
-                                                    const f32x16_t (&acc)[FM][FN], int64_t rbase, int64_t cbase,
-                                                    int l32, int h) {
-    const int esize = out.dtype == 0 ? 4 : 2;
-    const bool vec = s.d_n == 1 && s.d_m % 4 == 0 && ((reinterpret_cast<uintptr_t>(out.d) + od * esize) & 15) == 0;
-    char *dbase = static_cast<char *>(out.d) + od * esize;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int64_t gr = rbase + 32 * i + l32;
-        if (gr >= s.m) continue;
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4) {
-                const int64_t gc = cbase + 32 * j + 8 * e4 + 4 * h;
-                const float x0 = acc[i][j][4 * e4], x1 = acc[i][j][4 * e4 + 1], x2 = acc[i][j][4 * e4 + 2],
-                            x3 = acc[i][j][4 * e4 + 3];
-                if (vec && gc + 4 <= s.n) {
-                    char *p = dbase + (gr * s.d_m + gc) * esize;
-                    if (out.dtype == 0)
-                        *reinterpret_cast<float4 *>(p) = make_float4(x0, x1, x2, x3);
-                    else if (out.dtype == 1)
-                        *reinterpret_cast<uint2 *>(p) = make_uint2(uint32_t(f32_to_bf16(x0)) | (uint32_t(f32_to_bf16(x1)) << 16),
-                                                                   uint32_t(f32_to_bf16(x2)) | (uint32_t(f32_to_bf16(x3)) << 16));
-                    else
-                        *reinterpret_cast<uint2 *>(p) = make_uint2(uint32_t(f32_to_f16(x0)) | (uint32_t(f32_to_f16(x1)) << 16),
-                                                                   uint32_t(f32_to_f16(x2)) | (uint32_t(f32_to_f16(x3)) << 16));
-                } else if (gc < s.n) {
-                    const float xs[4] = {x0, x1, x2, x3};
-                    out.visit([&](auto stf) {
-                        for (int e = 0; e < 4 && gc + e < s.n; ++e) stf(s, od, gr, gc + e, xs[e]);
-                    });
-                }
-            }
-    }
-}
-
 // The persistent 256 x 256 streamed GEMM: a workgroup a CU walks tiles blockIdx.x, + gridDim.x, ... and
 // overlaps each tile's end with the next one's start. During a tile's last k step the stage the step does
-// not read fills with the next tile's first k tile, and the sums are stored from registers, so the next
-// tile's first loads are in flight across the last MFMAs and the stores, and no workgroup launches between
-// tiles. Same operand staging, k loop and results as gemm_stream_tile (one batch, one split: z and split-k
+// not read fills with the next tile's first k tile, and the sums go out through the stage the step did read
+// (row-contiguous stores), so the next tile's first loads are in flight across the last MFMAs and the stores,
+// and no workgroup launches between tiles. Same operand staging, k loop and results as gemm_stream_tile (one batch, one split: z and split-k
 // go through gemm_stream).
 template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF>
 __device__ __forceinline__ void gemm_stream_persist_run(const GemmShape &s, const uint16_t *__restrict__ a,
@@ -955,7 +917,32 @@ __device__ __forceinline__ void gemm_stream_persist_run(const GemmShape &s, cons
             }
             stage ^= 1;
         }
-        stream_store_direct<FM, FN>(s, out, od, acc, cur.m0 + wm * WR, cur.n0 + wn * WCOLS, l32, h);
+        // the sums go out through LDS, 32 rows of the wave at a time, as row-contiguous 16-byte stores (stores
+        // straight from the accumulators, 32 rows x 32 bytes an instruction, take several times longer): the
+        // stage the last k step read is free once every wave is past its reads (the other stage holds the next
+        // tile's first k tile); seven waves stage there, the eighth in the LDS past the two stages
+        __syncthreads();
+        {
+            constexpr int PITCH = WCOLS * 4 + 16;
+            char *rows = wave < 7 ? smem + (stage ^ 1) * STAGE_BYTES + wave * (32 * PITCH) : smem + 2 * STAGE_BYTES;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4)
+                        *reinterpret_cast<float4 *>(rows + l32 * PITCH + (32 * j + 8 * e4 + 4 * h) * 4) =
+                            make_float4(acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]);
+                // the wave's own rows: its writes land before its lanes read them back
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                stream_store_rows<WCOLS, PITCH, 32>(s, out, od, rows, cur.m0 + wm * WR + 32 * i, cur.n0 + wn * WCOLS, lane);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        }
         if (!has_next) break;
         t = tnext;
         cur = nxt;

@@ -188,7 +188,7 @@ int device_cus() {
 template <bool F16, bool AT, bool BT, bool BUF>
 int launch_stream_persist_kernel(hipStream_t st, const GemmShape &s, const void *a, const void *b, void *out,
                                  int dtype) {
-    constexpr int lds = gemm_stream_stages<64, 256>() * 2 * 256 * 64 * 2;
+    constexpr int lds = gemm_stream_persist_lds_bytes();
     auto kern = gemm_stream_persist<F16, 64, 4, AT, BT, BUF>;
     static bool attr = false;
     if (!attr) {

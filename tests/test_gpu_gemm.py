@@ -91,7 +91,7 @@ def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
 def test_gemm_persistent_walks_every_tile(hip, m, n, k, at, bt, out):
     """The persistent 256 x 256 kernel (config 10) with more tiles than CUs, so each workgroup runs several
     and prefetches the next one's first k tile during its last: ragged m and n, a single k tile (k = 64),
-    every layout, stores from registers as 16-byte / 8-byte vectors and, for a row length that is not a
+    every layout, row stores staged through LDS as 16-byte vectors and, for a row length that is not a
     multiple of 4 (n = 4401), element by element."""
     rng = np.random.default_rng(m + n + k)
     a = D.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
