@@ -9,6 +9,7 @@ function assigned back into their memory.
 
 from __future__ import annotations
 
+import collections
 import functools
 
 import numpy as np
@@ -32,7 +33,7 @@ class Compiled:
         self._device = None if device is None else device_name(device)
         self._plans = {}
         self._latest = None
-        self._graphs = {}  # id(plan) -> "warm" after its first call, then (graph, staging buffers, fixed, ptrs)
+        self._graphs = {}  # id(plan) -> captured graphs by the addresses they read in place (empty: warm)
 
     def _target(self, args):
         if self._device is not None:
@@ -74,40 +75,49 @@ class Compiled:
     def plan(self):
         return self._plans[self._latest][1]
 
+    # Arguments of at least this many bytes are read by a captured graph where they lie (one graph per set of
+    # such addresses, the newest GRAPHS_PER_PLAN kept) instead of being copied into its staging buffers, whose
+    # copy would cost as much as a memory-bound plan itself.
+    DIRECT_BYTES = 1 << 20
+    GRAPHS_PER_PLAN = 8
+
     def _run(self, plan, workspace, traced, ptrs, keep):
         """``plan.run_in``; with ``config.compiler.hip_graphs`` (the reference's CUDA graphs,
         ``lumen/graph/tracer.py:958-1049``) a plan runs as usual on its first call (which builds and autotunes
         its kernels), is captured on its second into a HIP graph over device buffers of its own for the
-        call's arguments and runtime scalars, and from then on each call copies those in (stream-ordered)
-        and launches the graph. Weights and the workspace are read where they were captured; when one moves,
-        the plan is captured again. Profiled runs (``plan.profile``) are never captured. Returns the input
-        pointers the run read."""
+        call's runtime scalars and small arguments, and from then on each call copies those in (stream-ordered)
+        and launches the graph. Weights, the workspace and large arguments are read where they were captured;
+        a call whose large arguments or weights lie elsewhere is captured again (the newest few graphs of a
+        plan are kept, so alternating inputs replay too). Profiled runs (``plan.profile``) are never captured.
+        Returns the input pointers the run read."""
         if not config.compiler.hip_graphs or getattr(plan, "_profiling", False):
             plan.run_in(workspace.ptr, ptrs)
             return ptrs
-        state = self._graphs.get(id(plan))
-        staged = [i for i, (kind, _) in enumerate(traced.layout) if kind in ("arg", "scalar")]
-        fixed = [workspace.ptr] + [p for i, p in enumerate(ptrs) if i not in staged]
-        if state is None:
-            self._graphs[id(plan)] = "warm"
+        graphs = self._graphs.get(id(plan))
+        staged = [i for i, (kind, _) in enumerate(traced.layout)
+                  if kind == "scalar" or (kind == "arg" and keep[i].nbytes < self.DIRECT_BYTES)]
+        fixed = (workspace.ptr,) + tuple(p for i, p in enumerate(ptrs) if i not in staged)
+        if graphs is None:
+            self._graphs[id(plan)] = collections.OrderedDict()  # warm: the first call runs plainly
             plan.run_in(workspace.ptr, ptrs)
             return ptrs
-        if state == "warm" or state[2] != fixed:
+        entry = graphs.get(fixed)
+        if entry is None:
             dev = int(plan.device.split(":")[1])
             buffers = {i: DeviceBuffer(dev, max(1, keep[i].nbytes)) for i in staged}
             gptrs = [buffers[i].ptr if i in buffers else p for i, p in enumerate(ptrs)]
-            graph = None
-            self._graphs[id(plan)] = None
             for i, b in buffers.items():
                 native.d2d(b.ptr, ptrs[i], keep[i].nbytes)
-            graph = plan.capture(workspace.ptr, gptrs)
-            state = (graph, buffers, fixed, gptrs)
-            self._graphs[id(plan)] = state
+            entry = (plan.capture(workspace.ptr, gptrs), buffers, gptrs)
+            graphs[fixed] = entry
+            while len(graphs) > self.GRAPHS_PER_PLAN:
+                graphs.popitem(last=False)
         else:
-            graph, buffers, _, gptrs = state
+            graphs.move_to_end(fixed)
+            _, buffers, gptrs = entry
             for i, b in buffers.items():
                 native.d2d(b.ptr, ptrs[i], keep[i].nbytes)
-        graph.launch()
+        entry[0].launch()
         return gptrs
 
     def last_buffers(self):
