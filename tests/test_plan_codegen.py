@@ -107,6 +107,27 @@ def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep, monkeypatc
     assert [s.kind for s in r.steps] == ["dot", "loop"]  # 4 tiles: left to the autotuned tiled kernels
 
 
+def test_large_epilogue_dots_get_their_other_k_loop_for_the_autotuner(monkeypatch):
+    """An epilogue GEMM large enough to tune is also generated (and compiled) with the other k loop (k tile 32
+    with cross-tile prefetch), as a separate kernel; small ones, or any with the autotuner off, get none."""
+    from lumen_amd.compiler import codegen
+
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
+    monkeypatch.setattr(Plan, "AUTOTUNE_MACS", 1)
+    with L.config.compiler.patch(horizontal_fusion=False):
+        p = _plan(_epilogue_fn, *EPI_SHAPES, build=True)
+    (si, alts), = p.epi_alts.items()
+    (var, k, src), = alts
+    assert var == 1 and codegen.GemmEpilogueKernel.VARIANTS[var] == (32, True)
+    assert k.name != p.steps[si].name and k.name in src and ", 32, 4, " in src and ", true>(s, a, b" in src
+    assert p.alt_objects[(si, 0)].endswith(".hsaco")
+    with L.config.compiler.patch(horizontal_fusion=False, autotune=False):
+        assert not _plan(_epilogue_fn, *EPI_SHAPES).epi_alts
+    monkeypatch.setattr(Plan, "AUTOTUNE_MACS", 1 << 30)
+    with L.config.compiler.patch(horizontal_fusion=False):
+        assert not _plan(_epilogue_fn, *EPI_SHAPES).epi_alts  # 2^26 multiply-adds
+
+
 def test_one_row_kernel_for_a_normalization_chain():
     p = _plan(lambda x, w: F.softmax(F.rms_norm(x, 256, w) * 3.0, -1), ((32, 256), "float32"), ((256,), "float32"))
     assert [s.kind for s in p.steps] == ["row"]
