@@ -110,8 +110,11 @@ class Compiled:
                 native.d2d(b.ptr, ptrs[i], keep[i].nbytes)
             entry = (plan.capture(workspace.ptr, gptrs), buffers, gptrs)
             graphs[fixed] = entry
-            while len(graphs) > self.GRAPHS_PER_PLAN:
-                graphs.popitem(last=False)
+            if len(graphs) > self.GRAPHS_PER_PLAN:
+                # launches of the evicted graph queued earlier may still read its staging buffers
+                native.sync(dev)
+                while len(graphs) > self.GRAPHS_PER_PLAN:
+                    graphs.popitem(last=False)
         else:
             graphs.move_to_end(fixed)
             _, buffers, gptrs = entry
