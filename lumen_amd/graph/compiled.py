@@ -80,6 +80,9 @@ class Compiled:
     # copy would cost as much as a memory-bound plan itself.
     DIRECT_BYTES = 1 << 20
     GRAPHS_PER_PLAN = 8
+    # Plans of fewer native steps run uncaptured: launching a graph costs the host ~40 us, launching a step
+    # ~3 us, so a short plan (a fused elementwise chain is one kernel) loses time to the graph.
+    GRAPH_MIN_STEPS = 16
 
     def _run(self, plan, workspace, traced, ptrs, keep):
         """``plan.run_in``; with ``config.compiler.hip_graphs`` (the reference's CUDA graphs,
@@ -88,9 +91,11 @@ class Compiled:
         call's runtime scalars and small arguments, and from then on each call copies those in (stream-ordered)
         and launches the graph. Weights, the workspace and large arguments are read where they were captured;
         a call whose large arguments or weights lie elsewhere is captured again (the newest few graphs of a
-        plan are kept, so alternating inputs replay too). Profiled runs (``plan.profile``) are never captured.
+        plan are kept, so alternating inputs replay too). Profiled runs (``plan.profile``) and plans of fewer
+        than GRAPH_MIN_STEPS native steps are never captured.
         Returns the input pointers the run read."""
-        if not config.compiler.hip_graphs or getattr(plan, "_profiling", False):
+        short = len(getattr(plan, "native_steps", ())) < self.GRAPH_MIN_STEPS and plan._native is not None
+        if not config.compiler.hip_graphs or getattr(plan, "_profiling", False) or short:
             plan.run_in(workspace.ptr, ptrs)
             return ptrs
         graphs = self._graphs.get(id(plan))

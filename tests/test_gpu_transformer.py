@@ -121,6 +121,7 @@ def test_hip_graph_reads_large_arguments_in_place(hip, monkeypatch):
     from lumen_amd.graph.compiled import Compiled
 
     monkeypatch.setattr(Compiled, "GRAPHS_PER_PLAN", 2)
+    monkeypatch.setattr(Compiled, "GRAPH_MIN_STEPS", 1)
 
     def fn(x, s):
         return F.softmax(x.float() * s, -1).bfloat16()
@@ -144,7 +145,7 @@ def test_hip_graph_reads_large_arguments_in_place(hip, monkeypatch):
         assert np.array_equal(g_, w_)
 
 
-def test_hip_graph_replays_match_uncaptured_runs(hip):
+def test_hip_graph_replays_match_uncaptured_runs(hip, monkeypatch):
     """With hip_graphs the third and later calls of a compiled function replay one captured HIP graph whose
     arguments and runtime scalars are staged into its own buffers: several calls with new inputs, new
     scalars and eager device work in between, each equal bit for bit to the same call run uncaptured; then
@@ -154,6 +155,15 @@ def test_hip_graph_replays_match_uncaptured_runs(hip):
     def fn(x, w, s):
         return F.relu(F.matmul(x, w, "float32", "float32")) * s + x.float().sum()
 
+    from lumen_amd.graph.compiled import Compiled
+
+    with L.config.compiler.patch(hip_graphs=True):  # a short plan runs uncaptured by default
+        f = L.compile(fn, device="hip")
+        ones = [L.tensor(np.ones(shape, np.float32), "bfloat16") for shape in ((512, 256), (256, 320))]
+        for _ in range(3):
+            f(*ones, 1.0)
+        assert len(f.plan.native_steps) < Compiled.GRAPH_MIN_STEPS and not f._graphs.get(id(f.plan))
+    monkeypatch.setattr(Compiled, "GRAPH_MIN_STEPS", 1)
     rng = np.random.default_rng(5)
     w = L.tensor(D.bf16_to_f32(D.bf16_bits(rng.standard_normal((256, 320)) * 0.1)), "bfloat16")
     xs = [L.tensor(D.bf16_to_f32(D.bf16_bits(rng.standard_normal((512, 256)))), "bfloat16") for _ in range(5)]
