@@ -736,6 +736,12 @@ def _store(expr_name, dtype):
     return f"({STORE_T[dtype]})({expr_name})"
 
 
+def _restrict(v, aliased):
+    """The pointer qualifier of value ``v``'s kernel parameter: ``__restrict__`` unless another parameter may
+    address the same memory."""
+    return "" if v in aliased else " __restrict__"
+
+
 def _vec_width(numel, elem_bytes):
     for v in (8, 4, 2):
         if numel % v == 0 and v * elem_bytes <= 16 and v * elem_bytes in (4, 8, 16) or (v * elem_bytes == 2 and False):
@@ -757,8 +763,11 @@ class LoopKernel:
     LEAD_CHUNK = 128
     LEAD_UNROLL = 8
 
-    def __init__(self, graph, step, name, views: dict, out_views: dict):
+    def __init__(self, graph, step, name, views: dict, out_views: dict, aliased=frozenset()):
         self.graph, self.step, self.name = graph, step, name
+        # values whose memory another argument of the kernel shares (an output written over the input it
+        # replaces, element for element): their pointers are not declared __restrict__
+        self.aliased = aliased
         self.views, self.out_views = views, out_views
         self.args = []  # ("in"|"out", var)
         self.extra_fill = []
@@ -777,10 +786,10 @@ class LoopKernel:
         ps = []
         self.args = []
         for k, v in enumerate(self.step.inputs):
-            ps.append(f"const {STORE_T[self.graph.types[v].dtype]}* __restrict__ in{k}")
+            ps.append(f"const {STORE_T[self.graph.types[v].dtype]}*{_restrict(v, self.aliased)} in{k}")
             self.args.append(("in", v))
         for k, v in enumerate(self.step.outputs):
-            ps.append(f"{STORE_T[self.graph.types[v].dtype]}* __restrict__ out{k}")
+            ps.append(f"{STORE_T[self.graph.types[v].dtype]}*{_restrict(v, self.aliased)} out{k}")
             self.args.append(("out", v))
         return ", ".join(ps)
 
@@ -1236,8 +1245,9 @@ class GemmEpilogueKernel:
     VARIANTS = ((64, False), (32, True))
 
     def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None,
-                 variant=0):
+                 variant=0, aliased=frozenset()):
         self.graph, self.dot, self.loop = graph, dot_step, loop_step
+        self.aliased = aliased  # as LoopKernel.aliased
         self.variant = variant
         self.desc, self.at, self.bt, self.f16, self.store_dot = desc, at, bt, f16, store_dot
         # (value, sum): a float32 loop output summed over the rows into `sum` [n] (atomically, into zeros)
@@ -1274,7 +1284,7 @@ class GemmEpilogueKernel:
         ddt = g.types[dv].dtype
         lin = [v for v in loop.inputs if v != dv]
         # the loop's body, evaluated 4 columns at a time at flat index base + lane of the [m, n] result
-        lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views)
+        lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views, self.aliased)
         em = Emitter(g, loop.nodes, {v: (k, self.views[v]) for k, v in enumerate(lin)})
         em.vec = 4
         accs = [f"acc.{c}" for c in "xyzw"]
@@ -1323,11 +1333,12 @@ class GemmEpilogueKernel:
             ret, colsum_fn = "", []
         self.args = [("in", dot.nodes[0].inputs[0]), ("in", dot.nodes[0].inputs[1])]
         self.args += [("in", v) for v in lin] + [("out", v) for v in outs]
-        fields = [f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k};" for k, v in enumerate(lin)]
-        fields += [f"{STORE_T[g.types[v].dtype]}* __restrict__ out{k};" for k, v in enumerate(outs)]
+        al = self.aliased
+        fields = [f"const {STORE_T[g.types[v].dtype]}*{_restrict(v, al)} in{k};" for k, v in enumerate(lin)]
+        fields += [f"{STORE_T[g.types[v].dtype]}*{_restrict(v, al)} out{k};" for k, v in enumerate(outs)]
         params = ["const uint16_t* __restrict__ a", "const uint16_t* __restrict__ b"]
-        params += [f"const {STORE_T[g.types[v].dtype]}* __restrict__ in{k}" for k, v in enumerate(lin)]
-        params += [f"{STORE_T[g.types[v].dtype]}* __restrict__ out{k}" for k, v in enumerate(outs)]
+        params += [f"const {STORE_T[g.types[v].dtype]}*{_restrict(v, al)} in{k}" for k, v in enumerate(lin)]
+        params += [f"{STORE_T[g.types[v].dtype]}*{_restrict(v, al)} out{k}" for k, v in enumerate(outs)]
         init = ", ".join([f"in{k}" for k in range(len(lin))] + [f"out{k}" for k in range(len(outs))])
         shape = (f"s.m = {d.m}LL; s.n = {d.n}LL; s.k = {d.k}LL; s.nbatch = 0; s.a_m = {d.a_m}LL; "
                  f"s.a_k = {d.a_k}LL; s.b_k = {d.b_k}LL; s.b_n = {d.b_n}LL; s.d_m = {d.n}LL; s.d_n = 1; "

@@ -174,8 +174,11 @@ def compile_graph(graph: Graph, packable=()) -> tuple[Graph, list]:
 class Plan:
     """A graph compiled for ``device`` (``"hip:0"``): steps, workspace layout and native step list."""
 
-    def __init__(self, graph: Graph, device="hip:0", build_kernels=True, packable=(), compiled=None):
+    def __init__(self, graph: Graph, device="hip:0", build_kernels=True, packable=(), compiled=None, donate=None):
         self.device = device
+        # output position -> input position: outputs the caller writes back over that input after each run
+        # (the weights a step assigns); those the placement can compute in place are written there directly
+        self.donate = dict(donate or {})
         self.source_graph = graph
         self.graph, self.packs = compiled if compiled is not None else compile_graph(graph, packable)
         self._lay_out()
@@ -183,7 +186,7 @@ class Plan:
         if limit and compiled is None and self.workspace_bytes > limit:
             # remat.rs via plan/compile.rs:37-44: recompute values past the live-bytes peak
             def plan_of(g):
-                return Plan(graph, device, build_kernels=False, compiled=(g, self.packs))
+                return Plan(graph, device, build_kernels=False, compiled=(g, self.packs), donate=self.donate)
 
             g = remat.rematerialize(self.graph, limit, plan_of)
             if g is not self.graph:
@@ -241,6 +244,78 @@ class Plan:
         self.steps = best[2]
         self._place()
 
+    # ---- outputs computed in place of an input (the reference's donated buffers)
+    def _in_place_outputs(self):
+        """``{output value: input position}`` for the ``donate`` pairs whose output can be written straight over
+        its input: the output's step is an elementwise loop (or a GEMM epilogue) that reads the input only at
+        the element it writes, through elementwise operations of the input's shape, and every other step that
+        reads the input's memory (the input, its views, a pack's concatenation) runs before it. The caller's
+        copy of such an output back into the input is then not needed, nor its workspace."""
+        g = self.graph
+        if not self.donate:
+            return {}
+        # the input positions whose memory each value may address
+        roots = {v: {i} for i, v in enumerate(g.inputs)}
+        packs = {tuple(g.inputs[i] for i in pk): set(pk) for pk in self.packs}
+        for st in self.steps:
+            if st.kind == "view":
+                n = st.nodes[0]
+                if n.output in self.packed:
+                    roots[n.output] = packs.get(tuple(n.inputs), set().union(*(roots.get(u, set()) for u in n.inputs)))
+                elif n.inputs[0] in roots:
+                    roots[n.output] = roots[n.inputs[0]]
+        # a producing step that other readers of the old value follow, none of them reading its results, moves
+        # after the last of them (a weight's update after the GEMM that reads the weight for the input gradient)
+        for op, ip in sorted(self.donate.items()):
+            v = g.outputs[op]
+            si = next((i for i, st in enumerate(self.steps) if v in st.outputs), None)
+            if si is None:
+                continue
+            later = [sj for sj in range(si + 1, len(self.steps))
+                     if any(ip in roots.get(w, ()) for w in self.steps[sj].inputs)]
+            if not later:
+                continue
+            made = set(self.steps[si].outputs)
+            if any(x in made for st in self.steps[si + 1:later[-1] + 1] for x in st.inputs):
+                continue
+            self.steps.insert(later[-1], self.steps.pop(si))
+        producer = {v: si for si, st in enumerate(self.steps) for v in st.outputs}
+        out, taken = {}, set()
+        for op, ip in sorted(self.donate.items()):
+            v, u = g.outputs[op], g.inputs[ip]
+            tv, tu = g.types[v], g.types[u]
+            if (ip in taken or g.outputs.count(v) != 1 or v in roots or u in g.outputs or tv.dtype != tu.dtype
+                    or tuple(tv.shape) != tuple(tu.shape) or v not in producer):
+                continue
+            si = producer[v]
+            st = self.steps[si]
+            if st.kind == "loop":
+                body, others = st.nodes, []
+            elif st.kind == "hloop":
+                member = next(m for m in st.members if v in m.outputs)
+                body, others = member.nodes, [m for m in st.members if m is not member]
+            elif st.kind == "dot" and getattr(st, "epi", None) is not None:
+                body, others = st.epi.nodes, [st.nodes[0]]
+            else:
+                continue
+            # nothing reads the input's memory after the step, nor in it but through `body` at its own element
+            if any(ip in roots.get(w, ()) and (sj > si or (sj == si and w != u))
+                   for sj, s2 in enumerate(self.steps) for w in s2.inputs):
+                continue
+            if any(ip in roots.get(w, ()) for o in others for w in o.inputs):
+                continue
+            reached, same = {u}, True
+            for n in body:
+                if any(x in reached for x in n.inputs):
+                    if n.prim not in fusion.ELEMENTWISE or tuple(g.types[n.output].shape) != tuple(tu.shape):
+                        same = False
+                        break
+                    reached.add(n.output)
+            if same:
+                out[v] = ip
+                taken.add(ip)
+        return out
+
     # ---- placement
     def _place(self):
         g = self.graph
@@ -252,6 +327,9 @@ class Plan:
                 st.kind = "loop"
         self.loc: dict[int, Loc] = {}
         self.scratch: dict[int, Loc] = {}
+        self.in_place = self._in_place_outputs()
+        self.in_place_outputs = {g.outputs.index(v): i for v, i in self.in_place.items()}
+        self.aliased = frozenset(self.in_place) | frozenset(g.inputs[i] for i in self.in_place.values())
         for i, v in enumerate(g.inputs):
             t = g.types[v]
             self.loc[v] = Loc(("in", i), 0, _contig(t.shape), t.dtype, t.shape)
@@ -349,6 +427,9 @@ class Plan:
                         self.loc[c] = Loc(("ws", 0), off // D.size_of(ct.dtype), _contig(ct.shape), ct.dtype, ct.shape)
                     self.loc[v] = _operand_view(self.loc[c], start, aliases[v][2], t)
                     continue
+                if v in self.in_place:  # written over the input it replaces
+                    self.loc[v] = Loc(("in", self.in_place[v]), 0, _contig(t.shape), t.dtype, t.shape)
+                    continue
                 off, size = take(t.nbytes())
                 live[v] = (off, size)
                 strides = _contig(t.shape)
@@ -383,7 +464,7 @@ class Plan:
         self.output_locs = []
         for v in g.outputs:
             loc = self.loc[v]
-            if loc.base[0] == "in" or not loc.contiguous():
+            if (loc.base[0] == "in" and v not in self.in_place) or not loc.contiguous():
                 t = g.types[v]
                 off = self.workspace_bytes
                 self.workspace_bytes += -(-t.nbytes() // ALIGNMENT) * ALIGNMENT
@@ -576,7 +657,7 @@ class Plan:
                 for m in st.members:
                     views = {v: self.loc[v].view() for v in m.inputs}
                     outs = {v: self.loc[v].view() for v in m.outputs}
-                    parts.append(codegen.LoopKernel(g, m, "KNAME", views, outs))
+                    parts.append(codegen.LoopKernel(g, m, "KNAME", views, outs, self.aliased))
                 k = codegen.HorizontalKernel(parts)
                 body = k.source()
                 name = f"hloop_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
@@ -591,7 +672,7 @@ class Plan:
                 views = {v: self.loc[v].view() for v in lin}
                 outs = {v: self.loc[v].view() for v in st.outputs}
                 k = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
-                                               colsum=getattr(st, "epi_colsum", None))
+                                               colsum=getattr(st, "epi_colsum", None), aliased=self.aliased)
                 body = k.source()
                 name = f"gemm_epi_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
                 k.name = st.name = name
@@ -604,7 +685,8 @@ class Plan:
                         if not k.variant_ok(var):
                             continue
                         kv = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
-                                                        colsum=getattr(st, "epi_colsum", None), variant=var)
+                                                        colsum=getattr(st, "epi_colsum", None), variant=var,
+                                                        aliased=self.aliased)
                         bv = kv.source()
                         kv.name = f"gemm_epi_{hashlib.sha1(bv.encode()).hexdigest()[:10]}"
                         self.epi_alts.setdefault(si, []).append((var, kv, codegen.HEADER + bv.replace("KNAME", kv.name)))
@@ -619,7 +701,7 @@ class Plan:
                 st.inputs = [v for v in n.inputs[1:]]
             views = {v: self.loc[v].view() for v in st.inputs}
             outs = {v: self.loc[v].view() for v in st.outputs}
-            k = codegen.LoopKernel(g, st, "KNAME", views, outs)
+            k = codegen.LoopKernel(g, st, "KNAME", views, outs, self.aliased)
             body = k.source()
             name = f"{st.kind}_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
             k.name = name
@@ -647,10 +729,11 @@ class Plan:
         self.alt_objects = {key: p for key, p in zip(alts, paths[len(keys):])}
 
     def _epi_overlaps(self, st):
-        """Whether an epilogue GEMM step writes memory it also reads (then it is never run for timing alone)."""
+        """Whether an epilogue GEMM step writes memory it also reads (then it is never run for timing alone).
+        Outputs written over their input count as not overlapping: the autotuner writes them elsewhere."""
         ins = [self.loc[v] for v in st.nodes[0].inputs if v in self.loc] + \
               [self.loc[v] for v in st.epi.inputs if v != st.nodes[0].output and v in self.loc]
-        outs = [self.loc[v] for v in st.outputs if v in self.loc]
+        outs = [self.loc[v] for v in st.outputs if v in self.loc and v not in self.in_place]
 
         def span(loc):
             lo = loc.offset * D.size_of(loc.dtype)
@@ -875,10 +958,13 @@ class Plan:
         the plan launches. Kept per generated source for the process."""
         from lumen_amd import native as nv
 
+        from lumen_amd.tensor import DeviceBuffer
+
         if not self.epi_alts:
             return
         if not hasattr(self, "objects"):
             self.build()
+        g = self.graph
         ev0, ev1 = nv.Event(), nv.Event()
         for si, alts in self.epi_alts.items():
             st = self.steps[si]
@@ -886,8 +972,13 @@ class Plan:
             if key not in Plan._tuned:
                 k0 = self.kernels[si]
                 ptrs = []
-                for _, v in k0.args:
+                spare = []  # outputs computed in place of an input go to a buffer of their own while timed
+                for kind, v in k0.args:
                     loc = self.loc[v]
+                    if kind == "out" and v in self.in_place:
+                        spare.append(DeviceBuffer(int(self.device.split(":")[1]), g.types[v].nbytes()))
+                        ptrs.append(spare[-1].ptr)
+                        continue
                     base = workspace_ptr if loc.base[0] == "ws" else input_ptrs[loc.base[1]]
                     ptrs.append(base + loc.offset * D.size_of(loc.dtype))
                 args = (C.c_uint64 * max(1, len(ptrs)))(*ptrs)

@@ -22,6 +22,10 @@ class CompilerFlags:
     # dQ = dS K reads it back, instead of a second kernel recomputing S and dP (off: no dS workspace)
     attention_store_ds: bool = True
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
+    # a weight the compiled function assigns is computed over its old value where the step producing it reads
+    # the old value only at the element it writes and nothing reads it later (off: into the workspace, then
+    # copied back after the run)
+    update_in_place: bool = True
     # simplify's structural rewrites after pattern matching (swapped/folded dots, ops moved across layouts)
     simplify_structural: bool = True
     # try the list and depth-first step schedules and keep the order needing the least workspace

@@ -60,7 +60,11 @@ class Compiled:
                 from lumen_amd.compiler.plan import Plan
 
                 weight_pos = [i for i, (kind, _) in enumerate(traced.layout) if kind == "weight"]
-                plan = Plan(traced.graph, target, packable=weight_pos)
+                # each weight the function assigns: its new value may be computed over the old one
+                at = {k: i for i, (kind, k) in enumerate(traced.layout) if kind == "weight"}
+                donate = {traced.n_returned + j: at[k] for j, k in enumerate(traced.written)} \
+                    if config.compiler.update_in_place else {}
+                plan = Plan(traced.graph, target, packable=weight_pos, donate=donate)
                 workspace = DeviceBuffer(int(target.split(":")[1]), plan.workspace_bytes)
                 for w in traced.weights:
                     w._placed(target)
@@ -166,11 +170,15 @@ class Compiled:
             self._last_buffers = (workspace.ptr, ptrs)
             outs = []
             for v, loc in zip(g.outputs, plan.output_locs):
+                if loc.base[0] == "in":  # computed over the weight it replaces
+                    outs.append(keep[loc.base[1]])
+                    continue
                 t = Tensor(loc.dtype, loc.shape, target, buffer=workspace, offset=loc.offset * _size(loc.dtype))
                 outs.append(t)
-            # weights the function assigned: written back into their memory, in stream order
+            # the other weights the function assigned: written back into their memory, in stream order
             for j, k in enumerate(traced.written):
-                traced.weights[k]._placed(target).copy_(outs[traced.n_returned + j])
+                if traced.n_returned + j not in plan.in_place_outputs:
+                    traced.weights[k]._placed(target).copy_(outs[traced.n_returned + j])
             self._keep = keep
         for i, path, value in traced.static_writes:
             nn.assign(args[i], path, value)

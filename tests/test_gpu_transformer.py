@@ -191,3 +191,33 @@ def test_hip_graph_replays_match_uncaptured_runs(hip, monkeypatch):
             losses[graphs].append(D.bf16_to_f32(model.head._placed("hip:0").raw()).copy())
     assert losses[True][:4] == losses[False][:4]
     assert np.array_equal(losses[True][4], losses[False][4])
+
+
+@pytest.mark.parametrize("cfg_name", ["TINY", "CONFIG4"])
+def test_weights_updated_in_place_match_copied_updates(hip, cfg_name):
+    """Every weight the training step assigns is computed over its old value (no workspace copy, no copy
+    back), including the weight-gradient GEMMs whose epilogue applies the update (at config 4 they are large
+    enough for the epilogue autotuner, which then writes them elsewhere while timing): three steps give the
+    losses and weights of the same steps with the updates written to the workspace and copied back, to
+    float32 rounding of the loss and one bf16 step of every weight (the column sums fused into some
+    epilogues add with atomics, in no fixed order)."""
+    cfg = getattr(W, cfg_name)
+    got = {}
+    for in_place in (True, False):
+        model, opt, weights, ids, targets, args = _setup(cfg, W.train_step)
+        args = (model, opt) + args[1:]
+        with L.config.compiler.patch(update_in_place=in_place, hip_graphs=True):
+            step = L.compile(W.train_step, device="hip")
+            losses = [float(L.to_numpy(step(*args))) for _ in range(3)]
+            traced = trace(W.train_step, args)
+            if in_place:
+                assert len(step.plan.in_place_outputs) == len(traced.written)
+                assert not any(st.kind == "copy" for st in step.plan.steps)
+            else:
+                assert not step.plan.in_place_outputs
+        got[in_place] = (losses, [D.bf16_to_f32(p._placed("hip:0").raw()).astype(np.float64)
+                                  for _, p in model.named_parameters()])
+    for a, b in zip(got[True][0], got[False][0]):
+        assert abs(a - b) <= 1e-5 * abs(b), (a, b)
+    for (name, _), a, b in zip(model.named_parameters(), got[True][1], got[False][1]):
+        assert np.all(np.abs(a - b) <= _bf16_step(b)), (name, float(np.abs(a - b).max()))

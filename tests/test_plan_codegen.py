@@ -281,3 +281,66 @@ def test_memory_limit_rematerializes_values_without_changing_them():
     xs = [(rng.standard_normal(s) * 0.1).astype(np.float32) for s, _ in REMAT_METAS]
     for a, b in zip(oracle.run(p0.graph, xs), oracle.run(p1.graph, xs)):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _donated(fn, metas, donate):
+    g = L.make_graph(fn)(*[L.empty(list(s), d, "meta") for s, d in metas])
+    return Plan(g, build_kernels=False, donate=donate)
+
+
+def test_assigned_weights_of_the_training_step_are_updated_in_place():
+    """Each weight the training step assigns is computed over the weight it replaces: its loc is the weight's
+    own input, no output copy remains, every step still follows the producers of what it reads, and the
+    generated kernels declare the aliased pointers without __restrict__."""
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    traced = trace(W.train_step, (model, opt, ids, ids))
+    at = {k: i for i, (kind, k) in enumerate(traced.layout) if kind == "weight"}
+    donate = {traced.n_returned + j: at[k] for j, k in enumerate(traced.written)}
+    p = Plan(traced.graph, build_kernels=False, packable=list(at.values()), donate=donate)
+    g = p.graph
+    assert p.in_place_outputs == donate
+    assert not any(st.kind == "copy" for st in p.steps)
+    for op, ip in donate.items():
+        assert p.output_locs[op].base == ("in", ip) and p.output_locs[op].offset == 0
+    made = set(g.inputs)
+    for st in p.steps:
+        assert all(u in made for u in st.inputs), st.label()
+        made.update(st.outputs)
+    import re
+
+    checked = 0
+    for si, k in p.kernels.items():
+        sig = re.search(r"void\s+\w+\((.*?)\)\s*\{", p.sources[si], re.S).group(1).split(", ")
+        assert len(sig) == len(k.args), p.sources[si][:300]
+        for param, (_, v) in zip(sig, k.args):
+            assert ("__restrict__" in param) == (v not in p.aliased), param
+            checked += v in p.aliased
+    assert checked >= 2 * len(donate)
+
+
+def test_updates_stay_out_of_place_when_their_input_is_read_elsewhere():
+    """An output is not written over its input when its step reads the input at other elements (a transpose)
+    or when a step that needs the output still reads the old input; a plain elementwise update is."""
+    sq = ((64, 64), "float32")
+    p = _donated(lambda w: (w * 0.5,), [sq], {0: 0})
+    assert p.in_place_outputs == {0: 0} and p.output_locs[0].base == ("in", 0)
+    p = _donated(lambda w: (w - w.t(),), [sq], {0: 0})
+    assert p.in_place_outputs == {} and p.output_locs[0].base == ("ws", 0)
+
+    def later(w, x):
+        nw = w * 0.5
+        return nw, F.matmul(x, nw, "float32", "float32") + F.matmul(x, w, "float32", "float32")
+
+    p = _donated(later, [sq, sq], {0: 0})  # the update moves after the other reader of w
+    assert p.in_place_outputs == {0: 0}
+    prod = {v: si for si, st in enumerate(p.steps) for v in st.outputs}
+    readers = [si for si, st in enumerate(p.steps) if p.graph.inputs[0] in st.inputs]
+    assert max(readers) == prod[p.graph.outputs[0]]
+
+    def needed(w, x):
+        nw = w * 0.5
+        return nw, F.matmul(x, nw, "float32", "float32") + w
+
+    p = _donated(needed, [sq, sq], {0: 0})  # w is read with a result of the update: it cannot move
+    assert p.in_place_outputs == {}
