@@ -186,10 +186,14 @@ int nhip_flash_bwd_noalloc(const nhip_attn_desc *desc, const void *q, const void
  *
  * h [b, d] and w [v, d] row-major (both bf16, both f16, or both float32), target [b] int32 or int64 (as
  * target_dtype NHIP_LCE_I32 / NHIP_LCE_I64). out is float32 [2, b]: row 0 the loss lse - logit[class], row 1
- * lse = max + log(sum_j exp(logit_j - max)), class = target clamped into [0, v). The float32 logits of
- * chunk_rows rows at a time go through `workspace` (nhip_linear_cross_entropy_workspace bytes: chunk_rows * v
- * float32) by nhip_gemm, then one workgroup a row reduces them (maximum, float32 exponentials summed in
- * float64, picked logit), so the [b, v] logits never exist whole. */
+ * lse = max + log(sum_j exp(logit_j - max)), class = target clamped into [0, v). The [b, v] logits never
+ * exist whole. With 16-bit operands, d % 64 == 0 and v % 64 == 0 (and h, w 16-byte aligned) the GEMM's store
+ * reduces each row's 64-class blocks to a (maximum, float32 sum of exponentials) pair and picks the class's
+ * logit, and a second kernel combines a row's pairs in float64 (workspace: b * v / 64 pairs of floats, rounded
+ * up to 256 bytes, plus b floats; at least one row of logits). Otherwise the float32 logits of chunk_rows rows
+ * at a time go through `workspace` (chunk_rows * v float32) by nhip_gemm, then one workgroup a row reduces them
+ * (maximum, float32 exponentials summed in float64, picked logit). nhip_linear_cross_entropy_workspace gives
+ * the bytes for either form. */
 enum {
     NHIP_LCE_I32 = 0,
     NHIP_LCE_I64 = 1,

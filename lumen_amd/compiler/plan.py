@@ -449,7 +449,7 @@ class Plan:
                     d, _ = self._gemm_desc(st.nodes[0])
                     st.scratch = st.splits * max(1, math.prod(d.batch[i] for i in range(d.nbatch))) * d.m * d.n * 4
             if st.kind == "linear_cross_entropy":
-                st.scratch = self._lce_desc(st.nodes[0]).chunk_rows * g.types[st.nodes[0].inputs[1]].shape[0] * 4
+                st.scratch = self._lce_scratch(self._lce_desc(st.nodes[0]))
             if st.scratch:
                 off, size = take(st.scratch)
                 self.scratch[id(st)] = Loc(("ws", 0), off // 4, (1,), "float32", (st.scratch // 4,))
@@ -926,6 +926,16 @@ class Plan:
         d.dtype = NHIP_DT[h.dtype]
         d.target_dtype = nv.NHIP_LCE_I64 if t.dtype == "int64" else nv.NHIP_LCE_I32
         return d
+
+    @staticmethod
+    def _lce_scratch(desc):
+        """The step's scratch bytes: what nhip_linear_cross_entropy_workspace asks for the descriptor (the fused
+        form's per-block partials, or chunk_rows rows of float32 logits)."""
+        from lumen_amd import native as nv
+
+        n = C.c_size_t()
+        nv.call("nhip_linear_cross_entropy_workspace", C.byref(desc), C.byref(n))
+        return n.value
 
     # ---- autotuning (lumen/autotune/mod.rs:20-150): bf16/f16 dots of at least 2^30 multiply-adds try every tile
     # config the kernel accepts, timed with HIP events on the step's own operands (their values do not change

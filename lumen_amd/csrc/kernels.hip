@@ -440,6 +440,151 @@ __global__ __launch_bounds__(256) void lce_rows_kernel(const float *__restrict__
     }
 }
 
+// The fused form: the streamed GEMM's store runs LceOut instead of writing logits. gemm_stream_tile hands a
+// lane four consecutive columns of one row, and the 16 lanes of a DPP row (lanes 16 q .. 16 q + 15) hold the 64
+// columns of one row of a wave's 64-column block (a row's lanes are all in or all out of range, rows by row
+// and columns because v % 64 == 0): each block's maximum and float32 sum of exp(logit - maximum) combine
+// across those lanes by DPP rotations, and the block's first lane stores them as part[row][block]; the lane
+// holding the row's clamped class (read ahead with the chunk, Pre) stores that logit. lce_merge_kernel then
+// reduces a row's v / 64 pairs: nothing of size [b, v] is written.
+template <int CTRL>
+__device__ __forceinline__ float lce_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+struct LceOut {
+    float2 *part;
+    float *picked;
+    const void *target;
+    int t64;
+    int64_t nblk;
+    static constexpr int kPrefetch = 8;
+    static constexpr bool kColSum = false;
+    struct Pre {
+        int64_t cls;
+    };
+    __device__ __forceinline__ Pre load(int64_t r, int64_t) const {
+        const int64_t t = t64 ? static_cast<const int64_t *>(target)[r] : static_cast<const int32_t *>(target)[r];
+        const int64_t v = nblk * 64;
+        return Pre{t < 0 ? 0 : (t >= v ? v - 1 : t)};
+    }
+    __device__ __forceinline__ void operator()(int64_t r, int64_t c, float4 acc, const Pre &pre) const {
+        // row_ror 8, row_ror 4, then the quad permutations [2,3,0,1] and [1,0,3,2]: every lane of the DPP row
+        // ends with the combination of all 16
+        float m = fmaxf(fmaxf(acc.x, acc.y), fmaxf(acc.z, acc.w));
+        m = fmaxf(m, lce_dpp<0x128>(m));
+        m = fmaxf(m, lce_dpp<0x124>(m));
+        m = fmaxf(m, lce_dpp<0x4e>(m));
+        m = fmaxf(m, lce_dpp<0xb1>(m));
+        // exp(x - m) = 2^((x - m) log2 e): the difference is exact near the maximum, where the terms matter
+        constexpr float kLog2e = 1.4426950408889634f;
+        float e = 0.0f;
+        if (m != -INFINITY)
+            e = (__builtin_amdgcn_exp2f((acc.x - m) * kLog2e) + __builtin_amdgcn_exp2f((acc.y - m) * kLog2e)) +
+                (__builtin_amdgcn_exp2f((acc.z - m) * kLog2e) + __builtin_amdgcn_exp2f((acc.w - m) * kLog2e));
+        e += lce_dpp<0x128>(e);
+        e += lce_dpp<0x124>(e);
+        e += lce_dpp<0x4e>(e);
+        e += lce_dpp<0xb1>(e);
+        if ((c & 63) == 0) part[r * nblk + (c >> 6)] = make_float2(m, e);
+        if (pre.cls >= c && pre.cls < c + 4) {
+            const int64_t q = pre.cls - c;
+            picked[r] = q == 0 ? acc.x : (q == 1 ? acc.y : (q == 2 ? acc.z : acc.w));
+        }
+    }
+};
+
+template <bool F16, bool BUF>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void lce_gemm_kernel(
+    GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, LceOut out) {
+    extern __shared__ __align__(1024) char smem[];
+    gemm_stream_tile<F16, 64, 4, false, false, BUF, LceOut, 256, false>(s, a, b, out, smem);
+}
+
+// One wavefront a row: the maximum of the row's block maxima, then the float64 sum of each block's sum scaled
+// by exp(block maximum - row maximum) (float32 exponentials, as lce_rows_kernel); lse and loss rounded as there.
+__global__ __launch_bounds__(256) void lce_merge_kernel(const float2 *__restrict__ part, const float *__restrict__ picked,
+                                                        int64_t nblk, float *__restrict__ out, int64_t b) {
+    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= b) return;  // the whole wavefront
+    const float2 *p = part + row * nblk;
+    float m = -INFINITY;
+    for (int64_t j = lane; j < nblk; j += 64) m = fmaxf(m, p[j].x);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    double sum = 0.0;
+    for (int64_t j = lane; j < nblk; j += 64) {
+        const float2 q = p[j];
+        if (q.x != -INFINITY) sum += double(q.y) * double(lce_exp(q.x - m));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) {
+        const float l = float(double(m) + log(sum));
+        out[row] = float(double(l) - double(picked[row]));
+        out[b + row] = l;
+    }
+}
+
+// Whether `d` takes the fused form (16-bit operands, k a multiple of the GEMM's k tile, whole 64-class blocks).
+bool lce_fused(const nhip_lce_desc *d) {
+    return d->dtype != NHIP_F32 && d->b > 0 && d->d > 0 && d->d % 64 == 0 && d->v % 64 == 0;
+}
+
+size_t lce_part_bytes(const nhip_lce_desc *d) { return (size_t(d->b) * size_t(d->v / 64) * 8 + 255) / 256 * 256; }
+
+size_t lce_workspace_bytes(const nhip_lce_desc *d) {
+    if (d->b <= 0 || d->v <= 0) return 0;
+    if (lce_fused(d)) {
+        // the partials and picked logits, and at least one row of logits for the unfused form (operands that
+        // are not 16-byte aligned)
+        const size_t fused = lce_part_bytes(d) + size_t(d->b) * 4, row = size_t(d->v) * 4;
+        return fused > row ? fused : row;
+    }
+    const int64_t chunk = d->chunk_rows <= 0 || d->chunk_rows > d->b ? d->b : d->chunk_rows;
+    return size_t(chunk) * size_t(d->v) * 4;
+}
+
+int lce_fused_on(hipStream_t st, const nhip_lce_desc *d, const void *h, const void *w, const void *target, float *out,
+                 void *ws) {
+    GemmShape s;
+    std::memset(&s, 0, sizeof(s));
+    s.m = d->b;
+    s.n = d->v;
+    s.k = d->d;
+    s.a_m = d->d;
+    s.a_k = 1;
+    s.b_k = 1;
+    s.b_n = d->d;
+    s.d_m = d->v;
+    s.d_n = 1;
+    s.tiles_m = int((d->b + 255) / 256);
+    s.tiles_n = int((d->v + 255) / 256);
+    LceOut o;
+    o.part = static_cast<float2 *>(ws);
+    o.picked = reinterpret_cast<float *>(static_cast<char *>(ws) + lce_part_bytes(d));
+    o.target = target;
+    o.t64 = d->target_dtype == NHIP_LCE_I64;
+    o.nblk = d->v / 64;
+    constexpr int lds = gemm_stream_lds_bytes<64, 4>();
+    const bool buf = stream_buffer_ok(s.m, s.n, s.k, false, false, s.a_m, s.a_k, s.b_k, s.b_n);
+    const bool f16 = d->dtype == NHIP_F16;
+    auto kern = f16 ? (buf ? lce_gemm_kernel<true, true> : lce_gemm_kernel<true, false>)
+                    : (buf ? lce_gemm_kernel<false, true> : lce_gemm_kernel<false, false>);
+    if (int rc = check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                       "hipFuncSetAttribute"))
+        return rc;
+    if (int64_t(s.tiles_m) * s.tiles_n > 0x7fffffff) return fail("nhip_linear_cross_entropy: too many tiles");
+    hipLaunchKernelGGL(kern, dim3(unsigned(s.tiles_m * s.tiles_n)), dim3(512), lds, st, s,
+                       static_cast<const uint16_t *>(h), static_cast<const uint16_t *>(w), o);
+    if (int rc = check(hipGetLastError(), "lce_gemm_kernel launch")) return rc;
+    hipLaunchKernelGGL(lce_merge_kernel, dim3(unsigned((d->b + 3) / 4)), dim3(256), 0, st,
+                       static_cast<const float2 *>(o.part), static_cast<const float *>(o.picked), o.nblk, out, d->b);
+    return check(hipGetLastError(), "lce_merge_kernel launch");
+}
+
 int64_t lce_chunk(const nhip_lce_desc *d) {
     return d->chunk_rows <= 0 || d->chunk_rows > d->b ? d->b : d->chunk_rows;
 }
@@ -453,7 +598,13 @@ int lce_on(hipStream_t st, const nhip_lce_desc *d, const void *h, const void *w,
         return fail("nhip_linear_cross_entropy: targets must be int32 or int64");
     if (d->b == 0) return 0;
     if (!ws) return fail("nhip_linear_cross_entropy: no workspace");
-    const int64_t chunk = lce_chunk(d);
+    int64_t chunk = lce_chunk(d);
+    if (lce_fused(d)) {
+        if (aligned16(h) && aligned16(w)) return lce_fused_on(st, d, h, w, target, out, ws);
+        // unaligned operands: the unfused form, as many rows a pass as the fused form's workspace holds
+        const int64_t fit = int64_t(lce_workspace_bytes(d) / (size_t(d->v) * 4));
+        chunk = chunk < fit ? chunk : fit;
+    }
     const int64_t esize = d->dtype == NHIP_F32 ? 4 : 2;
     for (int64_t r0 = 0; r0 < d->b; r0 += chunk) {
         const int64_t rows = d->b - r0 < chunk ? d->b - r0 : chunk;
@@ -517,7 +668,7 @@ int nhip_linear_cross_entropy(const nhip_lce_desc *desc, const void *h, const vo
 }
 
 int nhip_linear_cross_entropy_workspace(const nhip_lce_desc *desc, size_t *bytes) {
-    *bytes = desc->b > 0 && desc->v > 0 ? size_t(lce_chunk(desc)) * size_t(desc->v) * 4 : 0;
+    *bytes = lce_workspace_bytes(desc);
     return 0;
 }
 

@@ -64,26 +64,69 @@ def test_bf16_with_clamped_int64_targets_and_chunks(hip, monkeypatch):
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
 
 
-def test_c_abi_matches_plan(hip):
-    """nhip_linear_cross_entropy through the C ABI (workspace from nhip_linear_cross_entropy_workspace, two
-    chunks) against the compiled plan (one chunk): the same float32 values up to the GEMM tile the row
-    count selects (rtol 1e-5)."""
+def _abi(h, w, t, chunk_rows, h_offset=0):
+    """nhip_linear_cross_entropy through the C ABI with the workspace nhip_linear_cross_entropy_workspace asks
+    for; h at ``h_offset`` bytes into its block. Returns (out [2, b], workspace bytes)."""
+    b, d = h.shape
+    desc = nv.LceDesc()
+    desc.b, desc.v, desc.d, desc.chunk_rows = b, w.shape[0], d, chunk_rows
+    desc.dtype, desc.target_dtype = nv.NHIP_BF16, nv.NHIP_LCE_I32 if t.dtype == np.int32 else nv.NHIP_LCE_I64
+    ws = C.c_size_t()
+    nv.call("nhip_linear_cross_entropy_workspace", C.byref(desc), C.byref(ws))
+    dh = Dev(nbytes=h.nbytes + 16)
+    nv.h2d(dh.ptr + h_offset, np.ascontiguousarray(h).ctypes.data, h.nbytes)
+    dw, dt, do, dws = Dev(w), Dev(t), Dev(nbytes=2 * b * 4), Dev(nbytes=ws.value)
+    nv.call("nhip_linear_cross_entropy", C.byref(desc), dh.ptr + h_offset, dw.ptr, dt.ptr, do.ptr, dws.ptr)
+    return do.get((2, b), np.float32), ws.value
+
+
+@pytest.mark.parametrize("v", [2048, 2000])
+def test_c_abi_matches_plan(hip, v):
+    """nhip_linear_cross_entropy through the C ABI against the compiled plan: with v a multiple of 64 both take
+    the fused form (workspace: a (maximum, sum) pair a row and 64-class block plus a logit a row); otherwise
+    the ABI call goes in 50-row chunks of float32 logits and the plan in one: the same float32 values up to
+    the GEMM tile the row count selects (rtol 1e-5)."""
     rng = np.random.default_rng(8)
-    b, v, d = 96, 2048, 64
+    b, d = 96, 64
     h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
     w = D.bf16_bits((rng.standard_normal((v, d)) * 0.1).astype(np.float32))
     t = rng.integers(0, v, b).astype(np.int32)
     want, _, _ = _run(h, w, t, "bfloat16")
-    desc = nv.LceDesc()
-    desc.b, desc.v, desc.d, desc.chunk_rows = b, v, d, 50
-    desc.dtype, desc.target_dtype = nv.NHIP_BF16, nv.NHIP_LCE_I32
-    ws = C.c_size_t()
-    nv.call("nhip_linear_cross_entropy_workspace", C.byref(desc), C.byref(ws))
-    assert ws.value == 50 * v * 4
-    dh, dw, dt, do, dws = Dev(h), Dev(w), Dev(t), Dev(nbytes=2 * b * 4), Dev(nbytes=ws.value)
-    nv.call("nhip_linear_cross_entropy", C.byref(desc), dh.ptr, dw.ptr, dt.ptr, do.ptr, dws.ptr)
-    got = do.get((2, b), np.float32)
+    got, ws = _abi(h, w, t, 50)
+    assert ws == (b * (v // 64) * 8 + 255) // 256 * 256 + b * 4 if v % 64 == 0 else ws == 50 * v * 4
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_fused_form_with_ragged_tiles_and_clamped_targets(hip):
+    """The fused form (the GEMM's store reduces each 64-class block, a merge kernel the blocks) with rows and
+    classes that fill neither 256-row nor 256-class tiles (b 300, v 4160 = 65 blocks), logits large enough
+    that most exponentials underflow, and int64 targets below 0 and past v (clamped): against the oracle at
+    float32 tolerance."""
+    rng = np.random.default_rng(41)
+    b, v, d = 300, 4160, 128
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32) * 3.0)
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.6).astype(np.float32))
+    t = rng.integers(-5, v + 5, b).astype(np.int64)
+    t[:4] = [-1, v, v + 7, v - 1]
+    got, want, f = _run(h, w, t, "bfloat16")
+    assert Plan._lce_scratch(f.plan._lce_desc(f.plan.steps[0].nodes[0])) < b * v * 4 // 16
+    assert np.ptp(want[1]) > 10  # rows of very different scales
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+
+
+def test_fused_form_with_unaligned_operands_takes_the_row_kernel(hip):
+    """h one bf16 element past a 16-byte boundary: the fused form's loads need 16-byte rows, so the call goes
+    through float32 logit rows in chunks that fit the fused form's workspace, and agrees with the aligned call
+    to float32 rounding of the two reductions (rtol 1e-5)."""
+    rng = np.random.default_rng(43)
+    b, v, d = 64, 1024, 64
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.1).astype(np.float32))
+    t = rng.integers(0, v, b).astype(np.int32)
+    aligned, ws = _abi(h, w, t, 0)
+    unaligned, ws2 = _abi(h, w, t, 0, h_offset=2)
+    assert ws == ws2 and ws < b * v * 4
+    np.testing.assert_allclose(unaligned, aligned, rtol=1e-5, atol=1e-5 * np.abs(aligned).max())
 
 
 def test_compiled_eval_loss_uses_the_fused_step(hip):

@@ -167,20 +167,26 @@ def test_loop_over_a_row_space_joins_the_row_kernel():
     assert [s.kind for s in big] == ["row"], [(s.kind, s.label()) for s in p.steps]
 
 
-def test_linear_cross_entropy_is_a_builtin_step_with_bounded_scratch(monkeypatch):
-    """Primitive::LinearCrossEntropy lowers to one built-in step whose scratch holds a chunk of float32 logit
-    rows (Plan.LCE_SCRATCH bytes at most), not the whole [b, v]."""
+@pytest.mark.parametrize("v", [32000, 32001])
+def test_linear_cross_entropy_is_a_builtin_step_with_bounded_scratch(monkeypatch, v):
+    """Primitive::LinearCrossEntropy lowers to one built-in step whose scratch is never the whole [b, v]: with
+    bf16 operands, k a multiple of 64 and whole 64-class blocks the fused form's (maximum, sum) pair a row
+    and block plus a logit a row; otherwise a chunk of float32 logit rows (Plan.LCE_SCRATCH bytes at most)."""
     from lumen_amd.compiler.plan import Plan
     from lumen_amd.graph import prims
 
     monkeypatch.setattr(Plan, "LCE_SCRATCH", 1 << 20)
     h = L.empty([4096, 256], "bfloat16", "meta")
-    w = L.empty([32000, 256], "bfloat16", "meta")
+    w = L.empty([v, 256], "bfloat16", "meta")
     t = L.empty([4096], "int64", "meta")
     p = Plan(L.make_graph(lambda h, w, t: prims.linear_cross_entropy(h, w, t))(h, w, t), build_kernels=False)
     assert [s.kind for s in p.steps] == ["linear_cross_entropy"]
     d = p._lce_desc(p.steps[0].nodes[0])
-    assert d.chunk_rows == (1 << 20) // (32000 * 4) and p.steps[0].scratch == d.chunk_rows * 32000 * 4
+    assert d.chunk_rows == (1 << 20) // (v * 4)
+    if v % 64 == 0:
+        assert p.steps[0].scratch == 4096 * (v // 64) * 8 + 4096 * 4
+    else:
+        assert p.steps[0].scratch == d.chunk_rows * v * 4
 
 
 def test_hoisting_casts_into_producers_reads_fewer_bytes(monkeypatch):
