@@ -84,9 +84,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="5", choices=["1", "2", "3", "4", "5", "tiny"],
+    ap.add_argument("--config", default="5", choices=["1", "2", "3", "4", "5", "tiny", "lce"],
                     help="4, 5, tiny: the training step; 1, 2, 3: the single-op configurations (relu(matmul) f32, "
-                         "the fused elementwise/norm/softmax chain, flash attention forward + backward)")
+                         "the fused elementwise/norm/softmax chain, flash attention forward + backward); lce: the "
+                         "config-5 eval loss, fused linear cross entropy against unfused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     ap.add_argument("--probe", action="store_true",
@@ -107,7 +108,7 @@ def main():
     from lumen_amd import native
     from lumen_amd import workloads as W
 
-    if args.config in ("1", "2", "3"):
+    if args.config in OP_CONFIGS:
         native.set_device(0)
         out = OP_CONFIGS[args.config](args)
         print(json.dumps(out), flush=True)
@@ -489,7 +490,72 @@ def _attn_cpu(b, s, n, d, sl=256):
                       f"in the C oracle (1 thread), scaled by (S/{sl})^2 x B x N and x3.5 for forward + backward"}
 
 
-OP_CONFIGS = {"1": _config1, "2": _config2, "3": _config3}
+def _config_lce(args):
+    """The eval loss mean(cross_entropy(h . w^T, t)) at the config-5 head's shapes (h [16384, 2048], w [32000,
+    2048] bf16, int64 targets): the linear_cross_entropy step (the fused GEMM store reduction and its merge)
+    against the same loss compiled unfused (logits GEMM + cross-entropy row kernel), calls alternated."""
+    import numpy as np
+
+    import lumen_amd as L
+    import lumen_amd.functional as F
+    from lumen_amd import dtypes as D
+    from oracle import oracle
+
+    def fn(h, w, t):
+        return F.mean(F.cross_entropy(F.matmul(h, w.t(), "float32", "float32"), t))
+
+    b, v, d = 16384, 32000, 2048
+    rng = np.random.default_rng(0)
+    h = D.bf16_bits(rng.standard_normal((b, d)).astype(np.float32))
+    w = D.bf16_bits((rng.standard_normal((v, d)) * 0.02).astype(np.float32))
+    t = rng.integers(0, v, b).astype(np.int64)
+    hd = L.tensor(D.bf16_to_f32(h), "bfloat16").to("hip")
+    wd = L.tensor(D.bf16_to_f32(w), "bfloat16").to("hip")
+    td = L.from_numpy(t).to("hip")
+    fs = {}
+    for fused in (True, False):
+        with L.config.compiler.patch(fused_linear_cross_entropy=fused):
+            fs[fused] = L.compile(fn, device="hip")
+            fs[fused](hd, wd, td)
+    assert "linear_cross_entropy" in [st.kind for st in fs[True].plan.steps]
+    ms = {True: [], False: []}
+    for _ in range(2):
+        for fused in (True, False):
+            with L.config.compiler.patch(fused_linear_cross_entropy=fused):
+                ms[fused].append(_time_calls(lambda: fs[fused](hd, wd, td), args.steps, args.warmup))
+    loss = {k: float(L.to_numpy(f(hd, wd, td))) for k, f in fs.items()}
+    with L.config.compiler.patch(fused_linear_cross_entropy=True):
+        per = _plan_kernel_ms(fs[True], lambda: fs[True](hd, wd, td))
+    plan = fs[True].plan
+    si = next(i for i, st in enumerate(plan.steps) if st.kind == "linear_cross_entropy")
+    flops = 2 * b * v * d
+    k_ms = per[si]
+    tf = flops / (k_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "kernel": f"linear_cross_entropy step {si}: lce_gemm_kernel + lce_merge_kernel [{b}, {d}]x[{v}, {d}]",
+            "per_launch": {"flops": flops, "bytes": (b + v) * d * 2 + b * 8, "ms": round(k_ms, 4)}}
+    cpu = None
+    if not args.no_cpu:
+        r = 16
+        g = L.make_graph(fn)(L.empty([r, d], "bfloat16", "meta"), L.empty([v, d], "bfloat16", "meta"),
+                             L.empty([r], "int64", "meta"))
+        oracle.set_threads(16)
+        t0 = time.perf_counter()
+        oracle.run(g, [h[:r], w, t[:r]])
+        c = (time.perf_counter() - t0) * b / r
+        oracle.set_threads(1)
+        cpu = {"value": round(c * 1e3, 1), "unit": "ms/call", "cores": 16, "kind": "port",
+               "sample": f"{r} of the {b} rows (the whole w) in the C oracle's unfused loss, scaled by rows"}
+    best = min(ms[True])
+    return _op_line(args, "linear cross entropy eval-loss call ms", best, best, "ms/step",
+                    {"workload": "eval loss mean(cross_entropy(h @ w^T, t)), h [16384, 2048], w [32000, 2048] bf16"},
+                    roof, cpu, "bf16",
+                    {"fused_ms": [round(x, 4) for x in ms[True]], "unfused_ms": [round(x, 4) for x in ms[False]],
+                     "loss": loss[True], "loss_unfused": loss[False]})
+
+
+OP_CONFIGS = {"1": _config1, "2": _config2, "3": _config3, "lce": _config_lce}
 
 
 def _traffic(kernel, config):
