@@ -644,7 +644,10 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
                         (lds_v4i16_t *)(sg + ((krow + 8) * DkdvLds<D>::kStagePitch + col) * 2));
                     const uint2 xa = __builtin_bit_cast(uint2, x), ya = __builtin_bit_cast(uint2, y);
                     const int f = (2 * wave + ksl) * 2 + qb;
-                    *reinterpret_cast<uint4 *>(blk + f * 512 + lane * 8) = make_uint4(xa.x, xa.y, ya.x, ya.y);
+                    // written once and read once by the next kernel, far beyond the caches: nontemporal
+                    typedef unsigned int ntv4 __attribute__((ext_vector_type(4)));
+                    ntv4 v = {xa.x, xa.y, ya.x, ya.y};
+                    __builtin_nontemporal_store(v, reinterpret_cast<ntv4 *>(blk + f * 512 + lane * 8));
                 }
         }
 
@@ -826,7 +829,12 @@ __global__ __launch_bounds__(256, 2) void flash_dq_ds_kernel(AttnParams p) {
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
-            for (int qh = 0; qh < 2; ++qh) fs[B][kk][qh] = *reinterpret_cast<const uint4 *>(src + (2 * kk + qh) * 512);
+            for (int qh = 0; qh < 2; ++qh) {
+                // read once: nontemporal, so the stream of dS does not evict the K rows every query block re-reads
+                typedef unsigned int ntv4 __attribute__((ext_vector_type(4)));
+                const ntv4 v = __builtin_nontemporal_load(reinterpret_cast<const ntv4 *>(src + (2 * kk + qh) * 512));
+                fs[B][kk][qh] = make_uint4(v.x, v.y, v.z, v.w);
+            }
     };
     f32x16_t acc[2][FN];
 #pragma unroll
