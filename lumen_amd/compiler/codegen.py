@@ -51,6 +51,16 @@ typedef __bf16 lk_bf16x2 __attribute__((ext_vector_type(2)));
 DEV uint32_t sb2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((lk_f32x2){a, b}, lk_bf16x2));
 }
+// a vector of 4, 8 or 16 bytes loaded nontemporal: the generated kernels' full-size operands are read once a
+// launch, and keeping their lines would evict what other loads re-read
+template <class T> DEV T ld_nt(const T *p) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)));
+  } else {
+    typedef uint32_t nv __attribute__((ext_vector_type(sizeof(T) / 4)));
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const nv *>(p)));
+  }
+}
 DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
 DEV float r_f16(float f) { return lb_f16(sb_f16(f)); }
@@ -872,7 +882,7 @@ class LoopKernel:
                         lines.append(f"const {STORE_T[dt]} {nm} = in{arg}[{base} + {lane}];")
                 continue
             tmp = em.tmp("V")
-            lines.append(f"const {vt}<{V}> {tmp} = *reinterpret_cast<const {vt}<{V}>*>(in{arg} + {base});")
+            lines.append(f"const {vt}<{V}> {tmp} = ld_nt(reinterpret_cast<const {vt}<{V}>*>(in{arg} + {base}));")
             ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
             for lane, nm in enumerate(names):
                 if nm is not None:
