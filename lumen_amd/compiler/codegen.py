@@ -61,6 +61,15 @@ template <class T> DEV T ld_nt(const T *p) {
     return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const nv *>(p)));
   }
 }
+// a vector stored nontemporal: for values no kernel reads until much later
+template <class T> DEV void st_nt(T *p, const T &v) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, v), reinterpret_cast<uint32_t *>(p));
+  } else {
+    typedef uint32_t nv __attribute__((ext_vector_type(sizeof(T) / 4)));
+    __builtin_nontemporal_store(__builtin_bit_cast(nv, v), reinterpret_cast<nv *>(p));
+  }
+}
 DEV float lb_f16(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
 DEV uint16_t sb_f16(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
 DEV float r_f16(float f) { return lb_f16(sb_f16(f)); }
@@ -778,6 +787,7 @@ class LoopKernel:
         # values whose memory another argument of the kernel shares (an output written over the input it
         # replaces, element for element): their pointers are not declared __restrict__
         self.aliased = aliased
+        self.far = frozenset()  # outputs no kernel reads soon: stored nontemporal
         self.views, self.out_views = views, out_views
         self.args = []  # ("in"|"out", var)
         self.extra_fill = []
@@ -836,7 +846,8 @@ class LoopKernel:
         for k, v in enumerate(st.outputs):
             dt = g.types[v].dtype
             if V > 1 and self.out_views[v].contiguous():
-                stores.append(self._vec_store(f"out{k}", "base", [per_v[l][k] for l in range(V)], dt, V, em))
+                stores.append(self._vec_store(f"out{k}", "base", [per_v[l][k] for l in range(V)], dt, V, em,
+                                              nt=v in self.far))
             else:
                 view = self.out_views[v]
                 for lane in range(V):
@@ -889,7 +900,7 @@ class LoopKernel:
                     lines.append(f"const {STORE_T[dt]} {nm} = __builtin_bit_cast({STORE_T[dt]}, ({ct}){tmp}.e[{lane}]);")
         return lines
 
-    def _vec_store(self, ptr, base, names, dt, V, em=None):
+    def _vec_store(self, ptr, base, names, dt, V, em=None, nt=False):
         esz = D.size_of(dt)
         if em is not None and dt == "bfloat16":
             names = [em.unrounded(n) for n in names]
@@ -902,13 +913,15 @@ class LoopKernel:
             parts = [f"{{ u32v<{V // 2}> {t};"]
             for l in range(0, V, 2):
                 parts.append(f"{t}.e[{l // 2}] = sb2_bf16({names[l]}, {names[l + 1]});")
-            parts.append(f"*reinterpret_cast<u32v<{V // 2}>*>({ptr} + {base}) = {t}; }}")
+            dst = f"reinterpret_cast<u32v<{V // 2}>*>({ptr} + {base})"
+            parts.append(f"st_nt({dst}, {t}); }}" if nt else f"*{dst} = {t}; }}")
             return " ".join(parts)
         ct = "uint16_t" if esz == 2 else ("uint32_t" if esz == 4 else "uint64_t")
         parts = [f"{{ {vt}<{V}> {t};"]
         for l, n in enumerate(names):
             parts.append(f"{t}.e[{l}] = __builtin_bit_cast({ct}, ({STORE_T[dt]}){_store(n, dt)});")
-        parts.append(f"*reinterpret_cast<{vt}<{V}>*>({ptr} + {base}) = {t}; }}")
+        dst = f"reinterpret_cast<{vt}<{V}>*>({ptr} + {base})"
+        parts.append(f"st_nt({dst}, {t}); }}" if nt else f"*{dst} = {t}; }}")
         return " ".join(parts)
 
     # ---- row kernels
@@ -1010,7 +1023,7 @@ class LoopKernel:
                 dt = g.types[v].dtype
                 base = f"(r * {C}LL + ({j} * {T} + tid) * {V})"
                 if V > 1 and self.out_views[v].contiguous():
-                    s = self._vec_store(f"out{oi}", base, [lanes[l][k] for l in range(V)], dt, V, em)
+                    s = self._vec_store(f"out{oi}", base, [lanes[l][k] for l in range(V)], dt, V, em, nt=v in self.far)
                 else:
                     s = " ".join(
                         f"out{oi}[{self._out_addr(self.out_views[v], g.types[v].shape, f'({base} + {l})')}] = "
@@ -1258,6 +1271,7 @@ class GemmEpilogueKernel:
                  variant=0, aliased=frozenset()):
         self.graph, self.dot, self.loop = graph, dot_step, loop_step
         self.aliased = aliased  # as LoopKernel.aliased
+        self.far = frozenset()  # as LoopKernel.far
         self.variant = variant
         self.desc, self.at, self.bt, self.f16, self.store_dot = desc, at, bt, f16, store_dot
         # (value, sum): a float32 loop output summed over the rows into `sum` [n] (atomically, into zeros)
@@ -1295,6 +1309,7 @@ class GemmEpilogueKernel:
         lin = [v for v in loop.inputs if v != dv]
         # the loop's body, evaluated 4 columns at a time at flat index base + lane of the [m, n] result
         lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views, self.aliased)
+        lk.far = self.far
         em = Emitter(g, loop.nodes, {v: (k, self.views[v]) for k, v in enumerate(lin)})
         em.vec = 4
         accs = [f"acc.{c}" for c in "xyzw"]
@@ -1327,7 +1342,7 @@ class GemmEpilogueKernel:
             names = dnames if (self.store_dot and k == 0) else [per_lane[l][k - (1 if self.store_dot else 0)] for l in range(4)]
             view = self.out_views[v]
             if view.contiguous():
-                stores.append(lk._vec_store(f"out{k}", "base", names, dt, 4, em))
+                stores.append(lk._vec_store(f"out{k}", "base", names, dt, 4, em, nt=v in self.far))
             else:
                 for lane in range(4):
                     addr = lk._out_addr(view, g.types[v].shape, f"(base + {lane})")

@@ -647,10 +647,18 @@ class Plan:
         return aliases
 
     # ---- kernels
+    FAR_STEPS = 8  # an output whose first reader runs at least this many steps later is stored nontemporal
+
     def _gen_kernels(self):
         import hashlib
 
         g = self.graph
+        first_read = {}
+        for si, st in enumerate(self.steps):
+            for u in st.inputs:
+                first_read.setdefault(u, si)
+        far = frozenset(v for si, st in enumerate(self.steps) for v in st.outputs
+                        if first_read.get(v, len(self.steps)) - si >= self.FAR_STEPS)
         for si, st in enumerate(self.steps):
             if st.kind == "hloop":
                 parts = []
@@ -658,6 +666,7 @@ class Plan:
                     views = {v: self.loc[v].view() for v in m.inputs}
                     outs = {v: self.loc[v].view() for v in m.outputs}
                     parts.append(codegen.LoopKernel(g, m, "KNAME", views, outs, self.aliased))
+                    parts[-1].far = far
                 k = codegen.HorizontalKernel(parts)
                 body = k.source()
                 name = f"hloop_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
@@ -673,6 +682,7 @@ class Plan:
                 outs = {v: self.loc[v].view() for v in st.outputs}
                 k = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
                                                colsum=getattr(st, "epi_colsum", None), aliased=self.aliased)
+                k.far = far
                 body = k.source()
                 name = f"gemm_epi_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
                 k.name = st.name = name
@@ -687,6 +697,7 @@ class Plan:
                         kv = codegen.GemmEpilogueKernel(g, st, st.epi, d, at, bt, f16, st.store_dot, views, outs,
                                                         colsum=getattr(st, "epi_colsum", None), variant=var,
                                                         aliased=self.aliased)
+                        kv.far = far
                         bv = kv.source()
                         kv.name = f"gemm_epi_{hashlib.sha1(bv.encode()).hexdigest()[:10]}"
                         self.epi_alts.setdefault(si, []).append((var, kv, codegen.HEADER + bv.replace("KNAME", kv.name)))
@@ -702,6 +713,7 @@ class Plan:
             views = {v: self.loc[v].view() for v in st.inputs}
             outs = {v: self.loc[v].view() for v in st.outputs}
             k = codegen.LoopKernel(g, st, "KNAME", views, outs, self.aliased)
+            k.far = far
             body = k.source()
             name = f"{st.kind}_{hashlib.sha1(body.encode()).hexdigest()[:10]}"
             k.name = name

@@ -317,7 +317,7 @@ def test_assigned_weights_of_the_training_step_are_updated_in_place():
 
     checked = 0
     for si, k in p.kernels.items():
-        sig = re.search(r"void\s+\w+\((.*?)\)\s*\{", p.sources[si], re.S).group(1).split(", ")
+        sig = re.search(r"extern \"C\".*?void\s+\w+\((.*?)\)\s*\{", p.sources[si], re.S).group(1).split(", ")
         assert len(sig) == len(k.args), p.sources[si][:300]
         for param, (_, v) in zip(sig, k.args):
             assert ("__restrict__" in param) == (v not in p.aliased), param
