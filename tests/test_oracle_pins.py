@@ -282,3 +282,154 @@ def test_swap_pairs_slice_and_select():
     c = np.array([[True, False] * 4] * 3)
     (se,) = _run(lambda p, v: prims.select(p, v, prims.neg(v)), c, x)
     np.testing.assert_array_equal(se, np.where(c, x, -x))
+
+
+# ---- exp, log, sqrt, tanh at float32 rounding; reduce_max; eq and lt; the identity transfer ops ----------
+# (reference ``lumen/reference/mod.rs:603-612`` evaluates Exp/Log/Sqrt/Tanh in float64 and rounds once;
+# ``:645-717`` folds ReduceMax from the dtype's lowest value with NaN propagation; ``:498-530`` the
+# comparisons; the transfer and wait primitives return their operand unchanged.)
+
+_UNARY_CORE = {
+    "exp": (np.exp, (-80, 80)), "log": (np.log, (1e-30, 1e30)),
+    "sqrt": (np.sqrt, (0.0, 1e6)), "tanh": (np.tanh, (-12, 12)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_UNARY_CORE))
+def test_float32_exp_log_sqrt_tanh_are_float64_rounded_once(name):
+    """float32 results within one ulp of NumPy's float64 function rounded once to float32, and equal to it
+    on at least 99.9% of inputs; ``sqrt`` is correctly rounded in both, so it must match everywhere.
+    ``log`` draws its inputs log-uniformly so every binade from 2^-100 to 2^100 is covered."""
+    ref, (lo, hi) = _UNARY_CORE[name]
+    rng = np.random.default_rng(100 + len(name))
+    if name == "log":
+        x = np.exp(rng.uniform(np.log(lo), np.log(hi), 4000)).astype(np.float32)
+    else:
+        x = rng.uniform(lo, hi, 4000).astype(np.float32)
+    (got,) = _run(getattr(prims, name), x)
+    assert got.dtype == np.float32
+    want = ref(x.astype(np.float64)).astype(np.float32)
+    assert _f32_ulps(got, want).max() <= 1
+    assert (got == want).mean() >= (1.0 if name == "sqrt" else 0.999)
+
+
+def test_bf16_exp_log_sqrt_tanh_round_once_to_bf16():
+    """With bf16 operands the float64 value is rounded once to bf16 (round to nearest even): compared bit
+    for bit with NumPy's float64 function rounded by the reference test's bf16 helper, on every bf16
+    pattern in each function's domain."""
+    pats = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        vals = D.bf16_to_f32(pats).astype(np.float64)
+    for name, ref, keep in [("exp", np.exp, np.abs(vals) < 80), ("log", np.log, vals > 0),
+                            ("sqrt", np.sqrt, vals >= 0), ("tanh", np.tanh, np.isfinite(vals))]:
+        sel = pats[keep & np.isfinite(vals)]
+        (got,) = _run(getattr(prims, name), sel)
+        want = D.bf16_bits(ref(D.bf16_to_f32(sel).astype(np.float64)))
+        assert np.array_equal(got, want), name
+
+
+def test_exp_log_sqrt_tanh_special_values():
+    """The special points each function fixes: exp(±0) = 1, exp(-inf) = 0, log(0) = -inf, log of a
+    negative is NaN, sqrt(-0) = -0, sqrt of a negative is NaN, tanh keeps the sign of zero and saturates
+    to ±1 (in float32 already above 9.01), and NaN propagates through all four."""
+    sp = np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 4.0, -4.0, 20.0], np.float64)
+    with np.errstate(all="ignore"):
+        checks = {
+            "exp": [1.0, 1.0, np.e, 1 / np.e, np.inf, 0.0, np.nan, np.exp(4.0), np.exp(-4.0), np.exp(20.0)],
+            "log": [-np.inf, -np.inf, 0.0, np.nan, np.inf, np.nan, np.nan, np.log(4.0), np.nan, np.log(20.0)],
+            "sqrt": [0.0, -0.0, 1.0, np.nan, np.inf, np.nan, np.nan, 2.0, np.nan, np.sqrt(20.0)],
+            "tanh": [0.0, -0.0, np.tanh(1.0), -np.tanh(1.0), 1.0, -1.0, np.nan, np.tanh(4.0), -np.tanh(4.0), 1.0],
+        }
+    for name, want in checks.items():
+        (got,) = _run(getattr(prims, name), sp)
+        np.testing.assert_allclose(got, want, rtol=1e-15, err_msg=name)
+        assert np.array_equal(np.signbit(got[:2]), np.signbit(np.asarray(want[:2]))), name
+    (t32,) = _run(prims.tanh, np.array([9.2, -9.2, 1e-30, -1e-30], np.float32))
+    np.testing.assert_array_equal(t32, np.array([1.0, -1.0, 1e-30, -1e-30], np.float32))
+    (s32,) = _run(prims.sqrt, np.array([2.0, 1e-40, 3.0e38], np.float32))
+    np.testing.assert_array_equal(s32, np.sqrt(np.array([2.0, 1e-40, 3.0e38], np.float32)))
+
+
+def _reduce_max(x, axes, **kw):
+    return _run(lambda v: prims.reduce_max(v, axes), x, **kw)[0]
+
+
+def test_float_reduce_max_matches_numpy_with_nan_and_negative_rows():
+    """float32/float64 reduce_max equals ``np.max`` over each axis set: all-negative rows (an identity of
+    0 instead of -inf would show), ``-inf``-only rows, a NaN anywhere in a row making the row NaN (NaN
+    after larger values and before them), and ±0 mixes."""
+    rng = np.random.default_rng(21)
+    for dt in (np.float32, np.float64):
+        x = rng.normal(size=(5, 7, 9)).astype(dt)
+        x[0] = -np.abs(x[0]) - 1.0          # all negative
+        x[1, 2] = -np.inf                   # a -inf-only row along the last axis
+        x[2, 3, 0] = np.nan                 # NaN first in its row
+        x[2, 4, 8] = np.nan                 # NaN last in its row
+        x[3, 5] = np.where(np.arange(9) % 2 == 0, -0.0, 0.0).astype(dt)
+        for axes in ([2], [1], [0], [0, 2], [1, 2], [0, 1, 2]):
+            got = _reduce_max(x, axes)
+            want = np.max(x, axis=tuple(axes))
+            assert got.dtype == dt
+            np.testing.assert_array_equal(got, want, err_msg=f"{dt} {axes}")
+        row = _reduce_max(x, [2])
+        assert np.isneginf(row[1, 2]) and np.isnan(row[2, 3]) and np.isnan(row[2, 4])
+        assert (row[0] < 0).all()
+
+
+def test_bf16_reduce_max_and_integer_identities():
+    """bf16 reduce_max is the bf16 pattern of the largest value (NaN propagated); integer reduce_max
+    starts from the type's lowest value (so an all-negative int8/int32/int64 row keeps its maximum) and
+    unsigned types from 0; an empty reduced axis gives that identity."""
+    rng = np.random.default_rng(22)
+    v = rng.normal(size=(6, 33)).astype(np.float32) - 3.0
+    v[4, 10] = np.nan
+    b = D.bf16_bits(v)
+    got = _reduce_max(b, [1])
+    want = D.bf16_bits(np.max(D.bf16_to_f32(b), axis=1))
+    assert np.array_equal(got[np.arange(6) != 4], want[np.arange(6) != 4])
+    assert np.isnan(D.bf16_to_f32(got[4:5]))[0]
+    for dt in (np.int8, np.int32, np.int64, np.uint8, np.uint32):
+        info = np.iinfo(dt)
+        x = rng.integers(info.min, info.max, size=(4, 17), endpoint=True, dtype=dt)
+        if info.min < 0:
+            x[1] = rng.integers(info.min, 0, size=17, dtype=dt)
+            x[2] = info.min
+        got = _reduce_max(x, [1])
+        np.testing.assert_array_equal(got, np.max(x, axis=1), err_msg=str(dt))
+        (empty,) = _run(lambda t: prims.reduce_max(t, [1]), np.zeros((3, 0), dt))
+        np.testing.assert_array_equal(empty, np.full(3, info.min, dt), err_msg=str(dt))
+    (fempty,) = _run(lambda t: prims.reduce_max(t, [0]), np.zeros((0, 2), np.float32))
+    np.testing.assert_array_equal(fempty, np.full(2, -np.inf, np.float32))
+
+
+def test_eq_and_lt_follow_ieee_and_integer_order():
+    """eq and lt give bool: NaN compares unequal and unordered (even to itself), -0 == +0 and not
+    -0 < +0, infinities order at the ends; integer comparisons use the full width (no wrap in a
+    difference), including unsigned values above the signed range."""
+    a = np.array([np.nan, np.nan, -0.0, 0.0, -np.inf, 1.0, 2.0, np.inf, 3.0], np.float32)
+    b = np.array([np.nan, 1.0, 0.0, -0.0, np.inf, 1.0, 1.0, np.inf, np.nan], np.float32)
+    (e,) = _run(prims.eq, a, b)
+    (l,) = _run(prims.lt, a, b)
+    assert e.dtype == np.bool_ and l.dtype == np.bool_
+    np.testing.assert_array_equal(e, a == b)
+    np.testing.assert_array_equal(l, a < b)
+    for dt in (np.int8, np.int64, np.uint32, np.uint64):
+        info = np.iinfo(dt)
+        x = np.array([info.min, info.max, 0, info.max, info.min], dt)
+        y = np.array([info.max, info.min, 0, info.max - 1, info.min], dt)
+        (e,) = _run(prims.eq, x, y)
+        (l,) = _run(prims.lt, x, y)
+        np.testing.assert_array_equal(e, x == y, err_msg=str(dt))
+        np.testing.assert_array_equal(l, x < y, err_msg=str(dt))
+
+
+@pytest.mark.parametrize("name", ["to_host", "to_device", "host_wait", "device_wait"])
+def test_transfer_and_wait_primitives_return_their_operand(name):
+    """The transfer and wait primitives are the identity on values (only placement or ordering changes):
+    float NaN payloads, -0 and bf16 patterns pass through bit for bit."""
+    x = np.array([[np.nan, -0.0, 1.5], [np.inf, -3.25, 1e-40]], np.float32)
+    (got,) = _run(lambda t: prims.bind(name, t), x)
+    assert np.array_equal(got.view(np.uint32), x.view(np.uint32))
+    b = np.array([0x7FC1, 0x8000, 0x3F80, 0xFF80], np.uint16)
+    (gb,) = _run(lambda t: prims.bind(name, t), b)
+    assert np.array_equal(gb, b)
