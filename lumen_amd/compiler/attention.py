@@ -502,7 +502,7 @@ def lower(plan, step):
     a.config = getattr(step, "config", -1) if p["name"] == FWD else -1  # the forward's tile (autotuned or forced)
     from lumen_amd.config import config
 
-    a.deterministic = backward_mode()
+    a.deterministic = backward_mode() if step.mode is None else step.mode
     if p["name"] == FWD:
         q, k, v = n.inputs
         (qb, qs, qd), (kb, ks, kd), (vb, vs, vd) = p["q_dims"], p["k_dims"], p["v_dims"]
@@ -554,24 +554,40 @@ def _need_unit(*pairs):
 _ = (Node, TensorType)
 
 
-def backward_mode() -> int:
+def backward_mode(batch=0, heads=0, sq=0, sk=0) -> int:
     """The flash backward's dQ mode (nhip_attn_desc.deterministic): 0 added atomically by the dK/dV kernel,
-    1 from the dS tiles the dK/dV kernel stores, 2 by a kernel recomputing S and dP."""
+    1 from the dS tiles the dK/dV kernel stores, 2 by a kernel recomputing S and dP.
+
+    Mode 1's dS tiles grow with Sq x Sk (2 GiB an attention at B 4, N 16, S 4096), so a shape whose tiles
+    would exceed ``config.compiler.attention_ds_max_bytes`` (or an eighth of a set ``memory_limit``) takes
+    mode 2, whose workspace is two floats a query row, as the reference's recomputing backward is."""
     from lumen_amd.config import config
 
     if not config.compiler.deterministic:
         return 0
-    return 1 if config.compiler.attention_store_ds else 2
+    if not config.compiler.attention_store_ds:
+        return 2
+    cap = config.compiler.attention_ds_max_bytes
+    if config.compiler.memory_limit:
+        cap = min(cap, config.compiler.memory_limit // 8)
+    return 2 if ds_bytes(batch, heads, sq, sk) > cap else 1
 
 
-def backward_workspace_bytes(b, nh, sq, sk, hd, mode) -> int:
-    """Workspace bytes of nhip_flash_bwd (its nhip_flash_bwd_workspace): delta and the base-2 LSE (two floats
-    a query row), then 256-byte aligned the float32 dQ accumulator (mode 0) or the 16-bit dS tiles, 128 keys x
-    64 queries each (mode 1)."""
-    rows = 2 * b * nh * sq * 4
-    if mode == 2:
-        return rows
-    base = -(-rows // 256) * 256
-    if mode == 1:
-        return base + b * nh * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2
-    return base + b * nh * sq * hd * 4
+def ds_bytes(batch, heads, sq, sk) -> int:
+    """Bytes of mode 1's 16-bit dS tiles, 128 keys x 64 queries each (attention.h flash_bwd_ds_bytes)."""
+    return batch * heads * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2
+
+
+def backward_workspace_bytes(b, nh, sq, sk, hd, kvh, mode) -> int:
+    """Workspace bytes of nhip_flash_bwd for these sizes and mode, as the library itself reports them
+    (nhip_flash_bwd_workspace), so the plan's scratch can never be smaller than what the kernels write."""
+    import ctypes as C
+
+    from lumen_amd import native as nv
+
+    a = nv.AttnDesc()
+    a.batch, a.sq, a.sk, a.heads, a.kv_heads, a.head_dim = b, sq, sk, nh, kvh, hd
+    a.deterministic = mode
+    n = C.c_size_t()
+    nv.call("nhip_flash_bwd_workspace", C.byref(a), C.byref(n))
+    return n.value

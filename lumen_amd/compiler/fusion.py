@@ -41,6 +41,7 @@ class Step:
     rows: tuple | None = None       # (R, C) of a row kernel
     name: str = ""
     scratch: int = 0                # bytes of workspace the step needs while it runs
+    mode: int | None = None         # flash_bwd: the dQ mode (nhip_attn_desc.deterministic)
 
     def label(self):
         return " → ".join(n.prim for n in self.nodes[:6]) + (" → …" if len(self.nodes) > 6 else "")
@@ -270,8 +271,9 @@ def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
                     from lumen_amd.compiler.attention import backward_mode, backward_workspace_bytes
 
                     b, sq, nh, hd = q.shape
-                    sk = graph.types[node.inputs[1]].shape[1]
-                    st.scratch = backward_workspace_bytes(b, nh, sq, sk, hd, backward_mode())
+                    sk, kvh = graph.types[node.inputs[1]].shape[1:3]
+                    st.mode = backward_mode(b, nh, sq, sk)
+                    st.scratch = backward_workspace_bytes(b, nh, sq, sk, hd, kvh, st.mode)
                 elif len(outs) == 1:
                     st.scratch = graph.types[outs[0]].numel() // graph.types[outs[0]].shape[-1] * 4
         elif kinds[k] in ("view", "reduce"):

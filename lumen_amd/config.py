@@ -21,6 +21,9 @@ class CompilerFlags:
     # deterministic attention backward: the dK/dV kernel stores dS (16-bit, B x N x Sk x Sq / 2 bytes causal) and
     # dQ = dS K reads it back, instead of a second kernel recomputing S and dP (off: no dS workspace)
     attention_store_ds: bool = True
+    # above this many bytes of dS tiles for one attention the deterministic backward recomputes S and dP
+    # instead (its workspace is O(Sq)), so long sequences do not need O(Sq x Sk) memory
+    attention_ds_max_bytes: int = 4 << 30
     hip_graphs: bool = True           # replay a plan's calls as a captured HIP graph (from its third call)
     # a weight the compiled function assigns is computed over its old value where the step producing it reads
     # the old value only at the element it writes and nothing reads it later (off: into the workspace, then

@@ -350,3 +350,50 @@ def test_updates_stay_out_of_place_when_their_input_is_read_elsewhere():
 
     p = _donated(needed, [sq, sq], {0: 0})  # w is read with a result of the update: it cannot move
     assert p.in_place_outputs == {}
+
+
+def _flash_bwd_steps(b, s, n, d, kvh=None):
+    kvh = kvh or n
+    metas = [((b, s, n, d), "bfloat16"), ((b, s, kvh, d), "bfloat16"), ((b, s, kvh, d), "bfloat16"),
+             ((b, s, n, d), "bfloat16")]
+
+    def loss(q, k, v, w):
+        return F.sum((F.flash_attention(q, k, v, is_causal=True) * w).float())
+
+    p = _plan(L.grad(loss, (0, 1, 2)), *metas)
+    return [st for st in p.steps if st.kind == "flash_bwd"]
+
+
+def test_long_sequences_take_the_recomputing_backward_with_o_s_scratch():
+    """The deterministic flash backward stores dS (O(Sq x Sk) bytes) only while that fits
+    ``attention_ds_max_bytes``; a longer sequence takes the recomputing mode, whose scratch is two floats a
+    query row, so the plan's memory grows linearly with the sequence as the reference's backward does."""
+    from lumen_amd.compiler import attention as A
+    from lumen_amd.config import config
+
+    (short,) = _flash_bwd_steps(1, 1024, 2, 64)
+    assert short.mode == 1 and short.scratch >= A.ds_bytes(1, 2, 1024, 1024)
+    with config.compiler.patch(attention_ds_max_bytes=1 << 20):
+        (long_,) = _flash_bwd_steps(1, 1024, 2, 64)
+        assert long_.mode == 2 and long_.scratch == 2 * 1 * 2 * 1024 * 4
+        (longer,) = _flash_bwd_steps(1, 4096, 2, 64)
+        assert longer.mode == 2 and longer.scratch == 4 * long_.scratch
+    with config.compiler.patch(memory_limit=8 * A.ds_bytes(1, 2, 1024, 1024) - 1):
+        (limited,) = _flash_bwd_steps(1, 1024, 2, 64)
+        assert limited.mode == 2
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1, 64), (2, 3, 200, 333, 128), (1, 4, 4097, 129, 64), (3, 2, 64, 1, 96)])
+def test_flash_backward_scratch_is_what_the_library_reports(mode, shape):
+    """The plan sizes a flash backward's scratch by asking the library (nhip_flash_bwd_workspace); checked
+    against the layout the kernels write — delta and the LSE (two floats a query row), then, 256-byte
+    aligned, the float32 dQ accumulator (mode 0) or 128 x 64 tiles of 16-bit dS (mode 1) — on ragged shapes."""
+    from lumen_amd.compiler import attention as A
+
+    b, n, sq, sk, d = shape
+    rows = 2 * b * n * sq * 4
+    want = {2: rows,
+            1: -(-rows // 256) * 256 + b * n * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2,
+            0: -(-rows // 256) * 256 + b * n * sq * d * 4}[mode]
+    assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode) == want

@@ -83,3 +83,14 @@ def test_module_weights_and_written_outputs():
     kinds = [k for k, _ in t.layout]
     assert kinds == ["arg", "scalar", "weight"]
     assert t.written == [0] and len(t.graph.outputs) == 2
+
+
+def test_to_with_an_unknown_device_string_names_the_device():
+    """``t.to("cuda")`` on a traced tensor raises the unknown-device error (this backend's GPU is ``hip``),
+    not a dtype error; known devices and dtype names still work."""
+    import pytest
+
+    with pytest.raises(ValueError, match="unknown device 'cuda'"):
+        L.make_graph(lambda x: x.to("cuda"))(L.empty([2], "float32", "meta"))
+    g = L.make_graph(lambda x: x.to("hip:0").to("bfloat16"))(L.empty([2], "float32", "meta"))
+    assert [n.prim for n in g.nodes] == ["cast"]
