@@ -27,29 +27,23 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
-def cpu_baseline(cfg, seq=None, threads=None):
-    """The CPU oracle (the C restatement of lumen/reference/mod.rs) timed on a bounded sample of the workload:
-    one whole training step (forward, autograd backward, SGD update) of a one-layer model at the config's
-    widths (d, heads, FFN, vocab) on one sequence of ``seq`` tokens, scaled to the configured step by
-    algorithmic FLOPs (the step is dot-dominated). Its dots fold each output row in the reference's
-    sequential k order, rows split over ``threads`` host threads."""
+def _oracle_step_seconds(cfg, seq, threads):
+    """Seconds the CPU oracle takes for one whole training step (forward, autograd backward, SGD update) of a
+    one-layer model at the config's widths on one sequence of ``seq`` tokens, and that sample's FLOPs."""
     import dataclasses
 
     import numpy as np
 
+    import lumen_amd as L
     from lumen_amd import workloads as W
     from lumen_amd.graph.trace import trace
     from oracle import oracle
 
-    threads = threads or min(16, os.cpu_count() or 1)
-    seq = seq or min(cfg.seq, 256)
     sample = dataclasses.replace(cfg, batch=1, layers=1, seq=seq)
     model, opt = W.build(sample, lr=1e-2)
     weights = W.init_weights(model)
     W.load(model, weights)
     ids, targets = W.batch(sample)
-    import lumen_amd as L
-
     args = (model, opt, L.from_numpy(ids), L.from_numpy(targets))
     traced = trace(W.train_step, args)
     names = {id(p): n for n, p in model.named_parameters()}
@@ -62,20 +56,47 @@ def cpu_baseline(cfg, seq=None, threads=None):
         else:
             ins.append(weights[names[id(traced.weights[k])]])
     oracle.set_threads(threads)
-    t = time.perf_counter()
-    oracle.run(traced.graph, ins)
-    total = time.perf_counter() - t
-    oracle.set_threads(1)
-    rate = sample.step_flops() / total
+    try:
+        t = time.perf_counter()
+        oracle.run(traced.graph, ins)
+        return time.perf_counter() - t, sample.step_flops()
+    finally:
+        oracle.set_threads(1)
+
+
+def cpu_baseline(cfg, seq=None, threads=None):
+    """The CPU oracle (the C restatement of lumen/reference/mod.rs, which evaluates a graph single-threaded)
+    timed on a bounded sample of the workload: one whole training step of a one-layer model at the config's
+    widths (d, heads, FFN, vocab) on one short sequence, scaled to the configured step by algorithmic FLOPs.
+    ``value`` is one thread of the host's cores, as the reference runs; a multi-threaded run of the same
+    sample (dots' output rows over ``threads`` threads, the reference's sequential k fold kept) is reported
+    beside it as ``multi_thread``."""
+    nproc = os.cpu_count() or 1
+    threads = threads or min(16, nproc)
+    seq = seq or min(cfg.seq, 32)
+    t1, f1 = _oracle_step_seconds(cfg, seq, 1)
+    tn, fn = _oracle_step_seconds(cfg, min(cfg.seq, 8 * seq), threads)
+    r1, rn = f1 / t1, fn / tn
+
+    def scaled(rate):
+        return round(cfg.step_flops() / rate * 1e3, 1)
+
     return {
-        "value": round(cfg.step_flops() / rate * 1e3, 1),
+        "value": scaled(r1),
         "unit": "ms/step",
-        "cores": threads,
+        "cores": 1,
+        "host_cores": nproc,
         "kind": "port",
-        "sample": f"oracle (C restatement of lumen/reference/mod.rs, dots' output rows over {threads} threads) on one "
+        "sample": f"oracle (C restatement of lumen/reference/mod.rs) on 1 thread of {nproc} host cores (nproc): one "
         f"whole train step of 1 layer at d={cfg.dim}, ffn={cfg.ffn}, vocab={cfg.vocab}, batch 1 x seq {seq} "
-        f"({sample.step_flops() / 1e9:.1f} GFLOP in {total:.2f} s, {rate / 1e9:.2f} GFLOP/s), scaled by FLOPs to "
-        f"the {cfg.step_flops() / 1e12:.1f} TFLOP step; nproc={os.cpu_count()}",
+        f"({f1 / 1e9:.1f} GFLOP in {t1:.2f} s, {r1 / 1e9:.2f} GFLOP/s), scaled by FLOPs to the "
+        f"{cfg.step_flops() / 1e12:.1f} TFLOP step; the short sequence makes attention a smaller share of the "
+        f"sample's FLOPs than of the step's (the rate is dot-dominated either way)",
+        "multi_thread": {
+            "value": scaled(rn), "unit": "ms/step", "cores": threads,
+            "sample": f"the same at seq {min(cfg.seq, 8 * seq)}, dots' output rows over {threads} threads "
+            f"({fn / 1e9:.1f} GFLOP in {tn:.2f} s, {rn / 1e9:.2f} GFLOP/s)",
+        },
     }
 
 
@@ -540,13 +561,12 @@ def _config_lce(args):
         r = 16
         g = L.make_graph(fn)(L.empty([r, d], "bfloat16", "meta"), L.empty([v, d], "bfloat16", "meta"),
                              L.empty([r], "int64", "meta"))
-        oracle.set_threads(16)
         t0 = time.perf_counter()
         oracle.run(g, [h[:r], w, t[:r]])
         c = (time.perf_counter() - t0) * b / r
-        oracle.set_threads(1)
-        cpu = {"value": round(c * 1e3, 1), "unit": "ms/call", "cores": 16, "kind": "port",
-               "sample": f"{r} of the {b} rows (the whole w) in the C oracle's unfused loss, scaled by rows"}
+        cpu = {"value": round(c * 1e3, 1), "unit": "ms/call", "cores": 1, "host_cores": os.cpu_count(),
+               "kind": "port",
+               "sample": f"{r} of the {b} rows (the whole w) in the C oracle's unfused loss (1 thread), scaled by rows"}
     best = min(ms[True])
     return _op_line(args, "linear cross entropy eval-loss call ms", best, best, "ms/step",
                     {"workload": "eval loss mean(cross_entropy(h @ w^T, t)), h [16384, 2048], w [32000, 2048] bf16"},
