@@ -195,3 +195,61 @@ def test_forced_configs_reach_the_plan(hip):
     assert [getattr(s, "config", None) for s in steps if s.kind == "flash_fwd"] == [2]
     assert [getattr(s, "config", None) for s in steps if s.kind == "dot"] == [3]
     np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-2 * np.abs(want).max())
+
+
+def _attention_f64(q, k, v, g, scale, causal):
+    """Float64 attention of one (batch, head) slice, [S, D] operands: the output, the natural-log LSE and the
+    FlashAttention-2 gradients dQ, dK, dV of <O, g> (brute force on the whole score matrix)."""
+    s = (q @ k.T) * scale
+    if causal:
+        s = np.where(np.tril(np.ones(s.shape, bool), s.shape[1] - s.shape[0]), s, -np.inf)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    l_ = e.sum(-1, keepdims=True)
+    p = e / l_
+    o = p @ v
+    dv = p.T @ g
+    dp = g @ v.T
+    ds = p * (dp - (g * o).sum(-1, keepdims=True))
+    return o, (m + np.log(l_))[:, 0], ds @ k * scale, ds.T @ q * scale, dv
+
+
+@pytest.mark.parametrize("deterministic", [1, 0])
+def test_config3_full_size_slices_match_float64_attention(hip, deterministic):
+    """Config 3 at its real size, [8, 2048, 16, 128] causal with independent N(0, 1) q, k, v and dO: the
+    whole forward and backward run on the GPU; three (batch, head) slices of O and the LSE, and the dQ, dK,
+    dV of two of them, are compared with float64 attention computed here from the same bf16 inputs (bf16
+    tolerance: rtol 2e-2 plus 1e-2 of the slice's largest magnitude; LSE within 1e-3)."""
+    b, s, n, d = 8, 2048, 16, 128
+    rng = np.random.default_rng(33)
+    q, k, v, g = (D.bf16_bits(rng.standard_normal((b, s, n, d), np.float32)) for _ in range(4))
+    scale = 1.0 / math.sqrt(d)
+    desc = attn_desc(b, s, s, n, n, d, True, scale, deterministic=deterministic)
+    dq_, dk_, dv_, dg = Dev(q), Dev(k), Dev(v), Dev(g)
+    o, lse = Dev(nbytes=q.nbytes), Dev(nbytes=b * n * s * 4)
+    print("config3 full size fwd", flush=True)
+    nv.call("nhip_flash_fwd", C.byref(desc), dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr)
+    ws_bytes = C.c_size_t()
+    nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
+    ws = Dev(nbytes=ws_bytes.value)
+    gq, gk, gv = Dev(nbytes=q.nbytes), Dev(nbytes=k.nbytes), Dev(nbytes=v.nbytes)
+    print("config3 full size bwd mode", deterministic, flush=True)
+    nv.call("nhip_flash_bwd", C.byref(desc), dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, dg.ptr, lse.ptr, gq.ptr, gk.ptr,
+            gv.ptr, ws.ptr)
+    got_o = D.bf16_to_f32(o.get(q.shape, np.uint16))
+    got_lse = lse.get((b, n, s), np.float32)
+    got_g = [D.bf16_to_f32(t.get(q.shape, np.uint16)) for t in (gq, gk, gv)]
+    assert all(np.isfinite(x).all() for x in [got_o] + got_g)
+    f = [D.bf16_to_f32(x).astype(np.float64) for x in (q, k, v, g)]
+    for i, (bi, ni) in enumerate([(0, 0), (3, 7), (7, 15)]):
+        sl = [x[bi, :, ni, :] for x in f]
+        o64, lse64, dq64, dk64, dv64 = _attention_f64(*sl, scale, True)
+
+        def close(a, w, what):
+            np.testing.assert_allclose(a, w, rtol=2e-2, atol=1e-2 * np.abs(w).max(), err_msg=f"{what} b{bi} n{ni}")
+
+        close(got_o[bi, :, ni, :], o64, "o")
+        np.testing.assert_allclose(got_lse[bi, ni], lse64, rtol=1e-4, atol=1e-3)
+        if i < 2:
+            for name, a, w in zip(("dq", "dk", "dv"), got_g, (dq64, dk64, dv64)):
+                close(a[bi, :, ni, :], w, name)
