@@ -182,6 +182,29 @@ def _dims_of_dot(n, side, ty):
     return tuple(b), tuple(f), tuple(c)
 
 
+def _unexpand(G, v, batch_dims):
+    """``(x, nodes)`` if ``v`` is grouped-query attention's head expansion of ``x`` [B, S, Nkv, H]
+    (``expand_heads``: reshape to [B, S, Nkv, 1, H], broadcast to [B, S, Nkv, G, H], reshape to
+    [B, S, Nkv G, H], so head n reads key/value head n / G) and a dot reads ``v`` with batch dims
+    ``batch_dims`` = (0, 2); else ``(v, [])``. The kernels take ``x`` itself and the head ratio."""
+    r2 = G.node(v, "reshape")
+    bc = r2 and G.node(r2.inputs[0], "broadcast_in_dim")
+    r1 = bc and G.node(bc.inputs[0], "reshape")
+    if r1 is None or tuple(batch_dims) != (0, 2):
+        return v, []
+    x = r1.inputs[0]
+    xt = G.g.types[x]
+    if len(xt.shape) != 4:
+        return v, []
+    b, s, nkv, h = xt.shape
+    t1, t2, t3 = (G.g.types[n.output].shape for n in (r1, bc, r2))
+    grp = t2[3] if len(t2) == 5 else 0
+    if (t1 != (b, s, nkv, 1, h) or len(t2) != 5 or t2 != (b, s, nkv, grp, h) or t3 != (b, s, nkv * grp, h)
+            or tuple(bc.params["broadcast_dimensions"]) != (0, 1, 2, 3, 4)):
+        return v, []
+    return x, [r1, bc, r2]
+
+
 def match_forward(g: Graph):
     """Each forward attention of ``g``: a dict of its nodes, operands, scale and mask."""
     G = _G(g)
@@ -239,9 +262,14 @@ def match_forward(g: Graph):
             continue
         if vt.shape[vf[0]] != qt.shape[qc[0]]:
             continue
+        # grouped heads: the kernel reads the key/value heads themselves (head n reads head n / G)
+        k_in, k_exp = _unexpand(G, d1.inputs[1], kb)
+        v_in, v_exp = _unexpand(G, d2.inputs[1], vb)
+        if bool(k_exp) != bool(v_exp) or (k_exp and g.types[k_in].shape[2] != g.types[v_in].shape[2]):
+            k_in, v_in, k_exp, v_exp = d1.inputs[1], d2.inputs[1], [], []
         # value nodes of the body (constants and mask math are copied)
-        core = [d1, mul, *mask_nodes, rm[0], G.node(rm[1]), G.node(sub.inputs[1]), sub, exp, rs[0], G.node(rs[1]),
-                G.node(div.inputs[1]), div, cast, d2]
+        core = [*k_exp, *v_exp, d1, mul, *mask_nodes, rm[0], G.node(rm[1]), G.node(sub.inputs[1]), sub, exp, rs[0],
+                G.node(rs[1]), G.node(div.inputs[1]), div, cast, d2]
         # the log-sum-exp read by a backward: add(reshape(max), log(reshape(sum)))
         lse = None
         for u in G.users.get(rs[1], []):
@@ -251,9 +279,10 @@ def match_forward(g: Graph):
                         lse = (u, a)
         if lse:
             core += list(lse)
-        found.append(dict(core=core, d1=d1, d2=d2, q=d1.inputs[0], k=d1.inputs[1], v=d2.inputs[1], scale=scale,
+        found.append(dict(core=core, d1=d1, d2=d2, q=d1.inputs[0], k=k_in, v=v_in, scale=scale,
                           causal=causal, lse=lse[1].output if lse else None, q_dims=(qb, qf[0], qc[0]),
-                          k_dims=(kb, kf[0], kc[0]), v_dims=(vb, vc[0], vf[0]), mask_pred=pred))
+                          k_dims=(kb, kf[0], kc[0]), v_dims=(vb, vc[0], vf[0]), mask_pred=pred,
+                          shared={n.output for n in k_exp + v_exp}))
     return found
 
 
@@ -330,6 +359,14 @@ def match_backward(g: Graph):
             continue
         if any(tuple(x.params["rhs_batch"]) != (0, 2) for x in (dv, dk, dq)):
             continue
+        # grouped heads: K and V expanded to every query head, dK and dV summed over each group
+        k_in, k_exp = _unexpand(G, k, dst_dot.params["lhs_batch"])
+        v_in, v_exp = _unexpand(G, v, dpt.params["lhs_batch"])
+        if bool(k_exp) != bool(v_exp):
+            continue
+        grouped = bool(k_exp)
+        if grouped and g.types[k_in].shape[2] != g.types[v_in].shape[2]:
+            continue
         sq_, sk_ = g.types[pt].shape[3], g.types[pt].shape[2]
         # the mask here is over [Sk, Sq]: evaluate transposed
         causal = _causal_t(G, pred, sk_, sq_)
@@ -343,18 +380,27 @@ def match_backward(g: Graph):
             if len(us) != 1 or us[0].prim != "transpose" or tuple(us[0].params["permutation"]) != (0, 2, 1, 3):
                 ok = False
                 break
-            us2 = G.users.get(us[0].output, [])
+            hops = [us[0]]
+            if grouped and x is not dq:  # reshape [B, Sk, Nkv, G, D], sum over the group axis
+                r = G.users.get(us[0].output, [])
+                red = len(r) == 1 and r[0].prim == "reshape" and G.users.get(r[0].output, [])
+                if not (red and len(red) == 1 and red[0].prim == "reduce_sum" and tuple(red[0].params["axes"]) == (3,)
+                        and g.types[r[0].output].shape[:3] == g.types[k_in].shape[:3]):
+                    ok = False
+                    break
+                hops += [r[0], red[0]]
+            us2 = G.users.get(hops[-1].output, [])
             if len(us2) != 1 or us2[0].prim != "cast" or g.types[us2[0].output].dtype != qt.dtype:
                 ok = False
                 break
             outs.append(us2[0].output)
-            tail += [us[0], us2[0]]
+            tail += hops + [us2[0]]
         if not ok:
             continue
-        core = [dst_dot, mul_s, *mask_nodes, r_l, b_l, sub, pt_exp, ddot, td, rd, bd, dpt, sub_d, mul_p, mul_sc, c_ds,
-                c_pt, dv, dk, dq] + tail
-        found.append(dict(core=core, q=q, k=k, v=v, o=o, do=do, lse=lse, scale=scale, causal=causal, outs=outs,
-                          mask_pred=pred))
+        core = [*k_exp, *v_exp, dst_dot, mul_s, *mask_nodes, r_l, b_l, sub, pt_exp, ddot, td, rd, bd, dpt, sub_d, mul_p,
+                mul_sc, c_ds, c_pt, dv, dk, dq] + tail
+        found.append(dict(core=core, q=q, k=k_in, v=v_in, o=o, do=do, lse=lse, scale=scale, causal=causal, outs=outs,
+                          mask_pred=pred, shared={n.output for n in k_exp + v_exp}))
     return found
 
 
@@ -430,9 +476,10 @@ def match(graph: Graph) -> Graph:
                 continue
             inner = {n.output for n in nodes}
             # interior values must not escape but through the outputs
+            # (the head expansion of grouped K and V is a layout of an input: it stays for other readers too)
             escapes = any(
                 u.output not in inner for n in nodes if n.output not in outputs and n.prim not in ("full", "iota")
-                and not _is_index(G, n.output) for u in G.users.get(n.output, [])
+                and not _is_index(G, n.output) and n.output not in m["shared"] for u in G.users.get(n.output, [])
             )
             if escapes:
                 continue

@@ -79,6 +79,27 @@ def test_flash_attention_match_preserves_values(causal):
     _same(g, m)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_grouped_query_attention_matches_with_the_key_value_heads_as_operands(causal):
+    """Grouped heads (4 query heads over 2 key/value heads): the forward and the backward (dK and dV summed
+    over each group) both become flash fusions whose K and V operands are the [B, S, 2, D] tensors
+    themselves, not their expansion to every query head; the values are unchanged (oracle on both graphs)."""
+    def grads(q, k, v, do):
+        out, pull = L.vjp(lambda q, k, v: F.flash_attention(q, k, v, is_causal=causal), q, k, v)
+        return (out,) + pull(do)
+
+    metas = [L.empty(s, "bfloat16", "meta") for s in ([1, 40, 4, 64], [1, 40, 2, 64], [1, 40, 2, 64], [1, 40, 4, 64])]
+    g = L.make_graph(grads)(*metas)
+    m = attention.match(passes.frontend(g))
+    fus = [n for n in m.nodes if n.prim == "fusion"]
+    assert [n.params["name"] for n in fus] == ["flash_attention", "flash_attention_backward"]
+    for f in fus:
+        assert [tuple(m.types[u].shape) for u in f.inputs[1:3]] == [(1, 40, 2, 64)] * 2
+    assert [tuple(m.types[v].shape) for v in m.outputs] == [(1, 40, 4, 64), (1, 40, 4, 64), (1, 40, 2, 64),
+                                                            (1, 40, 2, 64)]
+    _same(g, m)
+
+
 def test_written_attention_matches():
     """Attention written as matmul -> scale -> causal mask -> softmax -> matmul is recognized too."""
 
