@@ -1263,9 +1263,10 @@ class GemmEpilogueKernel:
     (mn-contiguous operands), as nhip_gemm takes them."""
 
 
-    # The k loops a generated epilogue kernel can instantiate: (k tile, cross-tile fragment prefetch). Variant 0
-    # is gemm_stream's config 7 body; variant 1 its config 11 body (k tile 32, four stages, buffer loads only).
-    VARIANTS = ((64, False), (32, True))
+    # The k loops a generated epilogue kernel can instantiate: (k tile, gemm_stream_tile's k loop KL). Variant 0
+    # is gemm_stream's config 7 body; variant 1 its config 11 body (k tile 32, four stages, cross-tile fragment
+    # prefetch, buffer loads only); variant 2 its config 12 body (k tile 32, four stages, ping-pong waves).
+    VARIANTS = ((64, 0), (32, 1), (32, 2))
 
     def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None,
                  variant=0, aliased=frozenset()):
@@ -1286,9 +1287,10 @@ class GemmEpilogueKernel:
         self.args = []
 
     def variant_ok(self, variant):
-        """Whether k loop ``variant`` can run this dot (its k tile divides k; XPF needs the buffer-load path)."""
-        bk, xpf = self.VARIANTS[variant]
-        return self.desc.k % bk == 0 and (not xpf or self.buffer_ok())
+        """Whether k loop ``variant`` can run this dot (its k tile divides k; the cross-tile prefetch needs the
+        buffer-load path)."""
+        bk, kl = self.VARIANTS[variant]
+        return self.desc.k % bk == 0 and (kl != 1 or self.buffer_ok())
 
     def buffer_ok(self):
         """gemm.h's stream_buffer_ok: the operand bytes a 256 x 256 tile spans fit 32-bit buffer offsets."""
@@ -1378,7 +1380,7 @@ class GemmEpilogueKernel:
                 pre_uses.append(f"const {m.group(1)} {m.group(2)} = pre.{m.group(2)};")
             else:
                 rest.append(l)
-        bk, xpf = self.VARIANTS[self.variant]
+        bk, kl = self.VARIANTS[self.variant]
         if not self.variant_ok(self.variant):
             raise Unfusable(dv, f"GEMM epilogue k loop variant {self.variant} does not fit k = {d.k}")
         # chunks read ahead at a time: at most 64 VGPRs of 16-byte loads
@@ -1410,7 +1412,7 @@ class GemmEpilogueKernel:
             f"  {shape}",
             f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, {bk}, 4, {'true' if self.at else 'false'}, "
             f"{'true' if self.bt else 'false'}, {'true' if self.buffer_ok() else 'false'}, EpiKNAME, 256, "
-            f"{'true' if xpf else 'false'}>(s, a, b, EpiKNAME{{{init}}}, smem);",
+            f"{kl}>(s, a, b, EpiKNAME{{{init}}}, smem);",
             "}",
         ]
         return "\n".join(lines)

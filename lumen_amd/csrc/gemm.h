@@ -434,9 +434,9 @@ __device__ __forceinline__ void stage_acc(const f32x16_t (&acc)[FM][FN], int hal
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
 // functor called as out(row, col, float4, pre) with the float32 sums of four consecutive columns (col a
 // multiple of 4, within m x n) and pre = out.load(row, col), its other operands read ahead. `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
-// XPF (three or more stages, buffer loads): the k loop reads the next k tile's first fragments during the last
-// k step of the current one instead of after a barrier at the top of each tile.
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256, bool XPF = false>
+// KL, the k loop: 0 fragments of the next k step read under the current step's MFMAs; 1 (XPF) that read also
+// across k tiles; 2 (ping-pong) the two waves of each SIMD alternate between a memory phase and an MFMA phase.
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256, int KL = 0>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
     constexpr int NW = 2 * WN;       // wavefronts (2 x WN)
@@ -554,7 +554,59 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    if constexpr (XPF) {
+    constexpr bool XPF = KL == 1;
+    if constexpr (KL == 2) {
+        // Ping-pong: waves w and w + 4 share a SIMD (wm = 0 and 1). Each wave alternates a memory phase --
+        // issue its loads of tile kt + STAGES - 1 into the stage tile kt - 1 left, read all of tile kt's MFMA
+        // fragments into registers, wait for them and for its own loads of tile kt + 1 -- and an MFMA phase --
+        // the tile's FM x FN x BK / 16 MFMAs at raised wave priority -- with one workgroup barrier between
+        // phases. The wm = 1 waves run one phase behind, so in every phase one wave of each SIMD feeds its
+        // MFMA pipe while the other loads. Stage reuse: tile kt - 1 was last read in the phase before tile kt's
+        // first memory phase (every read completed before that phase's closing barrier); a tile is first read
+        // after a barrier that every wave reached with its own loads of it landed.
+        static_assert(STAGES >= 3 && NW == 8, "ping-pong needs 8 waves and loads two tiles ahead");
+        constexpr int NSTEP = BK / 16;
+        uint4 fa[NSTEP][FM], fb[NSTEP][FN];
+        auto wait_tiles = [&](int later) {  // at most `later` tiles of this thread's loads in flight, LDS reads done
+            if (later <= 0) __builtin_amdgcn_s_waitcnt(0x0070);
+            else if (later == 1) __builtin_amdgcn_s_waitcnt((LPS & 15) | ((LPS >> 4) << 14) | 0x0070);
+            else __builtin_amdgcn_s_waitcnt(((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | 0x0070);
+        };
+#pragma unroll
+        for (int st = 0; st < STAGES - 1; ++st)
+            if (st < ktiles) issue(st, st, 0, LPS);
+        wait_tiles(min(STAGES - 2, ktiles - 1));
+        __builtin_amdgcn_s_barrier();
+        if (wm == 1) __builtin_amdgcn_s_barrier();
+        for (int kt = 0; kt < ktiles; ++kt) {
+            __builtin_amdgcn_sched_barrier(0);
+            const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+            const char *tb = ta + TA::bytes;
+            if (kt + STAGES - 1 < ktiles) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+#pragma unroll
+            for (int i = 0; i < NSTEP; ++i) {
+#pragma unroll
+                for (int ii = 0; ii < FM; ++ii) fa[i][ii] = frag(ta, wm * WR + 32 * ii, 16 * i, std::integral_constant<bool, AT>{});
+#pragma unroll
+                for (int j = 0; j < FN; ++j) fb[i][j] = frag(tb, wn * WCOLS + 32 * j, 16 * i, std::integral_constant<bool, BT>{});
+            }
+            wait_tiles(min(STAGES - 2, ktiles - 2 - kt));
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int i = 0; i < NSTEP; ++i)
+#pragma unroll
+                for (int ii = 0; ii < FM; ++ii)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[ii][j] = Mfma<F16>::run(fb[i][j], fa[i][ii], acc[ii][j]);
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+        }
+        if (wm == 0) __builtin_amdgcn_s_barrier();
+    } else if constexpr (XPF) {
         // Fragments run ahead across k tiles: the last k step of tile kt waits for tile kt + 1's loads (issued
         // STAGES - 1 tiles earlier), meets the other waves at the barrier (which also frees tile kt's stage:
         // every wave's reads of it have completed) and reads tile kt + 1's first fragments under its own MFMAs,
@@ -956,11 +1008,11 @@ __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2
     gemm_stream_persist_run<F16, BK, WN, AT, BT, BUF>(s, a, b, out, smem);
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, bool XPF = false>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, int KL = 0>
 __global__ __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2))) void gemm_stream(
     GemmShape s, const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, AnyStore out) {
     extern __shared__ __align__(1024) char smem[];
-    gemm_stream_tile<F16, BK, WN, AT, BT, BUF, AnyStore, 256, XPF>(s, a, b, out, smem);
+    gemm_stream_tile<F16, BK, WN, AT, BT, BUF, AnyStore, 256, KL>(s, a, b, out, smem);
 }
 
 // The 128 x 128 tile: 4 wavefronts of 64 x 64, two 32 KiB stages, two workgroups a CU (dots with too few

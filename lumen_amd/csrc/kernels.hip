@@ -29,10 +29,12 @@ constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // 128 x 128 (2 stages) and with 8 waves of 128 x 64 (2 stages); k tile 32 with 8 waves (4 stages); and
 // gemm_stream128 (128 x 128 tiles, 4 waves of 64 x 64, 2 stages, two workgroups a CU); and
 // gemm_stream_persist (the 8-wave 256 x 256 kernel, one persistent workgroup a CU walking the tiles); and the
-// k tile 32, 8-wave kernel with its MFMA fragments read ahead across k tiles (gemm_stream_tile's XPF).
+// k tile 32, 8-wave kernel with its MFMA fragments read ahead across k tiles (gemm_stream_tile's XPF); and the
+// k tile 32, 8-wave kernel whose two waves a SIMD alternate memory and MFMA phases (ping-pong).
 constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
-              kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4, kStream8wX = kNumTiled + 5;
-constexpr int kNumConfigs = kNumTiled + 6;
+              kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4, kStream8wX = kNumTiled + 5,
+              kStream8wP = kNumTiled + 6;
+constexpr int kNumConfigs = kNumTiled + 7;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -113,11 +115,11 @@ int launch_mfma_cfg(hipStream_t st, GemmShape s, int64_t z, const void *a, const
     return check(hipGetLastError(), "gemm_mfma launch");
 }
 
-template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, bool XPF = false>
+template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, int KL = 0>
 int launch_stream_kernel(hipStream_t st, const GemmShape &s, int64_t z, const void *a, const void *b, void *out,
                          int dtype, int splits) {
     constexpr int lds = gemm_stream_lds_bytes<BK, WN>();
-    auto kern = gemm_stream<F16, BK, WN, AT, BT, BUF, XPF>;
+    auto kern = gemm_stream<F16, BK, WN, AT, BT, BUF, KL>;
     static bool attr = false;
     if (!attr) {
         if (check(hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds),
@@ -159,14 +161,21 @@ int launch_stream128(hipStream_t st, GemmShape s, int64_t z, const void *a, cons
     return launch_stream128_kernel<F16, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
 }
 
-// XPF: the cross-tile fragment prefetch (buffer-load path only; the 64-bit-address path runs without it)
-template <bool F16, int BK, int WN, bool AT, bool BT, bool XPF = false>
+// KL 1, the cross-tile fragment prefetch (buffer-load path only; the 64-bit-address path runs without it), or 2,
+// the ping-pong k loop
+template <bool F16, int BK, int WN, bool AT, bool BT, int KL = 0>
 int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
                   int splits = 1) {
     s.tiles_m = int((s.m + 255) / 256);
     s.tiles_n = int((s.n + 255) / 256);
-    if (XPF && stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
-        return launch_stream_kernel<F16, BK, WN, AT, BT, true, XPF>(st, s, z, a, b, out, dtype, splits);
+    if constexpr (KL == 2) {
+        if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
+            return launch_stream_kernel<F16, BK, WN, AT, BT, true, 2>(st, s, z, a, b, out, dtype, splits);
+        return launch_stream_kernel<F16, BK, WN, AT, BT, false, 2>(st, s, z, a, b, out, dtype, splits);
+    }
+    if constexpr (KL == 1)
+        if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
+            return launch_stream_kernel<F16, BK, WN, AT, BT, true, 1>(st, s, z, a, b, out, dtype, splits);
     if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
         return launch_stream_kernel<F16, BK, WN, AT, BT, true>(st, s, z, a, b, out, dtype, splits);
     return launch_stream_kernel<F16, BK, WN, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
@@ -223,7 +232,8 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream4w: return launch_stream<F16, 64, 2, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8w: return launch_stream<F16, 64, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8w32: return launch_stream<F16, 32, 4, AT, BT>(st, s, z, a, b, out, dtype);
-        case kStream8wX: return launch_stream<F16, 32, 4, AT, BT, true>(st, s, z, a, b, out, dtype);
+        case kStream8wX: return launch_stream<F16, 32, 4, AT, BT, 1>(st, s, z, a, b, out, dtype);
+        case kStream8wP: return launch_stream<F16, 32, 4, AT, BT, 2>(st, s, z, a, b, out, dtype);
         case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case kStreamPersist: return launch_stream_persist<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
@@ -329,7 +339,7 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
         if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist) && d->k % 64) ||
-            ((cfg == kStream8w32 || cfg == kStream8wX) && d->k % 32))
+            ((cfg == kStream8w32 || cfg == kStream8wX || cfg == kStream8wP) && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
         return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
