@@ -194,7 +194,8 @@ def main():
             f, b = plan.cost(si)
             t = per_step[si]
             rate = f"{f / (t * 1e-3) / 1e12:7.1f} TF/s" if f else f"{b / (t * 1e-3) / 1e9:7.1f} GB/s"
-            print(f"[top] step {si:4d} {t:8.3f} ms {rate}  {plan.steps[si].kind:9s} {plan.steps[si].name:18s} "
+            tcfg = getattr(plan.steps[si], "config", None), getattr(plan.steps[si], "epi_variant", None)
+            print(f"[top] step {si:4d} {t:8.3f} ms {rate}  {plan.steps[si].kind:9s} {plan.steps[si].name:18s} cfg {tcfg} "
                   f"{_describe(plan, si)[:110]}", file=sys.stderr)
     # dominant kernel: the step taking the most time; steps within 10% of it count as tied (the three
     # vocabulary-head GEMMs take the same time) and the earliest of them is reported, so that the choice does

@@ -137,9 +137,11 @@ DEV float fdiv_row(float a, float b, float r, int ok) {
   if (!ok) return a / b;
   return fdiv_q(a, b, r);
 }
-DEV float fmax_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
+// NaN-propagating float32 maximum and minimum (-0 below +0): gfx950's v_maximum3_f32 / v_minimum3_f32, one
+// instruction for two operands or a chain of three
+DEV float fmax_n(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 DEV double dmax_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmax(a, b); }
-DEV float fmin_n(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
+DEV float fmin_n(float a, float b) { return __builtin_elementwise_minimum(a, b); }
 DEV double dmin_n(double a, double b) { return (a != a || b != b) ? __builtin_nan("") : fmin(a, b); }
 // float -> integer saturating at the result dtype's limits, NaN -> 0 (lumen/reference/mod.rs saturate). lo and
 // hi are the dtype's limits as doubles (T is its compute type, which may be wider); the 64-bit maxima round to
@@ -166,16 +168,15 @@ DEV float wsum(float v) {
   v += LK_DPP(v, 0x143, 0xC, 0.0f);
   return lane63(v);
 }
-// the maximum propagates NaN: fmaxf skips it, so a NaN on any lane (a ballot) gives NaN
+// the maximum propagates NaN (fmax_n): a NaN on any lane reaches lane 63
 DEV float wmax(float v) {
-  const bool nan = __builtin_amdgcn_ballot_w64(v != v) != 0;
-  v = fmaxf(v, LK_DPP(v, 0xB1, 0xF, -INFINITY));
-  v = fmaxf(v, LK_DPP(v, 0x4E, 0xF, -INFINITY));
-  v = fmaxf(v, LK_DPP(v, 0x141, 0xF, -INFINITY));
-  v = fmaxf(v, LK_DPP(v, 0x140, 0xF, -INFINITY));
-  v = fmaxf(v, LK_DPP(v, 0x142, 0xA, -INFINITY));
-  v = fmaxf(v, LK_DPP(v, 0x143, 0xC, -INFINITY));
-  return nan ? __builtin_nanf("") : lane63(v);
+  v = fmax_n(v, LK_DPP(v, 0xB1, 0xF, -INFINITY));
+  v = fmax_n(v, LK_DPP(v, 0x4E, 0xF, -INFINITY));
+  v = fmax_n(v, LK_DPP(v, 0x141, 0xF, -INFINITY));
+  v = fmax_n(v, LK_DPP(v, 0x140, 0xF, -INFINITY));
+  v = fmax_n(v, LK_DPP(v, 0x142, 0xA, -INFINITY));
+  v = fmax_n(v, LK_DPP(v, 0x143, 0xC, -INFINITY));
+  return lane63(v);
 }
 DEV double wsum(double v) { for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64); return v; }
 DEV double wmax(double v) { for (int o = 32; o > 0; o >>= 1) v = dmax_n(v, __shfl_xor(v, o, 64)); return v; }
@@ -971,11 +972,6 @@ class LoopKernel:
             isf = D.is_float(acc_dt)
             accn = em.tmp("acc")
             em.emit(f"{act} {accn} = {_red_identity(red.prim, acc_dt)};")
-            # a float32 maximum: fmaxf (which skips NaN) and a NaN flag kept as a lane mask, NaN restored after
-            # the row's lanes are folded; one vector compare an element instead of fmax_n's three operations
-            nanf = em.tmp("anynan") if red.prim == "reduce_max" and acc_dt == "float32" else None
-            if nanf:
-                em.emit(f"bool {nanf} = false;")
             for j in range(J):
                 for lane in range(V):
                     cexpr = f"(({j} * {T} + tid) * {V} + {lane})"
@@ -986,12 +982,7 @@ class LoopKernel:
                     idx = ("rc", "r", cidx, vbase(j), lane)
                     val = em.value(red.inputs[0], idx)
                     guard = "" if exact else f"if ({cexpr} < {C}LL) "
-                    if nanf:
-                        em.emit(f"{guard}{{ {accn} = fmaxf({accn}, {val}); {nanf} |= ({val} != {val}); }}")
-                    else:
-                        em.emit(f"{guard}{accn} = {_red_update(em, red.prim, acc_dt, accn, val)};")
-            if nanf:
-                em.emit(f"if ({nanf}) {accn} = __builtin_nanf(\"\");")
+                    em.emit(f"{guard}{accn} = {_red_update(em, red.prim, acc_dt, accn, val)};")
             total = em.tmp("red")
             op = "wsum" if red.prim == "reduce_sum" else "wmax"
             em.emit(f"{act} {total} = {op}(({act}){accn});")

@@ -416,6 +416,9 @@ template <int D> struct DkdvLds {
     static constexpr int kStore = kBase + 4 * 32 * kStagePitch;      // + each wave's [32 keys][64 queries] dS
 };
 
+// Whether a dK/dV workgroup takes a pair of causal key blocks.
+template <bool CAUSAL, bool ATOMIC_DQ> struct DkdvPaired { static constexpr bool value = CAUSAL && !ATOMIC_DQ; };
+
 // STORE_DS (the deterministic mode's default): each tile's dS (rounded as for dK) is stored to p.ds for the
 // dQ = dS K kernel, instead of a second kernel recomputing S and dP.
 template <int D, bool F16, bool CAUSAL, bool ATOMIC_DQ = false, bool STORE_DS = false>
@@ -434,9 +437,21 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
     const int g = lane >> 4, s16 = lane & 15;
     const int64_t nkb = (p.sk + 127) / 128;
-    int64_t unit, kblk;
-    xcd_order(int64_t(gridDim.x) / nkb, nkb, unit, kblk);  // causal: key block 0 has the most queries
+    // causal (but for the atomic mode, whose registers it would spill): a workgroup takes key blocks i and
+    // nkb - 1 - i (every workgroup then has the same number of query tiles but for the middle block of an odd
+    // count), so no workgroup is left running alone at the end
+    constexpr bool PAIR = DkdvPaired<CAUSAL, ATOMIC_DQ>::value;
+    const int64_t per = PAIR ? (nkb + 1) / 2 : nkb;
+    int64_t unit, pidx;
+    xcd_order(int64_t(gridDim.x) / per, per, unit, pidx);
     const int64_t b = unit / p.kv_heads, nkv = unit % p.kv_heads;
+    for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
+    const int64_t kblk = pass == 0 ? pidx : nkb - 1 - pidx;
+    if (pass == 1) {
+        if (kblk == pidx) break;
+        __syncthreads();  // every wave is done with the first block's LDS tiles
+    }
+    [&]() {
     const int64_t kb0 = kblk * 128;
     const int64_t kj = kb0 + wave * 32 + l32;
     const bool kvalid = kj < p.sk;
@@ -754,6 +769,8 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
             *reinterpret_cast<uint2 *>(dvp + d) =
                 make_uint2(pack2<F16>(adv[dt][4 * e4], adv[dt][4 * e4 + 1]), pack2<F16>(adv[dt][4 * e4 + 2], adv[dt][4 * e4 + 3]));
         }
+    }();
+    }
 }
 
 // The atomic dQ accumulator (float32 [B, N, Sq, D]) rounded into dq (its strides): eight head-dim elements a
@@ -1134,7 +1151,10 @@ template <int D, bool F16, bool CAUSAL>
 int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
     const bool atomic = p.dqacc != nullptr;
     dim3 gd(unsigned((d->heads * d->sq + 3) / 4), unsigned(d->batch));
-    dim3 gk(unsigned((d->sk + 127) / 128 * d->kv_heads * d->batch));
+    // dK/dV: a workgroup per key block, or per pair of key blocks (i, nkb - 1 - i) (nhipk::DkdvPaired)
+    const int64_t nkb = (d->sk + 127) / 128;
+    dim3 gk(unsigned((nhipk::DkdvPaired<CAUSAL, false>::value ? (nkb + 1) / 2 : nkb) * d->kv_heads * d->batch));
+    dim3 gka(unsigned((nhipk::DkdvPaired<CAUSAL, true>::value ? (nkb + 1) / 2 : nkb) * d->kv_heads * d->batch));
     dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
     float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
     // 16-byte rows: D / 8 lanes each; else one wavefront a row
@@ -1154,7 +1174,7 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
     }
     if (check(hipGetLastError(), "flash delta launch")) return 1;
     if (atomic) {
-        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL, true>), gk, dim3(256), 0, s, p, lse2);
+        hipLaunchKernelGGL((nhipk::flash_dkdv_kernel<D, F16, CAUSAL, true>), gka, dim3(256), 0, s, p, lse2);
         if (check(hipGetLastError(), "flash dkdv+dq launch")) return 1;
         const int64_t rows = d->batch * d->heads * d->sq;
         dim3 gc(unsigned((rows * (D / 8) + 255) / 256));
