@@ -110,6 +110,8 @@ def main():
                          "the fused elementwise/norm/softmax chain, flash attention forward + backward); lce: the "
                          "config-5 eval loss, fused linear cross entropy against unfused")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--attn-shape", default="8,2048,16,128", help="config 3: B,S,N,D of the attention")
+    ap.add_argument("--attn-config", type=int, default=-1, help="config 3: the forward tile config (-1 default)")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     ap.add_argument("--probe", action="store_true",
                     help="after the measurement, replay the dominant step alone 3 times and a 1 GiB device copy 3 "
@@ -412,7 +414,9 @@ def _config2(args):
 
 def _config3(args):
     """Flash attention forward + backward, causal, Q/K/V/dO [8, 2048, 16, 128] bf16 through the C ABI
-    (nhip_flash_fwd, nhip_flash_bwd): 137.4 GFLOP forward + 343.6 GFLOP backward (2.5x) a step."""
+    (nhip_flash_fwd, nhip_flash_bwd): 137.4 GFLOP forward + 343.6 GFLOP backward (2.5x) a step.
+    ``--attn-shape B,S,N,D`` times another shape (config 4's attention is 16,512,8,64) and ``--attn-config``
+    picks the forward tile."""
     import ctypes as C
     import math
 
@@ -420,7 +424,7 @@ def _config3(args):
 
     from lumen_amd import native as nv
 
-    b, s, n, d = 8, 2048, 16, 128
+    b, s, n, d = (int(x) for x in args.attn_shape.split(","))
     rng = np.random.default_rng(0)
     from lumen_amd.tensor import DeviceBuffer
 
@@ -437,7 +441,7 @@ def _config3(args):
     lse = DeviceBuffer(0, b * n * s * 4)
     desc = nv.AttnDesc()
     desc.batch, desc.heads, desc.kv_heads, desc.sq, desc.sk, desc.head_dim = b, n, n, s, s, d
-    desc.dtype, desc.causal, desc.scale, desc.config = 1, 1, 1.0 / math.sqrt(d), -1
+    desc.dtype, desc.causal, desc.scale, desc.config = 1, 1, 1.0 / math.sqrt(d), args.attn_config
     desc.deterministic = 1  # dQ by its own kernel (the plans' default; faster here than atomic adds)
     desc.q_b, desc.q_s, desc.q_n = s * n * d, n * d, d
     for nm in ("k", "v", "o", "do", "dq", "dk", "dv"):
@@ -482,7 +486,7 @@ def _config3(args):
     if not args.no_cpu:
         cpu = _attn_cpu(b, s, n, d)
     return _op_line(args, "config3 flash attention fwd+bwd TFLOP/s", f_ms + b_ms, tf, "TFLOP/s",
-                    {"workload": "config3: causal flash attention fwd+bwd, [8,2048,16,128] bf16"}, roof, cpu, "bf16",
+                    {"workload": f"config3: causal flash attention fwd+bwd, [{b},{s},{n},{d}] bf16"}, roof, cpu, "bf16",
                     {"fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
                      "fwd_tflops": round(ff / (f_ms * 1e-3) / 1e12, 1),
                      "bwd_tflops": round(bf / (b_ms * 1e-3) / 1e12, 1)})
