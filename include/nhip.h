@@ -131,7 +131,10 @@ int nhip_gemm_workspace(const nhip_gemm_desc *desc, size_t *bytes);
  * lumen/codegen/attention/triton/kernel.py:34-256) ------------------------------------------------------ *
  *
  * Q [B, Sq, N, H], K [B, Sk, Nkv, H], V [B, Sk, Nkv, H], O [B, Sq, N, H] as element strides per axis
- * (batch, sequence, head; the head-dim axis is contiguous). N must be a multiple of Nkv (grouped-query).
+ * (batch, sequence, head; the head-dim axis is contiguous; every stride a multiple of 8 elements). N must be a
+ * multiple of Nkv (grouped-query). H is a multiple of 8, at most 256 for the forward and 128 for the backward
+ * (lumen/graph_compiler/passes/attention/forward.rs:100 MAX_HEAD, backward.rs:86); the kernels run at 64, 128 or
+ * 256 with the columns past H read as zeros, which needs each (batch, head) of an operand within 2 GiB.
  * LSE and delta are float32 [B, N, Sq] (contiguous). Causal masks key j for query i where
  * j > i + Sk - Sq (bottom-right aligned, lumen/functional/attention/flash.py:95-97). */
 typedef struct {
@@ -165,7 +168,7 @@ int nhip_attn_config_count(int *count);
 /* FlashAttention-2 backward (kernel.py:107-256): delta = rowsum(dO * O) (float32 [B, N, Sq]), then dK, dV
  * per key block, and dQ by desc->deterministic's mode: from the dS tiles the dK/dV kernel stored (1), per query
  * block by a kernel recomputing S and dP (2), or added atomically by the dK/dV kernel into a float32
- * [B, N, Sq, D] buffer in the workspace, then rounded into dq (0). `workspace` needs nhip_flash_bwd_workspace
+ * [B, N, Sq, D] buffer in the workspace (D = H padded to 64 or 128), then rounded into dq (0). `workspace` needs nhip_flash_bwd_workspace
  * bytes (mode 1: 2 B N Sk Sq bytes of dS tiles, rounded up to 128 keys x 64 queries). */
 int nhip_flash_bwd(const nhip_attn_desc *desc, const void *q, const void *k, const void *v, const void *o,
                    const void *d_o, const float *lse, void *dq, void *dk, void *dv, void *workspace);

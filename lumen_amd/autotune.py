@@ -75,8 +75,9 @@ class HipAttentionConfig:
         return [HipAttentionConfig(w) for w in HipAttentionConfig.WAVES]
 
     def fits(self, h: int, hv: int) -> bool:
-        """Whether the flash kernels take query/key head dim ``h`` and value head dim ``hv``."""
-        return h in (64, 128) and hv == h
+        """Whether the flash forward takes query/key head dim ``h`` and value head dim ``hv`` (a multiple of 8 up
+        to 256, the value head dim equal to it)."""
+        return 0 < h <= 256 and h % 8 == 0 and hv == h
 
     def key(self):
         return ("attention", self.waves)

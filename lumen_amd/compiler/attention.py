@@ -21,6 +21,14 @@ from lumen_amd.graph.ir import Graph, Node, TensorType
 
 FWD, BWD = "flash_attention", "flash_attention_backward"
 
+# Largest head dims the flash kernels take (``forward.rs:100`` MAX_HEAD, ``backward.rs:86`` MAX_BACKWARD_HEAD):
+# multiples of 8; the kernels run at 64, 128 or 256 with the columns past the head dim read as zeros.
+MAX_HEAD, MAX_BACKWARD_HEAD = 256, 128
+
+
+def _head_dim_ok(h, limit):
+    return h > 0 and h % 8 == 0 and h <= limit
+
 
 class _G:
     """Lookup helpers over a graph."""
@@ -258,7 +266,7 @@ def match_forward(g: Graph):
         qb, qf, qc = _dims_of_dot(d1, 0, qt)
         kb, kf, kc = _dims_of_dot(d1, 1, kt)
         vb, vf, vc = _dims_of_dot(d2, 1, vt)
-        if len(qf) != 1 or len(kf) != 1 or len(vf) != 1 or qt.shape[qc[0]] not in (64, 128):
+        if len(qf) != 1 or len(kf) != 1 or len(vf) != 1 or not _head_dim_ok(qt.shape[qc[0]], MAX_HEAD):
             continue
         if vt.shape[vf[0]] != qt.shape[qc[0]]:
             continue
@@ -355,8 +363,10 @@ def match_backward(g: Graph):
         if dv.inputs[1] != do or dk.inputs[1] != q or dq.inputs[1] != k:
             continue
         qt = g.types[q]
-        if qt.dtype not in ("bfloat16", "float16") or len(qt.shape) != 4 or qt.shape[3] not in (64, 128):
+        if qt.dtype not in ("bfloat16", "float16") or len(qt.shape) != 4 or not _head_dim_ok(qt.shape[3], MAX_BACKWARD_HEAD):
             continue
+        if any(len(g.types[x].shape) != 4 or g.types[x].shape[3] != qt.shape[3] for x in (k, v, o, do)):
+            continue  # the kernels take one head dim for Q, K, V and dO
         if any(tuple(x.params["rhs_batch"]) != (0, 2) for x in (dv, dk, dq)):
             continue
         # grouped heads: K and V expanded to every query head, dK and dV summed over each group

@@ -70,6 +70,7 @@ struct AttnParams {
     float *dqacc;  // float32 [B, N, Sq, D] dQ accumulated atomically by the dK/dV kernel (null: deterministic)
     uint16_t *ds;  // dS tiles [B, N, Sk / 128, Sq / 64][128 keys][64 queries] the dK/dV kernel stores (or null)
     int64_t sq, sk, heads, kv_heads, batch;
+    int64_t hd;  // the operands' head dim; the kernels run at D >= hd (head_dim_of) with columns hd.. read as zeros
     int64_t q_b, q_s, q_n, k_b, k_s, k_n, v_b, v_s, v_n, o_b, o_s, o_n;
     int64_t do_b, do_s, do_n, dq_b, dq_s, dq_n, dk_b, dk_s, dk_n, dv_b, dv_s, dv_n;
     float scale;
@@ -113,7 +114,7 @@ __device__ __forceinline__ void xcd_order(int64_t units, int64_t per, int64_t &u
 
 template <int D>
 __device__ __forceinline__ int kv_swz(int r) {
-    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
     else return ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
@@ -128,10 +129,12 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // Issues the loads of rows [k0, k0 + 64) of a [*, D] operand (row stride `rs` elements, `rows` rows) into
 // the swizzled tile `dst`. When the operand spans less than 2^31 bytes the loads are buffer loads (the row
 // offset a uniform operand, the lane's offset fixed) and rows past `rows` read zeros; otherwise 64-bit global
-// loads with rows past `rows` clamped to the last row. Either way those rows' scores are masked.
+// loads with rows past `rows` clamped to the last row. Either way those rows' scores are masked. Columns from
+// `cols` on (a head dim padded to D) read zeros: the buffer path takes an offset past the buffer's end there
+// (the launcher checks that padded operands take that path).
 template <int D, int NW = 4>
 __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs, int64_t k0, int64_t rows,
-                                                uint16_t *dst, int wave, int lane) {
+                                                uint16_t *dst, int wave, int lane, int64_t cols = D) {
     constexpr int RPS = 1024 / (D * 2);  // rows a wave instruction covers
     constexpr int SEGS = 64 / RPS;       // 1 KiB segments in the tile
     const int64_t bytes = ((rows - 1) * rs + D) * 2;
@@ -142,7 +145,8 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
         for (int seg = wave; seg < SEGS; seg += NW) {
             const int r = seg * RPS + lane / (D / 8);
             const int c = lane % (D / 8);
-            const uint32_t vo = uint32_t((r * rs + ((c ^ kv_swz<D>(r)) << 3)) * 2);
+            const int sc = c ^ kv_swz<D>(r);
+            const uint32_t vo = 8 * sc < cols ? uint32_t((r * rs + (sc << 3)) * 2) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(dst + seg * 512), 16, vo, so, 0, 0);
         }
         return;
@@ -162,10 +166,12 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
 // K/V tile a workgroup streams through LDS. More waves read K and V fewer times per query; fewer fill the CUs
 // when there are few query blocks. Two workgroups a CU hold the 64 KiB (D = 128) double-buffered tiles, so
 // each wave keeps 256 VGPRs at 4 waves a workgroup and 8 (one workgroup a CU at 8).
-template <int NW> struct FwdOccupancy { static constexpr int kBlocks = NW >= 8 ? 1 : (NW >= 4 ? 2 : 4); };
+template <int NW, int D = 128> struct FwdOccupancy {
+    static constexpr int kBlocks = D > 128 ? 1 : (NW >= 8 ? 1 : (NW >= 4 ? 2 : 4));
+};
 
 template <int D, bool F16, bool CAUSAL, int NW = 4>
-__global__ __launch_bounds__(64 * NW, FwdOccupancy<NW>::kBlocks) void flash_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * NW, (FwdOccupancy<NW, D>::kBlocks)) void flash_fwd_kernel(AttnParams p) {
     constexpr int QB = 32 * NW;  // queries a workgroup
     constexpr int BN = 64;
     constexpr int DS = D / 16, DT = D / 32;
@@ -199,14 +205,15 @@ __global__ __launch_bounds__(64 * NW, FwdOccupancy<NW>::kBlocks) void flash_fwd_
     const int nfull = full_end > 0 ? int(full_end / BN) : 0;
 
     if (ntiles > 0) {
-        load_tile_async<D, NW>(kp, p.k_s, 0, p.sk, smem, wave, lane);
-        load_tile_async<D, NW>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
+        load_tile_async<D, NW>(kp, p.k_s, 0, p.sk, smem, wave, lane, p.hd);
+        load_tile_async<D, NW>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hd);
     }
 
     uint4 qf[DS];
 #pragma unroll
     for (int t = 0; t < DS; ++t)
-        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        qf[t] = qvalid && 16 * t + 8 * h < p.hd ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h)
+                                                : make_uint4(0, 0, 0, 0);
 
     f32x16_t acc[DT];
 #pragma unroll
@@ -224,8 +231,8 @@ __global__ __launch_bounds__(64 * NW, FwdOccupancy<NW>::kBlocks) void flash_fwd_
         __syncthreads();                // ... and every thread's; tile kt-1's buffer is free
         if (kt + 1 < ntiles) {
             uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
-            load_tile_async<D, NW>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
-            load_tile_async<D, NW>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
+            load_tile_async<D, NW>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane, p.hd);
+            load_tile_async<D, NW>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hd);
         }
         if (CAUSAL && k0 > wq_last + shift) continue;  // every key of the tile is masked for this wave
         const char *Kb = reinterpret_cast<const char *>(Ks);
@@ -307,6 +314,7 @@ __global__ __launch_bounds__(64 * NW, FwdOccupancy<NW>::kBlocks) void flash_fwd_
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
+            if (32 * dt + 8 * e4 >= p.hd) continue;  // padded columns
             const uint32_t w0 = pack2<F16>(acc[dt][4 * e4 + 0] * inv, acc[dt][4 * e4 + 1] * inv);
             const uint32_t w1 = pack2<F16>(acc[dt][4 * e4 + 2] * inv, acc[dt][4 * e4 + 3] * inv);
             *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *ls
     const uint16_t *o = p.o_in + b * p.o_b + n * p.o_n + q * p.o_s;
     const uint16_t *g = p.d_o + b * p.do_b + n * p.do_n + q * p.do_s;
     float acc = 0.0f;
-    for (int d = lane; d < D; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
+    for (int d = lane; d < p.hd; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
     acc = wave_sum(acc);
     const int64_t i = (b * p.heads + n) * p.sq + q;
     if (p.dqacc)  // the row of the atomic dQ accumulator starts at zero
@@ -482,14 +490,14 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         int64_t q0;
         tile_src(j, qp, gp, ls, dl, q0);
         uint16_t *dst = smem + (j & 1) * 2 * TILE;
-        load_tile_async<D>(qp, p.q_s, q0, p.sq, dst, wave, lane);
-        load_tile_async<D>(gp, p.do_s, q0, p.sq, dst + TILE, wave, lane);
+        load_tile_async<D>(qp, p.q_s, q0, p.sq, dst, wave, lane, p.hd);
+        load_tile_async<D>(gp, p.do_s, q0, p.sq, dst + TILE, wave, lane, p.hd);
         if (wave == 0) load_row64_async(ls, q0, p.sq, Ls[j & 1], lane);
         if (wave == 1) load_row64_async(dl, q0, p.sq, Dl[j & 1], lane);
     };
     if constexpr (ATOMIC_DQ) {  // waited for with the first tile's loads
-        load_tile_async<D>(kp, p.k_s, kb0, p.sk, Ks, wave, lane);
-        load_tile_async<D>(kp, p.k_s, kb0 + 64, p.sk, Ks + 64 * D, wave, lane);
+        load_tile_async<D>(kp, p.k_s, kb0, p.sk, Ks, wave, lane, p.hd);
+        load_tile_async<D>(kp, p.k_s, kb0 + 64, p.sk, Ks + 64 * D, wave, lane, p.hd);
     }
     if (total > 0) issue(0);
 
@@ -518,8 +526,9 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
     uint4 kf[DS], vf[DS];
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
-        kf[t] = kvalid ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        vf[t] = kvalid ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        const bool in = kvalid && 16 * t + 8 * h < p.hd;
+        kf[t] = in ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        vf[t] = in ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
     }
     f32x16_t adk[DT], adv[DT];
 #pragma unroll
@@ -764,6 +773,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
             const int d = 32 * dt + 8 * e4 + 4 * h;
+            if (32 * dt + 8 * e4 >= p.hd) continue;  // padded columns
             *reinterpret_cast<uint2 *>(dkp + d) =
                 make_uint2(pack2<F16>(adk[dt][4 * e4], adk[dt][4 * e4 + 1]), pack2<F16>(adk[dt][4 * e4 + 2], adk[dt][4 * e4 + 3]));
             *reinterpret_cast<uint2 *>(dvp + d) =
@@ -782,6 +792,7 @@ __global__ __launch_bounds__(256) void flash_dq_round_kernel(AttnParams p) {
     const int64_t rows_all = p.heads * p.sq;
     if (row >= p.batch * rows_all) return;
     const int64_t b = row / rows_all, rem = row % rows_all, n = rem / p.sq, q = rem % p.sq;
+    if (c >= p.hd) return;  // padded columns
     const float4 x = *reinterpret_cast<const float4 *>(p.dqacc + row * D + c);
     const float4 y = *reinterpret_cast<const float4 *>(p.dqacc + row * D + c + 4);
     uint16_t *dst = p.dq + b * p.dq_b + n * p.dq_n + q * p.dq_s + c;
@@ -836,7 +847,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_ds_kernel(AttnParams p) {
     // K rows of step kt into LDS stage B (three stages: issued two steps ahead)
     auto issue_k = [&](auto bufc, int kt) {
         constexpr int B = decltype(bufc)::value;
-        load_tile_async<D, 4>(kp, p.k_s, int64_t(kt) * KT, p.sk, smem + B * KSTAGE, wave, lane);
+        load_tile_async<D, 4>(kp, p.k_s, int64_t(kt) * KT, p.sk, smem + B * KSTAGE, wave, lane, p.hd);
     };
     // dS fragments of step kt into register set B (two sets: issued one step ahead): 16-key steps 4 (kt & 1) + kk
     // and query halves qh of the 128-key block kt / 2
@@ -914,6 +925,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_ds_kernel(AttnParams p) {
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {
                 const int d = 32 * j + 8 * e4 + 4 * h;
+                if (32 * j + 8 * e4 >= p.hd) continue;  // padded columns
                 *reinterpret_cast<uint2 *>(dqp + d) = make_uint2(pack2<F16>(acc[qh][j][4 * e4], acc[qh][j][4 * e4 + 1]),
                                                                  pack2<F16>(acc[qh][j][4 * e4 + 2], acc[qh][j][4 * e4 + 3]));
             }
@@ -955,15 +967,16 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
     if (CAUSAL) full_end = min(full_end, q0 + shift + 1);
     const int nfull = full_end > 0 ? int(full_end / BN) : 0;
     if (ntiles > 0) {
-        load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane);
-        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane);
+        load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane, p.hd);
+        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hd);
     }
 
     uint4 qf[DS], gf[DS];
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
-        qf[t] = qvalid ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        gf[t] = qvalid ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        const bool in = qvalid && 16 * t + 8 * h < p.hd;
+        qf[t] = in ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        gf[t] = in ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
     }
     const float l2 = qvalid ? lse2[(b * p.heads + n) * p.sq + qi] : 0.0f;
     const float dl = qvalid ? p.delta[(b * p.heads + n) * p.sq + qi] : 0.0f;
@@ -980,8 +993,8 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
         __syncthreads();
         if (kt + 1 < ntiles) {
             uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
-            load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane);
-            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane);
+            load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane, p.hd);
+            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hd);
         }
         if (CAUSAL && k0 > wq_last + shift) continue;
         const char *Kb = reinterpret_cast<const char *>(smem + (kt & 1) * 2 * TILE);
@@ -1042,6 +1055,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4)
+            if (32 * dt + 8 * e4 < p.hd)  // padded columns are not stored
             *reinterpret_cast<uint2 *>(dqp + 32 * dt + 8 * e4 + 4 * h) =
                 make_uint2(pack2<F16>(acc[dt][4 * e4], acc[dt][4 * e4 + 1]), pack2<F16>(acc[dt][4 * e4 + 2], acc[dt][4 * e4 + 3]));
 }
@@ -1056,6 +1070,10 @@ namespace nhip {
 // Backward workspace: delta and the base-2 LSE (2 floats a query row), then by mode (nhip_attn_desc.deterministic)
 // 0: the float32 dQ accumulator [B, N, Sq, D]; 1: the dS tiles [B, N, ceil(Sk/128), ceil(Sq/64)][128][64] (16-bit);
 // 2: nothing (dQ recomputes S and dP).
+// The head dim the kernels run at: 64, 128 or 256, the operands' own head dim (a multiple of 8) padded up to it
+// with zero columns.
+inline int64_t kernel_head_dim(int64_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
+
 inline size_t flash_bwd_dq_offset(const nhip_attn_desc *d) {
     return (2 * size_t(d->batch) * d->heads * d->sq * sizeof(float) + 255) / 256 * 256;
 }
@@ -1065,7 +1083,7 @@ inline size_t flash_bwd_ds_bytes(const nhip_attn_desc *d) {
 inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
     if (d->deterministic == 2) return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
     if (d->deterministic == 1) return flash_bwd_dq_offset(d) + flash_bwd_ds_bytes(d);
-    return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * d->head_dim * sizeof(float);
+    return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * kernel_head_dim(d->head_dim) * sizeof(float);
 }
 
 inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
@@ -1075,6 +1093,7 @@ inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
     p.heads = d->heads;
     p.kv_heads = d->kv_heads;
     p.batch = d->batch;
+    p.hd = d->head_dim;
     p.q_b = d->q_b, p.q_s = d->q_s, p.q_n = d->q_n;
     p.k_b = d->k_b, p.k_s = d->k_s, p.k_n = d->k_n;
     p.v_b = d->v_b, p.v_s = d->v_s, p.v_n = d->v_n;
@@ -1091,9 +1110,26 @@ inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
 // workgroup, 1 = 8 waves (256 queries), 2 = 2 waves (64 queries). The backward kernels have one tile each.
 constexpr int kNumAttnConfigs = 3;
 
-inline int check_attn(const nhip_attn_desc *d, const char *what) {
-    if (d->head_dim != 64 && d->head_dim != 128)
-        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " (the hip kernels take 64 or 128)");
+// A padded head dim reads its zero columns through buffer loads, which take 32-bit offsets: every (batch, head)
+// slice of an operand must then span under 2 GiB (rows rounded up to the 64-row tiles).
+inline bool attn_span_ok(int64_t rows, int64_t rs, int64_t hd) {
+    return (((rows + 63) / 64 * 64) * rs + hd) * 2 < (int64_t(1) << 31);
+}
+
+inline int check_attn(const nhip_attn_desc *d, const char *what, int64_t max_hd = 128) {
+    if (d->head_dim <= 0 || d->head_dim % 8 || d->head_dim > max_hd)
+        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) +
+                    " (the hip kernels take multiples of 8 up to " + std::to_string(max_hd) + ")");
+    for (int64_t st : {d->q_b, d->q_s, d->q_n, d->k_b, d->k_s, d->k_n, d->v_b, d->v_s, d->v_n, d->o_b, d->o_s, d->o_n,
+                       d->do_b, d->do_s, d->do_n, d->dq_b, d->dq_s, d->dq_n, d->dk_b, d->dk_s, d->dk_n, d->dv_b, d->dv_s,
+                       d->dv_n})
+        if (st % 8) return fail(std::string(what) + ": every stride must be a multiple of 8 elements (16-byte rows)");
+    if (d->head_dim != kernel_head_dim(d->head_dim) &&
+        !(attn_span_ok(d->sq, d->q_s, d->head_dim) && attn_span_ok(d->sk, d->k_s, d->head_dim) &&
+          attn_span_ok(d->sk, d->v_s, d->head_dim) && attn_span_ok(d->sq, d->o_s, d->head_dim) &&
+          attn_span_ok(d->sq, d->do_s, d->head_dim)))
+        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " is padded to " +
+                    std::to_string(kernel_head_dim(d->head_dim)) + ", which needs each (batch, head) of an operand within 2 GiB");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
     if (d->deterministic < 0 || d->deterministic > 2)
@@ -1117,16 +1153,21 @@ int launch_fwd_nw(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_des
 
 template <int D, bool F16, bool CAUSAL>
 int launch_fwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *d) {
-    switch (d->config < 0 ? 0 : d->config) {
-        case 1: return launch_fwd_nw<D, F16, CAUSAL, 8>(s, p, d);
-        case 2: return launch_fwd_nw<D, F16, CAUSAL, 2>(s, p, d);
-        default: return launch_fwd_nw<D, F16, CAUSAL, 4>(s, p, d);
+    if constexpr (D > 128) {
+        // head dim 256: 4 waves, one workgroup a CU (its K/V tiles fill 128 KiB of LDS), whatever the config
+        return launch_fwd_nw<D, F16, CAUSAL, 4>(s, p, d);
+    } else {
+        switch (d->config < 0 ? 0 : d->config) {
+            case 1: return launch_fwd_nw<D, F16, CAUSAL, 8>(s, p, d);
+            case 2: return launch_fwd_nw<D, F16, CAUSAL, 2>(s, p, d);
+            default: return launch_fwd_nw<D, F16, CAUSAL, 4>(s, p, d);
+        }
     }
 }
 
 int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const void *k, const void *v, void *o,
                  float *lse) {
-    if (check_attn(d, "flash attention")) return 1;
+    if (check_attn(d, "flash attention", 256)) return 1;
     if (d->sq == 0 || d->batch == 0 || d->heads == 0) return 0;
     nhipk::AttnParams p = attn_params(d);
     p.q = static_cast<const uint16_t *>(q);
@@ -1136,7 +1177,13 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.lse = lse;
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_FWD(DD, FF, CC) return launch_fwd<DD, FF, CC>(s, p, d)
-    if (d->head_dim == 128) {
+    const int64_t kd = kernel_head_dim(d->head_dim);
+    if (kd == 256) {
+        if (f16) { if (d->causal) NHIP_FWD(256, true, true); NHIP_FWD(256, true, false); }
+        if (d->causal) NHIP_FWD(256, false, true);
+        NHIP_FWD(256, false, false);
+    }
+    if (kd == 128) {
         if (f16) { if (d->causal) NHIP_FWD(128, true, true); NHIP_FWD(128, true, false); }
         if (d->causal) NHIP_FWD(128, false, true);
         NHIP_FWD(128, false, false);
@@ -1158,7 +1205,7 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
     dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
     float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
     // 16-byte rows: D / 8 lanes each; else one wavefront a row
-    const bool vec = D % 8 == 0 && 64 % (D / 8 > 0 ? D / 8 : 1) == 0 && D / 8 <= 64 &&
+    const bool vec = d->head_dim == D && D % 8 == 0 && 64 % (D / 8 > 0 ? D / 8 : 1) == 0 && D / 8 <= 64 &&
                      ((reinterpret_cast<uintptr_t>(p.o_in) | reinterpret_cast<uintptr_t>(p.d_o)) & 15) == 0 &&
                      (p.o_b | p.o_n | p.o_s | p.do_b | p.do_n | p.do_s) % 8 == 0;
     if constexpr (D % 8 == 0 && D >= 8 && D <= 512 && 64 % (D / 8) == 0) {
@@ -1213,7 +1260,7 @@ int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.ds = d->deterministic == 1 ? reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + flash_bwd_dq_offset(d)) : nullptr;
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_BWD(DD, FF, CC) return launch_bwd<DD, FF, CC>(s, p, d)
-    if (d->head_dim == 128) {
+    if (kernel_head_dim(d->head_dim) == 128) {
         if (f16) { if (d->causal) NHIP_BWD(128, true, true); NHIP_BWD(128, true, false); }
         if (d->causal) NHIP_BWD(128, false, true);
         NHIP_BWD(128, false, false);

@@ -23,7 +23,13 @@ CASES = [
     (1, 64, 192, 4, 2, 128, True),
     (1, 96, 160, 1, 1, 64, False),
     (1, 1024, 1024, 2, 1, 128, True),
+    # head dims padded to the kernels' 64 or 128 (zero columns past them)
+    (1, 128, 160, 2, 2, 32, True),
+    (2, 96, 96, 4, 2, 96, True),
+    (1, 200, 136, 2, 1, 72, False),
 ]
+# the forward alone also takes head dims up to 256
+FWD_CASES = CASES + [(1, 200, 200, 2, 1, 256, True), (2, 64, 130, 2, 2, 192, False)]
 
 
 def _inputs(b, sq, sk, n, nkv, d, seed=0):
@@ -34,7 +40,7 @@ def _inputs(b, sq, sk, n, nkv, d, seed=0):
     return q, k, v
 
 
-@pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", CASES)
+@pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", FWD_CASES)
 def test_flash_forward_matches_unfused_graph(hip, b, sq, sk, n, nkv, d, causal):
     q, k, v = _inputs(b, sq, sk, n, nkv, d)
     scale = 1.0 / math.sqrt(d)
@@ -152,10 +158,10 @@ def test_flash_backward_config3_throughput(hip):
     assert np.isfinite(D.bf16_to_f32(gq.get(q.shape, np.uint16))).all()
 
 
-@pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", [CASES[1], CASES[2], CASES[3], CASES[5]])
+@pytest.mark.parametrize("b,sq,sk,n,nkv,d,causal", [CASES[1], CASES[2], CASES[3], CASES[5], CASES[7], FWD_CASES[-2]])
 def test_forward_tile_configs_agree_bit_for_bit(hip, b, sq, sk, n, nkv, d, causal):
     """Every forward tile config (4, 8 or 2 waves a workgroup) gives the same bits: each query is one lane's,
-    its keys visited in the same tiles and order whatever the workgroup size."""
+    its keys visited in the same tiles and order whatever the workgroup size (head dim 256 runs one tile)."""
     q, k, v = _inputs(b, sq, sk, n, nkv, d, seed=3)
     dq, dk, dv = Dev(q), Dev(k), Dev(v)
     count = C.c_int()

@@ -1,8 +1,10 @@
 """The reference's own attention cases (``tests/functional/test_attention.py:51-67`` forward,
 ``:354-359`` backward) compiled for hip: grouped heads, one query row, fewer keys than queries, head dims
-16/24/32/64/128 with a value head dim different from the query's. Shapes the flash kernels take (head dim 64
-or 128, equal value head dim, no query row left without keys) run as one flash step; the others run the
-unfused dot / row-softmax plan. Both are checked against float64 attention at the reference's tolerances."""
+16/24/32/64/128 with a value head dim different from the query's, plus head dims 24, 40, 96 and 256. Shapes the
+flash kernels take (a head dim that is a multiple of 8, up to 256 forward and 128 backward, as
+``passes/attention/forward.rs:100,725`` and ``backward.rs:86,473`` allow; equal value head dim; no query row left
+without keys) run as flash steps; the others run the unfused dot / row-softmax plan. Both are checked against
+float64 attention at the reference's tolerances."""
 
 import numpy as np
 import pytest
@@ -22,8 +24,12 @@ CASES = [  # (b, sq, sk, n, nkv, h, hv), causal — test_attention.py:53-60
     ((1, 1, 300, 8, 2, 128, 128), True),
     ((2, 5, 40, 2, 1, 16, 24), False),
     ((1, 70, 200, 2, 2, 128, 128), True),
-    # added here: the flash kernels' other head size with fewer keys than queries, non-causal
+    # added here: the flash kernels' other head size with fewer keys than queries, non-causal; head dims the
+    # kernels pad (96 to 128, 40 to 64) and the largest forward head dim
     ((1, 130, 77, 2, 1, 64, 64), False),
+    ((1, 100, 100, 4, 2, 96, 96), True),
+    ((2, 64, 70, 2, 2, 40, 40), False),
+    ((1, 70, 90, 2, 1, 256, 256), True),
 ]
 
 BACKWARD_CASES = [  # test_attention.py:354-359, plus two the hip flash backward takes
@@ -33,6 +39,9 @@ BACKWARD_CASES = [  # test_attention.py:354-359, plus two the hip flash backward
     ((1, 9, 24, 2, 2, 128, 128), True),
     ((1, 40, 40, 4, 2, 64, 64), True),
     ((2, 70, 150, 2, 2, 128, 128), False),
+    ((1, 100, 100, 4, 2, 96, 96), True),
+    ((1, 33, 47, 2, 2, 24, 24), False),
+    ((1, 64, 64, 2, 2, 256, 256), True),  # forward flash, backward past MAX_BACKWARD_HEAD: unfused
 ]
 
 
@@ -51,9 +60,9 @@ def reference(q, k, v, causal):
     return np.einsum("bnqk,bknh->bqnh", p, v)
 
 
-def _flash_ok(case):
+def _flash_ok(case, limit=256):
     (b, sq, sk, n, nkv, h, hv), causal = case
-    return h in (64, 128) and hv == h and not (causal and sk < sq)
+    return h % 8 == 0 and h <= limit and hv == h and not (causal and sk < sq)
 
 
 def _tensors(dtype, *shapes, seed=0):
@@ -114,7 +123,7 @@ def test_attention_backward_cases(hip, case, deterministic, store_ds):
     if _flash_ok(case):
         assert "flash_fwd" in kinds, kinds
         # grouped heads too: the kernel sums dK and dV over each group of query heads
-        assert "flash_bwd" in kinds, kinds
+        assert ("flash_bwd" in kinds) == _flash_ok(case, 128), kinds
     for g_, w_ in zip(got, want):
         w_ = np.asarray(w_, np.float32)
         np.testing.assert_allclose(g_, w_, rtol=2e-2, atol=2e-2 * np.abs(w_).max())

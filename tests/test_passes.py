@@ -252,3 +252,17 @@ def test_simplify_rewrites_keep_values_bit_for_bit(name):
     assert check(s), str(s)
     for seed in (0, 1):
         _same(g, s, seed)
+
+
+def test_attention_backward_with_a_different_value_head_dim_stays_unfused():
+    """A value head dim other than the query's (16 vs 24, one of the reference's backward cases) has no flash
+    kernel: neither the forward nor the backward is matched, and the values are unchanged."""
+    def grads(q, k, v, do):
+        out, pull = L.vjp(lambda q, k, v: F.flash_attention(q, k, v, is_causal=True), q, k, v)
+        return (out,) + pull(do)
+
+    metas = [L.empty(s, "bfloat16", "meta") for s in ([1, 3, 2, 16], [1, 50, 1, 16], [1, 50, 1, 24], [1, 3, 2, 24])]
+    g = L.make_graph(grads)(*metas)
+    m = attention.match(passes.frontend(g))
+    assert not [n for n in m.nodes if n.prim == "fusion"]
+    _same(g, m)

@@ -386,16 +386,18 @@ def test_long_sequences_take_the_recomputing_backward_with_o_s_scratch():
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
-@pytest.mark.parametrize("shape", [(1, 1, 1, 1, 64), (2, 3, 200, 333, 128), (1, 4, 4097, 129, 64), (3, 2, 64, 1, 96)])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1, 64), (2, 3, 200, 333, 128), (1, 4, 4097, 129, 64), (3, 2, 64, 1, 96),
+                                   (1, 2, 70, 70, 32)])
 def test_flash_backward_scratch_is_what_the_library_reports(mode, shape):
     """The plan sizes a flash backward's scratch by asking the library (nhip_flash_bwd_workspace); checked
     against the layout the kernels write — delta and the LSE (two floats a query row), then, 256-byte
-    aligned, the float32 dQ accumulator (mode 0) or 128 x 64 tiles of 16-bit dS (mode 1) — on ragged shapes."""
+    aligned, the float32 dQ accumulator (mode 0, its head dim padded to the kernel's 64 or 128) or 128 x 64 tiles
+    of 16-bit dS (mode 1) — on ragged shapes."""
     from lumen_amd.compiler import attention as A
 
     b, n, sq, sk, d = shape
     rows = 2 * b * n * sq * 4
     want = {2: rows,
             1: -(-rows // 256) * 256 + b * n * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2,
-            0: -(-rows // 256) * 256 + b * n * sq * d * 4}[mode]
+            0: -(-rows // 256) * 256 + b * n * sq * (64 if d <= 64 else 128) * 4}[mode]
     assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode) == want
