@@ -105,13 +105,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="5", choices=["1", "2", "3", "4", "5", "tiny", "lce"],
+    ap.add_argument("--config", default="5", choices=["1", "2", "3", "4", "5", "tiny", "lce", "gemm"],
                     help="4, 5, tiny: the training step; 1, 2, 3: the single-op configurations (relu(matmul) f32, "
                          "the fused elementwise/norm/softmax chain, flash attention forward + backward); lce: the "
-                         "config-5 eval loss, fused linear cross entropy against unfused")
+                         "config-5 eval loss, fused linear cross entropy against unfused; gemm: one nhip_gemm call")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--attn-shape", default="8,2048,16,128", help="config 3: B,S,N,D of the attention")
     ap.add_argument("--attn-config", type=int, default=-1, help="config 3: the forward tile config (-1 default)")
+    ap.add_argument("--gemm-shape", default="8192,8192,8192", help="gemm: m,n,k")
+    ap.add_argument("--gemm-config", type=int, default=-1, help="gemm: the tile config (-1 default)")
+    ap.add_argument("--gemm-out", default="f32", choices=["f32", "bf16"], help="gemm: the output dtype")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     ap.add_argument("--probe", action="store_true",
                     help="after the measurement, replay the dominant step alone 3 times and a 1 GiB device copy 3 "
@@ -516,6 +519,56 @@ def _attn_cpu(b, s, n, d, sl=256):
                       f"in the C oracle (1 thread), scaled by (S/{sl})^2 x B x N and x3.5 for forward + backward"}
 
 
+def _config_gemm(args):
+    """One dot through the C ABI (nhip_gemm) at ``--gemm-shape m,n,k`` (A [m, k] and B [n, k] k-contiguous bf16,
+    D [m, n] float32 or with ``--gemm-out bf16``) and tile config ``--gemm-config`` (-1: the default pick): the
+    GEMM kernels measured alone, for comparing k loops and for counter runs. Not a BASELINE configuration."""
+    import ctypes as C
+
+    import numpy as np
+
+    from lumen_amd import native as nv
+    from lumen_amd.tensor import DeviceBuffer
+
+    m, n, k = (int(x) for x in args.gemm_shape.split(","))
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal(m * k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    b = (rng.standard_normal(n * k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    out = nv.NHIP_BF16 if args.gemm_out == "bf16" else nv.NHIP_F32
+    da, db = DeviceBuffer(0, a.nbytes), DeviceBuffer(0, b.nbytes)
+    dd = DeviceBuffer(0, m * n * (2 if out == nv.NHIP_BF16 else 4))
+    nv.h2d(da.ptr, a.ctypes.data, a.nbytes)
+    nv.h2d(db.ptr, b.ctypes.data, b.nbytes)
+    g = nv.GemmDesc()
+    g.m, g.n, g.k, g.nbatch = m, n, k, 0
+    g.a_dtype = g.b_dtype = nv.NHIP_BF16
+    g.d_dtype = out
+    g.a_m, g.a_k, g.b_k, g.b_n, g.d_m, g.d_n = k, 1, 1, k, n, 1
+    g.config, g.splits = args.gemm_config, 0
+
+    def call():
+        nv.call("nhip_gemm", C.byref(g), da.ptr, db.ptr, dd.ptr)
+
+    for _ in range(max(1, args.warmup)):
+        call()
+    nv.sync()
+    e0, e1 = nv.Event(), nv.Event()
+    e0.record()
+    for _ in range(args.steps):
+        call()
+    e1.record()
+    nv.sync()
+    ms = e0.elapsed_ms(e1) / args.steps
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": f"nhip_gemm config {args.gemm_config}",
+            "per_launch": {"flops": 2 * m * n * k, "bytes": (m + n) * k * 2 + m * n * (2 if out == nv.NHIP_BF16 else 4),
+                           "ms": round(ms, 4)}}
+    return _op_line(args, "gemm TFLOP/s", ms, tf, "TFLOP/s",
+                    {"workload": f"gemm [{m}, {k}] x [{n}, {k}]^T -> {args.gemm_out}, config {args.gemm_config}"},
+                    roof, None, "bf16")
+
+
 def _config_lce(args):
     """The eval loss mean(cross_entropy(h . w^T, t)) at the config-5 head's shapes (h [16384, 2048], w [32000,
     2048] bf16, int64 targets): the linear_cross_entropy step (the fused GEMM store reduction and its merge)
@@ -580,7 +633,7 @@ def _config_lce(args):
                      "loss": loss[True], "loss_unfused": loss[False]})
 
 
-OP_CONFIGS = {"1": _config1, "2": _config2, "3": _config3, "lce": _config_lce}
+OP_CONFIGS = {"1": _config1, "2": _config2, "3": _config3, "lce": _config_lce, "gemm": _config_gemm}
 
 
 def _traffic(kernel, config):
