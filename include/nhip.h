@@ -156,6 +156,8 @@ typedef struct {
                                     1 = dQ = dS K from the 16-bit dS tiles the dK/dV kernel stores in the workspace
                                     (same bits every run); 2 = by a kernel recomputing S and dP (same bits every
                                     run, no dS workspace) */
+    int64_t value_head_dim;      /* V's, O's and dO's head dim Hv (0: H), a multiple of 8 like H; the forward.rs
+                                    `hv` (passes/attention/forward.rs:721) */
 } nhip_attn_desc;
 
 /* O = softmax(scale Q K^T [causal]) V, P rounded to the inputs' dtype before P V; writes LSE = m + log l

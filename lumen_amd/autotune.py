@@ -75,9 +75,9 @@ class HipAttentionConfig:
         return [HipAttentionConfig(w) for w in HipAttentionConfig.WAVES]
 
     def fits(self, h: int, hv: int) -> bool:
-        """Whether the flash forward takes query/key head dim ``h`` and value head dim ``hv`` (a multiple of 8 up
-        to 256, the value head dim equal to it)."""
-        return 0 < h <= 256 and h % 8 == 0 and hv == h
+        """Whether the flash forward takes query/key head dim ``h`` and value head dim ``hv`` (each a multiple of 8
+        up to 256)."""
+        return all(0 < d <= 256 and d % 8 == 0 for d in (h, hv))
 
     def key(self):
         return ("attention", self.waves)

@@ -268,7 +268,7 @@ def match_forward(g: Graph):
         vb, vf, vc = _dims_of_dot(d2, 1, vt)
         if len(qf) != 1 or len(kf) != 1 or len(vf) != 1 or not _head_dim_ok(qt.shape[qc[0]], MAX_HEAD):
             continue
-        if vt.shape[vf[0]] != qt.shape[qc[0]]:
+        if not _head_dim_ok(vt.shape[vf[0]], MAX_HEAD):  # the value head dim may differ from the query's
             continue
         # grouped heads: the kernel reads the key/value heads themselves (head n reads head n / G)
         k_in, k_exp = _unexpand(G, d1.inputs[1], kb)
@@ -365,8 +365,10 @@ def match_backward(g: Graph):
         qt = g.types[q]
         if qt.dtype not in ("bfloat16", "float16") or len(qt.shape) != 4 or not _head_dim_ok(qt.shape[3], MAX_BACKWARD_HEAD):
             continue
-        if any(len(g.types[x].shape) != 4 or g.types[x].shape[3] != qt.shape[3] for x in (k, v, o, do)):
-            continue  # the kernels take one head dim for Q, K, V and dO
+        hv = g.types[v].shape[3] if len(g.types[v].shape) == 4 else 0
+        if (len(g.types[k].shape) != 4 or g.types[k].shape[3] != qt.shape[3] or not _head_dim_ok(hv, MAX_BACKWARD_HEAD)
+                or any(len(g.types[x].shape) != 4 or g.types[x].shape[3] != hv for x in (o, do))):
+            continue  # one head dim for Q and K, one for V, O and dO
         if any(tuple(x.params["rhs_batch"]) != (0, 2) for x in (dv, dk, dq)):
             continue
         # grouped heads: K and V expanded to every query head, dK and dV summed over each group
@@ -568,6 +570,7 @@ def lower(plan, step):
         a.batch, a.heads = qt.shape[qb[0]], qt.shape[qb[1]]
         a.kv_heads = g.types[k].shape[kb[1]]
         a.sq, a.sk, a.head_dim = qt.shape[qs], g.types[k].shape[ks], qt.shape[qd]
+        a.value_head_dim = g.types[v].shape[vd]
         a.dtype = 1 if qt.dtype == "bfloat16" else 2
         _need_unit(ql, qd, kl, kd, vl, vd)
         a.q_b, a.q_n, a.q_s = ql.strides[qb[0]], ql.strides[qb[1]], ql.strides[qs]
@@ -585,6 +588,7 @@ def lower(plan, step):
     ls = {x: loc[x] for x in (q, k, v, o, do, lse)}
     a.batch, a.sq, a.heads, a.head_dim = qt.shape
     a.sk, a.kv_heads = kt.shape[1], kt.shape[2]
+    a.value_head_dim = g.types[v].shape[3]
     a.dtype = 1 if qt.dtype == "bfloat16" else 2
     for name, x in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do)):
         l_ = ls[x]
@@ -635,7 +639,7 @@ def ds_bytes(batch, heads, sq, sk) -> int:
     return batch * heads * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2
 
 
-def backward_workspace_bytes(b, nh, sq, sk, hd, kvh, mode) -> int:
+def backward_workspace_bytes(b, nh, sq, sk, hd, kvh, mode, hdv=0) -> int:
     """Workspace bytes of nhip_flash_bwd for these sizes and mode, as the library itself reports them
     (nhip_flash_bwd_workspace), so the plan's scratch can never be smaller than what the kernels write."""
     import ctypes as C
@@ -644,6 +648,7 @@ def backward_workspace_bytes(b, nh, sq, sk, hd, kvh, mode) -> int:
 
     a = nv.AttnDesc()
     a.batch, a.sq, a.sk, a.heads, a.kv_heads, a.head_dim = b, sq, sk, nh, kvh, hd
+    a.value_head_dim = hdv
     a.deterministic = mode
     n = C.c_size_t()
     nv.call("nhip_flash_bwd_workspace", C.byref(a), C.byref(n))

@@ -273,7 +273,8 @@ def fuse(graph: Graph, fuse_loops=True, packed=frozenset()) -> list:
                     b, sq, nh, hd = q.shape
                     sk, kvh = graph.types[node.inputs[1]].shape[1:3]
                     st.mode = backward_mode(b, nh, sq, sk)
-                    st.scratch = backward_workspace_bytes(b, nh, sq, sk, hd, kvh, st.mode)
+                    hdv = graph.types[node.inputs[2]].shape[3]
+                    st.scratch = backward_workspace_bytes(b, nh, sq, sk, hd, kvh, st.mode, hdv)
                 elif len(outs) == 1:
                     st.scratch = graph.types[outs[0]].numel() // graph.types[outs[0]].shape[-1] * 4
         elif kinds[k] in ("view", "reduce"):

@@ -70,7 +70,8 @@ struct AttnParams {
     float *dqacc;  // float32 [B, N, Sq, D] dQ accumulated atomically by the dK/dV kernel (null: deterministic)
     uint16_t *ds;  // dS tiles [B, N, Sk / 128, Sq / 64][128 keys][64 queries] the dK/dV kernel stores (or null)
     int64_t sq, sk, heads, kv_heads, batch;
-    int64_t hd;  // the operands' head dim; the kernels run at D >= hd (head_dim_of) with columns hd.. read as zeros
+    int64_t hd, hdv;  // Q/K's and V/O/dO's head dims; the kernels run at D >= both (kernel_head_dim), columns past
+                      // them read as zeros
     int64_t q_b, q_s, q_n, k_b, k_s, k_n, v_b, v_s, v_n, o_b, o_s, o_n;
     int64_t do_b, do_s, do_n, dq_b, dq_s, dq_n, dk_b, dk_s, dk_n, dv_b, dv_s, dv_n;
     float scale;
@@ -126,12 +127,23 @@ __device__ __forceinline__ int kv_off(int r, int col) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Zeros `elems` 16-bit elements of LDS (a multiple of 8) when the kernel's tiles can be partial (rows past the
+// operand's end, or a head dim padded to D), so that the chunks load_tile_async leaves unloaded hold zeros rather
+// than what an earlier kernel left there; every thread takes part, and a barrier follows.
+__device__ __forceinline__ void zero_tiles(uint16_t *p, int elems, bool partial) {
+    if (!partial) return;
+    for (int i = int(threadIdx.x) * 8; i < elems; i += int(blockDim.x) * 8)
+        *reinterpret_cast<uint4 *>(p + i) = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+}
+
 // Issues the loads of rows [k0, k0 + 64) of a [*, D] operand (row stride `rs` elements, `rows` rows) into
 // the swizzled tile `dst`. When the operand spans less than 2^31 bytes the loads are buffer loads (the row
-// offset a uniform operand, the lane's offset fixed) and rows past `rows` read zeros; otherwise 64-bit global
-// loads with rows past `rows` clamped to the last row. Either way those rows' scores are masked. Columns from
-// `cols` on (a head dim padded to D) read zeros: the buffer path takes an offset past the buffer's end there
-// (the launcher checks that padded operands take that path).
+// offset a uniform operand, the lane's offset fixed); otherwise 64-bit global loads with rows past `rows`
+// clamped to the last row. On the buffer path the lanes of rows past `rows` and of columns from `cols` on (a
+// head dim padded to D; the launcher checks that padded operands take this path) issue no load: their LDS
+// chunks keep what they held, which zero_tiles set to zeros when the kernel started (or an earlier tile's
+// finite values). Rows past `rows` have their scores masked; padded columns meet zeros in the other operand.
 template <int D, int NW = 4>
 __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs, int64_t k0, int64_t rows,
                                                 uint16_t *dst, int wave, int lane, int64_t cols = D) {
@@ -146,8 +158,9 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
             const int r = seg * RPS + lane / (D / 8);
             const int c = lane % (D / 8);
             const int sc = c ^ kv_swz<D>(r);
-            const uint32_t vo = 8 * sc < cols ? uint32_t((r * rs + (sc << 3)) * 2) : 0x80000000u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(dst + seg * 512), 16, vo, so, 0, 0);
+            const uint32_t vo = uint32_t((r * rs + (sc << 3)) * 2);
+            if (8 * sc < cols && k0 + r < rows)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(dst + seg * 512), 16, vo, so, 0, 0);
         }
         return;
     }
@@ -204,9 +217,10 @@ __global__ __launch_bounds__(64 * NW, (FwdOccupancy<NW, D>::kBlocks)) void flash
     if (CAUSAL) full_end = min(full_end, q0 + shift + 1);
     const int nfull = full_end > 0 ? int(full_end / BN) : 0;
 
+    zero_tiles(smem, 4 * TILE, p.sk % BN || p.hd < D || p.hdv < D);
     if (ntiles > 0) {
         load_tile_async<D, NW>(kp, p.k_s, 0, p.sk, smem, wave, lane, p.hd);
-        load_tile_async<D, NW>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hd);
+        load_tile_async<D, NW>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hdv);
     }
 
     uint4 qf[DS];
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(64 * NW, (FwdOccupancy<NW, D>::kBlocks)) void flash
         if (kt + 1 < ntiles) {
             uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
             load_tile_async<D, NW>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane, p.hd);
-            load_tile_async<D, NW>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hd);
+            load_tile_async<D, NW>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hdv);
         }
         if (CAUSAL && k0 > wq_last + shift) continue;  // every key of the tile is masked for this wave
         const char *Kb = reinterpret_cast<const char *>(Ks);
@@ -314,7 +328,7 @@ __global__ __launch_bounds__(64 * NW, (FwdOccupancy<NW, D>::kBlocks)) void flash
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-            if (32 * dt + 8 * e4 >= p.hd) continue;  // padded columns
+            if (32 * dt + 8 * e4 >= p.hdv) continue;  // padded columns
             const uint32_t w0 = pack2<F16>(acc[dt][4 * e4 + 0] * inv, acc[dt][4 * e4 + 1] * inv);
             const uint32_t w1 = pack2<F16>(acc[dt][4 * e4 + 2] * inv, acc[dt][4 * e4 + 3] * inv);
             *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * e4 + 4 * h) = make_uint2(w0, w1);
@@ -346,7 +360,7 @@ __global__ __launch_bounds__(256) void flash_prep_kernel(AttnParams p, float *ls
     const uint16_t *o = p.o_in + b * p.o_b + n * p.o_n + q * p.o_s;
     const uint16_t *g = p.d_o + b * p.do_b + n * p.do_n + q * p.do_s;
     float acc = 0.0f;
-    for (int d = lane; d < p.hd; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
+    for (int d = lane; d < p.hdv; d += 64) acc += half_to_f32<F16>(g[d]) * half_to_f32<F16>(o[d]);
     acc = wave_sum(acc);
     const int64_t i = (b * p.heads + n) * p.sq + q;
     if (p.dqacc)  // the row of the atomic dQ accumulator starts at zero
@@ -453,6 +467,8 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
     int64_t unit, pidx;
     xcd_order(int64_t(gridDim.x) / per, per, unit, pidx);
     const int64_t b = unit / p.kv_heads, nkv = unit % p.kv_heads;
+    zero_tiles(smem, ATOMIC_DQ ? DkdvLds<D>::kBase + 128 * D : DkdvLds<D>::kBase,
+               p.sq % BM || (ATOMIC_DQ && p.sk % 128) || p.hd < D || p.hdv < D);
     for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
     const int64_t kblk = pass == 0 ? pidx : nkb - 1 - pidx;
     if (pass == 1) {
@@ -491,7 +507,7 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
         tile_src(j, qp, gp, ls, dl, q0);
         uint16_t *dst = smem + (j & 1) * 2 * TILE;
         load_tile_async<D>(qp, p.q_s, q0, p.sq, dst, wave, lane, p.hd);
-        load_tile_async<D>(gp, p.do_s, q0, p.sq, dst + TILE, wave, lane, p.hd);
+        load_tile_async<D>(gp, p.do_s, q0, p.sq, dst + TILE, wave, lane, p.hdv);
         if (wave == 0) load_row64_async(ls, q0, p.sq, Ls[j & 1], lane);
         if (wave == 1) load_row64_async(dl, q0, p.sq, Dl[j & 1], lane);
     };
@@ -526,9 +542,10 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
     uint4 kf[DS], vf[DS];
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
-        const bool in = kvalid && 16 * t + 8 * h < p.hd;
-        kf[t] = in ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        vf[t] = in ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        kf[t] = kvalid && 16 * t + 8 * h < p.hd ? *reinterpret_cast<const uint4 *>(kp + kj * p.k_s + 16 * t + 8 * h)
+                                                : make_uint4(0, 0, 0, 0);
+        vf[t] = kvalid && 16 * t + 8 * h < p.hdv ? *reinterpret_cast<const uint4 *>(vp + kj * p.v_s + 16 * t + 8 * h)
+                                                 : make_uint4(0, 0, 0, 0);
     }
     f32x16_t adk[DT], adv[DT];
 #pragma unroll
@@ -773,11 +790,12 @@ __global__ __launch_bounds__(256) void flash_dkdv_kernel(AttnParams p, const flo
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
             const int d = 32 * dt + 8 * e4 + 4 * h;
-            if (32 * dt + 8 * e4 >= p.hd) continue;  // padded columns
-            *reinterpret_cast<uint2 *>(dkp + d) =
-                make_uint2(pack2<F16>(adk[dt][4 * e4], adk[dt][4 * e4 + 1]), pack2<F16>(adk[dt][4 * e4 + 2], adk[dt][4 * e4 + 3]));
-            *reinterpret_cast<uint2 *>(dvp + d) =
-                make_uint2(pack2<F16>(adv[dt][4 * e4], adv[dt][4 * e4 + 1]), pack2<F16>(adv[dt][4 * e4 + 2], adv[dt][4 * e4 + 3]));
+            if (32 * dt + 8 * e4 < p.hd)  // padded columns are not stored
+                *reinterpret_cast<uint2 *>(dkp + d) =
+                    make_uint2(pack2<F16>(adk[dt][4 * e4], adk[dt][4 * e4 + 1]), pack2<F16>(adk[dt][4 * e4 + 2], adk[dt][4 * e4 + 3]));
+            if (32 * dt + 8 * e4 < p.hdv)
+                *reinterpret_cast<uint2 *>(dvp + d) =
+                    make_uint2(pack2<F16>(adv[dt][4 * e4], adv[dt][4 * e4 + 1]), pack2<F16>(adv[dt][4 * e4 + 2], adv[dt][4 * e4 + 3]));
         }
     }();
     }
@@ -899,6 +917,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_ds_kernel(AttnParams p) {
             }
         }
     };
+    zero_tiles(smem, 3 * KSTAGE, p.sk % KT || p.hd < D);
     if (nk > 0) {
         issue_k(std::integral_constant<int, 0>{}, 0);
         issue_ds(std::integral_constant<int, 0>{}, 0);
@@ -966,17 +985,19 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
     int64_t full_end = p.sk;
     if (CAUSAL) full_end = min(full_end, q0 + shift + 1);
     const int nfull = full_end > 0 ? int(full_end / BN) : 0;
+    zero_tiles(smem, 4 * TILE, p.sk % BN || p.hd < D || p.hdv < D);
     if (ntiles > 0) {
         load_tile_async<D>(kp, p.k_s, 0, p.sk, smem, wave, lane, p.hd);
-        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hd);
+        load_tile_async<D>(vp, p.v_s, 0, p.sk, smem + TILE, wave, lane, p.hdv);
     }
 
     uint4 qf[DS], gf[DS];
 #pragma unroll
     for (int t = 0; t < DS; ++t) {
-        const bool in = qvalid && 16 * t + 8 * h < p.hd;
-        qf[t] = in ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
-        gf[t] = in ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h) : make_uint4(0, 0, 0, 0);
+        qf[t] = qvalid && 16 * t + 8 * h < p.hd ? *reinterpret_cast<const uint4 *>(qp + qi * p.q_s + 16 * t + 8 * h)
+                                                : make_uint4(0, 0, 0, 0);
+        gf[t] = qvalid && 16 * t + 8 * h < p.hdv ? *reinterpret_cast<const uint4 *>(gp + qi * p.do_s + 16 * t + 8 * h)
+                                                 : make_uint4(0, 0, 0, 0);
     }
     const float l2 = qvalid ? lse2[(b * p.heads + n) * p.sq + qi] : 0.0f;
     const float dl = qvalid ? p.delta[(b * p.heads + n) * p.sq + qi] : 0.0f;
@@ -994,7 +1015,7 @@ __global__ __launch_bounds__(256, 2) void flash_dq_kernel(AttnParams p, const fl
         if (kt + 1 < ntiles) {
             uint16_t *nk = smem + ((kt + 1) & 1) * 2 * TILE;
             load_tile_async<D>(kp, p.k_s, k0 + BN, p.sk, nk, wave, lane, p.hd);
-            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hd);
+            load_tile_async<D>(vp, p.v_s, k0 + BN, p.sk, nk + TILE, wave, lane, p.hdv);
         }
         if (CAUSAL && k0 > wq_last + shift) continue;
         const char *Kb = reinterpret_cast<const char *>(smem + (kt & 1) * 2 * TILE);
@@ -1073,6 +1094,12 @@ namespace nhip {
 // The head dim the kernels run at: 64, 128 or 256, the operands' own head dim (a multiple of 8) padded up to it
 // with zero columns.
 inline int64_t kernel_head_dim(int64_t hd) { return hd <= 64 ? 64 : hd <= 128 ? 128 : 256; }
+// V's (and O's, dO's) head dim: value_head_dim, or the query's when 0.
+inline int64_t value_head_dim(const nhip_attn_desc *d) { return d->value_head_dim ? d->value_head_dim : d->head_dim; }
+// The head dim the kernels run at for both.
+inline int64_t kernel_dim(const nhip_attn_desc *d) {
+    return kernel_head_dim(d->head_dim > value_head_dim(d) ? d->head_dim : value_head_dim(d));
+}
 
 inline size_t flash_bwd_dq_offset(const nhip_attn_desc *d) {
     return (2 * size_t(d->batch) * d->heads * d->sq * sizeof(float) + 255) / 256 * 256;
@@ -1083,7 +1110,7 @@ inline size_t flash_bwd_ds_bytes(const nhip_attn_desc *d) {
 inline size_t flash_bwd_workspace_bytes(const nhip_attn_desc *d) {
     if (d->deterministic == 2) return 2 * size_t(d->batch) * d->heads * d->sq * sizeof(float);
     if (d->deterministic == 1) return flash_bwd_dq_offset(d) + flash_bwd_ds_bytes(d);
-    return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * kernel_head_dim(d->head_dim) * sizeof(float);
+    return flash_bwd_dq_offset(d) + size_t(d->batch) * d->heads * d->sq * kernel_dim(d) * sizeof(float);
 }
 
 inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
@@ -1094,6 +1121,7 @@ inline nhipk::AttnParams attn_params(const nhip_attn_desc *d) {
     p.kv_heads = d->kv_heads;
     p.batch = d->batch;
     p.hd = d->head_dim;
+    p.hdv = value_head_dim(d);
     p.q_b = d->q_b, p.q_s = d->q_s, p.q_n = d->q_n;
     p.k_b = d->k_b, p.k_s = d->k_s, p.k_n = d->k_n;
     p.v_b = d->v_b, p.v_s = d->v_s, p.v_n = d->v_n;
@@ -1117,19 +1145,20 @@ inline bool attn_span_ok(int64_t rows, int64_t rs, int64_t hd) {
 }
 
 inline int check_attn(const nhip_attn_desc *d, const char *what, int64_t max_hd = 128) {
-    if (d->head_dim <= 0 || d->head_dim % 8 || d->head_dim > max_hd)
-        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) +
-                    " (the hip kernels take multiples of 8 up to " + std::to_string(max_hd) + ")");
+    for (int64_t hd : {d->head_dim, value_head_dim(d)})
+        if (hd <= 0 || hd % 8 || hd > max_hd)
+            return fail(std::string(what) + ": head dim " + std::to_string(hd) +
+                        " (the hip kernels take multiples of 8 up to " + std::to_string(max_hd) + ")");
     for (int64_t st : {d->q_b, d->q_s, d->q_n, d->k_b, d->k_s, d->k_n, d->v_b, d->v_s, d->v_n, d->o_b, d->o_s, d->o_n,
                        d->do_b, d->do_s, d->do_n, d->dq_b, d->dq_s, d->dq_n, d->dk_b, d->dk_s, d->dk_n, d->dv_b, d->dv_s,
                        d->dv_n})
         if (st % 8) return fail(std::string(what) + ": every stride must be a multiple of 8 elements (16-byte rows)");
-    if (d->head_dim != kernel_head_dim(d->head_dim) &&
+    const int64_t hv = value_head_dim(d), kd = kernel_dim(d);
+    if ((d->head_dim != kd || hv != kd) &&
         !(attn_span_ok(d->sq, d->q_s, d->head_dim) && attn_span_ok(d->sk, d->k_s, d->head_dim) &&
-          attn_span_ok(d->sk, d->v_s, d->head_dim) && attn_span_ok(d->sq, d->o_s, d->head_dim) &&
-          attn_span_ok(d->sq, d->do_s, d->head_dim)))
-        return fail(std::string(what) + ": head dim " + std::to_string(d->head_dim) + " is padded to " +
-                    std::to_string(kernel_head_dim(d->head_dim)) + ", which needs each (batch, head) of an operand within 2 GiB");
+          attn_span_ok(d->sk, d->v_s, hv) && attn_span_ok(d->sq, d->o_s, hv) && attn_span_ok(d->sq, d->do_s, hv)))
+        return fail(std::string(what) + ": head dims " + std::to_string(d->head_dim) + " / " + std::to_string(hv) +
+                    " are padded to " + std::to_string(kd) + ", which needs each (batch, head) of an operand within 2 GiB");
     if (d->dtype != NHIP_BF16 && d->dtype != NHIP_F16) return fail(std::string(what) + ": bf16 or f16 operands only");
     if (d->kv_heads <= 0 || d->heads % d->kv_heads) return fail(std::string(what) + ": heads must be a multiple of kv_heads");
     if (d->deterministic < 0 || d->deterministic > 2)
@@ -1177,7 +1206,7 @@ int flash_fwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.lse = lse;
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_FWD(DD, FF, CC) return launch_fwd<DD, FF, CC>(s, p, d)
-    const int64_t kd = kernel_head_dim(d->head_dim);
+    const int64_t kd = kernel_dim(d);
     if (kd == 256) {
         if (f16) { if (d->causal) NHIP_FWD(256, true, true); NHIP_FWD(256, true, false); }
         if (d->causal) NHIP_FWD(256, false, true);
@@ -1205,7 +1234,7 @@ int launch_bwd(hipStream_t s, const nhipk::AttnParams &p, const nhip_attn_desc *
     dim3 gq(unsigned((d->sq + 127) / 128 * d->heads * d->batch));
     float *lse2 = p.delta + size_t(d->batch) * d->heads * d->sq;
     // 16-byte rows: D / 8 lanes each; else one wavefront a row
-    const bool vec = d->head_dim == D && D % 8 == 0 && 64 % (D / 8 > 0 ? D / 8 : 1) == 0 && D / 8 <= 64 &&
+    const bool vec = d->head_dim == D && value_head_dim(d) == D && D % 8 == 0 && 64 % (D / 8 > 0 ? D / 8 : 1) == 0 && D / 8 <= 64 &&
                      ((reinterpret_cast<uintptr_t>(p.o_in) | reinterpret_cast<uintptr_t>(p.d_o)) & 15) == 0 &&
                      (p.o_b | p.o_n | p.o_s | p.do_b | p.do_n | p.do_s) % 8 == 0;
     if constexpr (D % 8 == 0 && D >= 8 && D <= 512 && 64 % (D / 8) == 0) {
@@ -1260,7 +1289,7 @@ int flash_bwd_on(hipStream_t s, const nhip_attn_desc *d, const void *q, const vo
     p.ds = d->deterministic == 1 ? reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + flash_bwd_dq_offset(d)) : nullptr;
     bool f16 = d->dtype == NHIP_F16;
 #define NHIP_BWD(DD, FF, CC) return launch_bwd<DD, FF, CC>(s, p, d)
-    if (kernel_head_dim(d->head_dim) == 128) {
+    if (kernel_dim(d) == 128) {
         if (f16) { if (d->causal) NHIP_BWD(128, true, true); NHIP_BWD(128, true, false); }
         if (d->causal) NHIP_BWD(128, false, true);
         NHIP_BWD(128, false, false);

@@ -80,6 +80,7 @@ class AttnDesc(C.Structure):
         ("config", C.c_int32),
     ] + [(f"{t}_{a}", C.c_int64) for t in ("q", "k", "v", "o", "do", "dq", "dk", "dv") for a in ("b", "s", "n")] + [
         ("deterministic", C.c_int32),
+        ("value_head_dim", C.c_int64),
     ]
 
 

@@ -17,7 +17,8 @@ def test_config_classes_and_candidates():
     with pytest.raises(ValueError):
         A.HipAttentionConfig(waves=3)
     assert attn[0].fits(128, 128) and attn[0].fits(32, 32) and attn[0].fits(256, 256) and attn[0].fits(96, 96)
-    assert not attn[0].fits(64, 128) and not attn[0].fits(20, 20) and not attn[0].fits(264, 264)
+    assert attn[0].fits(64, 128) and not attn[0].fits(20, 20) and not attn[0].fits(264, 264)
+    assert not attn[0].fits(64, 12)
 
 
 def test_use_blocks_nest_and_key_plans():

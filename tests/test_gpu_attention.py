@@ -259,3 +259,57 @@ def test_config3_full_size_slices_match_float64_attention(hip, deterministic):
         if i < 2:
             for name, a, w in zip(("dq", "dk", "dv"), got_g, (dq64, dk64, dv64)):
                 close(a[bi, :, ni, :], w, name)
+
+
+@pytest.mark.parametrize("d,dv,sq,sk,causal", [(16, 24, 5, 40, False), (32, 32, 70, 100, True), (96, 64, 64, 192, True),
+                                               (64, 64, 40, 40, True)])
+def test_partial_tiles_ignore_what_earlier_kernels_left_in_lds(hip, d, dv, sq, sk, causal):
+    """The LDS chunks a partial tile leaves unloaded (rows past the sequence end, columns past a padded head
+    dim) must not carry values an earlier kernel left in LDS: a forward and backward over all-NaN operands run
+    first on every CU, then the partial shapes (value head dim apart from the query's included) in every dQ
+    mode, checked finite and against the oracle."""
+    nb, ns, nn = 8, 2048, 16  # poison: NaN Q, K, V and dO through the same kernels on every CU
+    nanq = np.full((nb, ns, nn, 128), 0x7FC0, np.uint16)
+    pq, po, pl = Dev(nanq), Dev(nbytes=nanq.nbytes), Dev(nbytes=nb * nn * ns * 4)
+    pdesc = attn_desc(nb, ns, ns, nn, nn, 128, True, 0.1)
+    nv.call("nhip_flash_fwd", C.byref(pdesc), pq.ptr, pq.ptr, pq.ptr, po.ptr, pl.ptr)
+    rng = np.random.default_rng(d + dv + sk)
+    b, n = 2, 2
+    q, k = (D.bf16_bits(rng.standard_normal(s).astype(np.float32)) for s in ((b, sq, n, d), (b, sk, n, d)))
+    v, g = (D.bf16_bits(rng.standard_normal(s).astype(np.float32)) for s in ((b, sk, n, dv), (b, sq, n, dv)))
+    meta = [L.empty(list(x.shape), "bfloat16", "meta") for x in (q, k, v, g)]
+
+    def grads(q, k, v, do):
+        out, pull = L.vjp(lambda q, k, v: F.flash_attention(q, k, v, is_causal=causal), q, k, v)
+        return (out,) + pull(do)
+
+    want = oracle.values(L.make_graph(grads)(*meta), [q, k, v, g])
+    for mode in (1, 2, 0):
+        pws = C.c_size_t()
+        pdesc.deterministic = mode
+        nv.call("nhip_flash_bwd_workspace", C.byref(pdesc), C.byref(pws))
+        pw = Dev(nbytes=pws.value)
+        pg = Dev(nbytes=nanq.nbytes)
+        nv.call("nhip_flash_bwd", C.byref(pdesc), pq.ptr, pq.ptr, pq.ptr, po.ptr, pq.ptr, pl.ptr, pg.ptr, pg.ptr,
+                pg.ptr, pw.ptr)
+        desc = attn_desc(b, sq, sk, n, n, d, causal, 1.0 / math.sqrt(d), deterministic=mode)
+        desc.value_head_dim = dv
+        for t in ("v", "o", "do", "dv"):
+            rows = sk if t in ("v", "dv") else sq
+            setattr(desc, f"{t}_b", rows * n * dv)
+            setattr(desc, f"{t}_s", n * dv)
+            setattr(desc, f"{t}_n", dv)
+        dq_, dk_, dv_, dg = Dev(q), Dev(k), Dev(v), Dev(g)
+        o, lse = Dev(nbytes=g.nbytes), Dev(nbytes=b * n * sq * 4)
+        nv.call("nhip_flash_fwd", C.byref(desc), dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr)
+        ws_bytes = C.c_size_t()
+        nv.call("nhip_flash_bwd_workspace", C.byref(desc), C.byref(ws_bytes))
+        ws = Dev(nbytes=ws_bytes.value)
+        gq, gk, gv = Dev(nbytes=q.nbytes), Dev(nbytes=k.nbytes), Dev(nbytes=v.nbytes)
+        print("partial tiles", d, dv, sq, sk, causal, "mode", mode, flush=True)
+        nv.call("nhip_flash_bwd", C.byref(desc), dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, dg.ptr, lse.ptr, gq.ptr, gk.ptr,
+                gv.ptr, ws.ptr)
+        got = [D.bf16_to_f32(t.get(x.shape, np.uint16)) for t, x in ((o, g), (gq, q), (gk, k), (gv, v))]
+        for name, a, w in zip(("o", "dq", "dk", "dv"), got, want):
+            assert np.isfinite(a).all(), (name, mode)
+            np.testing.assert_allclose(a, w, rtol=2e-2, atol=1e-2 * max(1.0, np.abs(w).max()), err_msg=f"{name} {mode}")

@@ -2,8 +2,8 @@
 ``:354-359`` backward) compiled for hip: grouped heads, one query row, fewer keys than queries, head dims
 16/24/32/64/128 with a value head dim different from the query's, plus head dims 24, 40, 96 and 256. Shapes the
 flash kernels take (a head dim that is a multiple of 8, up to 256 forward and 128 backward, as
-``passes/attention/forward.rs:100,725`` and ``backward.rs:86,473`` allow; equal value head dim; no query row left
-without keys) run as flash steps; the others run the unfused dot / row-softmax plan. Both are checked against
+``passes/attention/forward.rs:100,725`` and ``backward.rs:86,473`` allow, the value head dim checked on its own;
+no query row left without keys) run as flash steps; the others run the unfused dot / row-softmax plan. Both are checked against
 float64 attention at the reference's tolerances."""
 
 import numpy as np
@@ -30,6 +30,7 @@ CASES = [  # (b, sq, sk, n, nkv, h, hv), causal — test_attention.py:53-60
     ((1, 100, 100, 4, 2, 96, 96), True),
     ((2, 64, 70, 2, 2, 40, 40), False),
     ((1, 70, 90, 2, 1, 256, 256), True),
+    ((1, 96, 96, 2, 2, 64, 128), True),  # value head dim above the query's
 ]
 
 BACKWARD_CASES = [  # test_attention.py:354-359, plus two the hip flash backward takes
@@ -62,7 +63,7 @@ def reference(q, k, v, causal):
 
 def _flash_ok(case, limit=256):
     (b, sq, sk, n, nkv, h, hv), causal = case
-    return h % 8 == 0 and h <= limit and hv == h and not (causal and sk < sq)
+    return all(d % 8 == 0 and d <= limit for d in (h, hv)) and not (causal and sk < sq)
 
 
 def _tensors(dtype, *shapes, seed=0):

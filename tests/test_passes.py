@@ -254,9 +254,10 @@ def test_simplify_rewrites_keep_values_bit_for_bit(name):
         _same(g, s, seed)
 
 
-def test_attention_backward_with_a_different_value_head_dim_stays_unfused():
-    """A value head dim other than the query's (16 vs 24, one of the reference's backward cases) has no flash
-    kernel: neither the forward nor the backward is matched, and the values are unchanged."""
+def test_attention_with_a_different_value_head_dim_is_matched():
+    """A value head dim other than the query's (16 vs 24, one of the reference's backward cases,
+    ``passes/attention/forward.rs:721-735`` checks each head dim on its own): the forward and the backward become
+    flash fusions reading V, O and dO at head dim 24 and Q, K at 16; the values are unchanged."""
     def grads(q, k, v, do):
         out, pull = L.vjp(lambda q, k, v: F.flash_attention(q, k, v, is_causal=True), q, k, v)
         return (out,) + pull(do)
@@ -264,5 +265,5 @@ def test_attention_backward_with_a_different_value_head_dim_stays_unfused():
     metas = [L.empty(s, "bfloat16", "meta") for s in ([1, 3, 2, 16], [1, 50, 1, 16], [1, 50, 1, 24], [1, 3, 2, 24])]
     g = L.make_graph(grads)(*metas)
     m = attention.match(passes.frontend(g))
-    assert not [n for n in m.nodes if n.prim == "fusion"]
+    assert [n.params["name"] for n in m.nodes if n.prim == "fusion"] == ["flash_attention", "flash_attention_backward"]
     _same(g, m)

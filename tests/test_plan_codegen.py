@@ -401,3 +401,5 @@ def test_flash_backward_scratch_is_what_the_library_reports(mode, shape):
             1: -(-rows // 256) * 256 + b * n * (-(-sk // 128)) * (-(-sq // 64)) * 128 * 64 * 2,
             0: -(-rows // 256) * 256 + b * n * sq * (64 if d <= 64 else 128) * 4}[mode]
     assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode) == want
+    if d == 32 and mode == 0:  # a value head dim above the query's pads the accumulator to the larger one
+        assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode, 96) == want + b * n * sq * 64 * 4
