@@ -115,6 +115,8 @@ def main():
     ap.add_argument("--gemm-shape", default="8192,8192,8192", help="gemm: m,n,k")
     ap.add_argument("--gemm-config", type=int, default=-1, help="gemm: the tile config (-1 default)")
     ap.add_argument("--gemm-out", default="f32", choices=["f32", "bf16"], help="gemm: the output dtype")
+    ap.add_argument("--gemm-library", action="store_true",
+                    help="gemm: also time the vendor library (torch.mm) on the same shape, alternating with ours")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
     ap.add_argument("--probe", action="store_true",
                     help="after the measurement, replay the dominant step alone 3 times and a 1 GiB device copy 3 "
@@ -560,13 +562,44 @@ def _config_gemm(args):
     nv.sync()
     ms = e0.elapsed_ms(e1) / args.steps
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    extra = {}
+    if args.gemm_library:
+        # the vendor library on the same shape for comparison (torch.mm dispatches to hipBLASLt on ROCm): the
+        # same bf16 operands (B as [n, k], used transposed) and output dtype, calls alternated with ours
+        import torch
+
+        ta = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).reshape(m, k).to("cuda")
+        tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).reshape(n, k).to("cuda")
+        od = torch.float32 if out == nv.NHIP_F32 else torch.bfloat16
+        to = torch.empty(m, n, dtype=od, device="cuda")
+
+        def lib():
+            if od == torch.float32:
+                torch.mm(ta, tb.t(), out_dtype=torch.float32)  # aten::mm.dtype: bf16 operands, float32 output
+            else:
+                torch.mm(ta, tb.t(), out=to)
+
+        lib_ms, our_ms = [], []
+        for _ in range(3):
+            for fn, acc in ((lib, lib_ms), (call, our_ms)):
+                fn()
+                torch.cuda.synchronize()
+                nv.sync()
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    fn()
+                torch.cuda.synchronize()
+                nv.sync()
+                acc.append((time.perf_counter() - t0) * 1e3 / args.steps)
+        extra = {"library_ms": [round(x, 4) for x in lib_ms], "ours_ms": [round(x, 4) for x in our_ms],
+                 "library": f"torch.mm (hipBLASLt on ROCm), bf16 operands, {args.gemm_out} output"}
     roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": f"nhip_gemm config {args.gemm_config}",
             "per_launch": {"flops": 2 * m * n * k, "bytes": (m + n) * k * 2 + m * n * (2 if out == nv.NHIP_BF16 else 4),
                            "ms": round(ms, 4)}}
     return _op_line(args, "gemm TFLOP/s", ms, tf, "TFLOP/s",
                     {"workload": f"gemm [{m}, {k}] x [{n}, {k}]^T -> {args.gemm_out}, config {args.gemm_config}"},
-                    roof, None, "bf16")
+                    roof, None, "bf16", extra)
 
 
 def _config_lce(args):
