@@ -81,6 +81,19 @@ __device__ __forceinline__ void mfma_ds_interleave() {
     }
 }
 
+// The same with NV global loads (VMEM reads, the loads into LDS) spread between the MFMAs as well.
+template <int T, int M, int NR, int NV, int ID>
+__device__ __forceinline__ void mfma_ds_vmem_interleave() {
+    if constexpr (T < M) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, ID);
+        constexpr int r = NR * (T + 1) / M - NR * T / M;
+        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, ID);
+        constexpr int v = NV * (T + 1) / M - NV * T / M;
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, ID);
+        mfma_ds_vmem_interleave<T + 1, M, NR, NV, ID>();
+    }
+}
+
 // Scheduling constraint: N times {one MFMA, then R LDS reads} (sync id ID).
 template <int N, int R, int ID>
 __device__ __forceinline__ void mfma_then_ds() {

@@ -459,6 +459,8 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int h = lane >> 5, l32 = lane & 31, g = lane >> 4, s16 = lane & 15;
+    // one wave a SIMD (WN = 2): the wave index as a scalar, so the loads' LDS destinations are scalar arithmetic
+    const int wave_u = WN == 2 ? __builtin_amdgcn_readfirstlane(wave) : wave;
     const int64_t ks = int64_t(blockIdx.z) * s.k;  // split-k: this workgroup's first k
     od += int64_t(blockIdx.z) * s.d_split;
     const uint16_t *pa = a + oa + ks * s.a_k, *pb = b + ob + ks * s.b_k;
@@ -483,7 +485,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
 #pragma unroll
         for (int i = 0; i < TA::segs / NW; ++i) {
             if (i < lo || i >= hi) continue;
-            const int seg = wave + NW * i;
+            const int seg = wave_u + NW * i;
             const int line = seg * TA::lines_per_seg + lane / TA::chunks, c = lane % TA::chunks;
             if constexpr (buf) {
                 const uint32_t vo = AT ? uint32_t((line * s.a_k + ((c ^ mnmaj_swz(line)) << 3)) * 2)
@@ -507,7 +509,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
 #pragma unroll
         for (int i = 0; i < TB::segs / NW; ++i) {
             if (TA::segs / NW + i < lo || TA::segs / NW + i >= hi) continue;
-            const int seg = wave + NW * i;
+            const int seg = wave_u + NW * i;
             const int line = seg * TB::lines_per_seg + lane / TB::chunks, c = lane % TB::chunks;
             if constexpr (buf) {
                 const uint32_t vo = BT ? uint32_t((line * s.b_k + ((c ^ mnmaj_swz(line)) << 3)) * 2)
@@ -614,6 +616,10 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         // first k step of tile kt, into the stage the previous barrier freed.
         static_assert(STAGES >= 3, "cross-tile fragment prefetch needs a tile of loads in flight");
         constexpr int NSTEP = BK / 16;
+        // UNI (one wave a SIMD): every k tile issues its loads and waits the same way -- past the last tile the
+        // loads repeat the last tile into the free stage -- so the loop body is one basic block and the loads
+        // can be placed among the MFMAs
+        constexpr bool UNI = WN == 2;
         uint4 fa[2][FM], fb[2][FN];
         auto read = [&](const char *ta, int buf, int kk) {
             const char *tb = ta + TA::bytes;
@@ -632,8 +638,8 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         };
 #pragma unroll
         for (int st = 0; st < STAGES - 1; ++st)
-            if (st < ktiles) issue(st, st, 0, LPS);
-        wait_tiles(min(STAGES - 2, ktiles - 1));
+            if (UNI || st < ktiles) issue(st, UNI ? min(st, ktiles - 1) : st, 0, LPS);
+        wait_tiles(UNI ? STAGES - 2 : min(STAGES - 2, ktiles - 1));
         __syncthreads();
         read(smem, 0, 0);
         for (int kt = 0; kt < ktiles; ++kt) {
@@ -648,20 +654,24 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                 if constexpr (i + 1 < NSTEP) {
                     read(ta, cur ^ 1, 16 * (i + 1));
                 } else {
-                    if (next) {
-                        wait_tiles(min(STAGES - 2, ktiles - 2 - kt));  // tile kt + 1 landed (this thread)
-                        asm volatile("s_barrier" ::: "memory");           // ... every thread's; stage kt is free
+                    if (UNI || next) {
+                        wait_tiles(UNI ? STAGES - 2 : min(STAGES - 2, ktiles - 2 - kt));  // tile kt + 1 landed (this thread)
+                        asm volatile("s_barrier" ::: "memory");  // ... every thread's; stage kt is free
                         read(tn, cur ^ 1, 0);
                     }
                 }
                 if constexpr (i == 0) {
-                    if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+                    if (UNI || more)
+                        issue((kt + STAGES - 1) % STAGES, UNI ? min(kt + STAGES - 1, ktiles - 1) : kt + STAGES - 1, 0, LPS);
                 }
 #pragma unroll
                 for (int ii = 0; ii < FM; ++ii)
 #pragma unroll
                     for (int j = 0; j < FN; ++j) acc[ii][j] = Mfma<F16>::run(fb[cur][j], fa[cur][ii], acc[ii][j]);
-                mfma_ds_interleave<0, FM * FN, NRD, i + 1>();
+                if constexpr (WN == 2 && i == 0)  // one wave a SIMD: the loads go out among the MFMAs too
+                    mfma_ds_vmem_interleave<0, FM * FN, NRD, LPS, i + 1>();
+                else
+                    mfma_ds_interleave<0, FM * FN, NRD, i + 1>();
                 __builtin_amdgcn_sched_barrier(0);
             };
             step(std::integral_constant<int, 0>{});
@@ -671,6 +681,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                 step(std::integral_constant<int, 3>{});
             }
         }
+        if constexpr (UNI) __builtin_amdgcn_s_waitcnt(0x0070);  // the repeated loads land before LDS is reused
     } else {
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
@@ -701,7 +712,13 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             if constexpr (kk + 16 < BK) read(cur ^ 1, kk + 16);
             // the next stage's loads, a quarter (a half for BK 32) each k step: spread among the MFMAs
             // rather than issued in one burst after the barrier
-            if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
+            // (with one wave a SIMD, WN = 2, nothing else covers the loads' latency: all of them go out in the first
+            // k step, a whole k tile ahead of their use)
+            if constexpr (WN == 2 && TM == 256) {
+                if (kk == 0 && more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+            } else {
+                if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
+            }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll

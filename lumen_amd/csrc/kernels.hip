@@ -30,11 +30,12 @@ constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // gemm_stream128 (128 x 128 tiles, 4 waves of 64 x 64, 2 stages, two workgroups a CU); and
 // gemm_stream_persist (the 8-wave 256 x 256 kernel, one persistent workgroup a CU walking the tiles); and the
 // k tile 32, 8-wave kernel with its MFMA fragments read ahead across k tiles (gemm_stream_tile's XPF); and the
-// k tile 32, 8-wave kernel whose two waves a SIMD alternate memory and MFMA phases (ping-pong).
+// k tile 32, 8-wave kernel whose two waves a SIMD alternate memory and MFMA phases (ping-pong); and the k tile
+// 32, 4-wave (128 x 128 a wave) kernel with the cross-tile fragment prefetch.
 constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
               kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4, kStream8wX = kNumTiled + 5,
-              kStream8wP = kNumTiled + 6;
-constexpr int kNumConfigs = kNumTiled + 7;
+              kStream8wP = kNumTiled + 6, kStream4wX = kNumTiled + 7;
+constexpr int kNumConfigs = kNumTiled + 8;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -234,6 +235,7 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream8w32: return launch_stream<F16, 32, 4, AT, BT>(st, s, z, a, b, out, dtype);
         case kStream8wX: return launch_stream<F16, 32, 4, AT, BT, 1>(st, s, z, a, b, out, dtype);
         case kStream8wP: return launch_stream<F16, 32, 4, AT, BT, 2>(st, s, z, a, b, out, dtype);
+        case kStream4wX: return launch_stream<F16, 32, 2, AT, BT, 1>(st, s, z, a, b, out, dtype);
         case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case kStreamPersist: return launch_stream_persist<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
@@ -339,7 +341,7 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
         if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist) && d->k % 64) ||
-            ((cfg == kStream8w32 || cfg == kStream8wX || cfg == kStream8wP) && d->k % 32))
+            ((cfg == kStream8w32 || cfg == kStream8wX || cfg == kStream8wP || cfg == kStream4wX) && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
         return launch_mfma<false>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
