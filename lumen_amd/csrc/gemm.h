@@ -642,6 +642,56 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         wait_tiles(UNI ? STAGES - 2 : min(STAGES - 2, ktiles - 1));
         __syncthreads();
         read(smem, 0, 0);
+        if constexpr (UNI && NSTEP == 2) {
+            // Placed by hand, one MFMA at a time: each of the two k steps runs its FM x FN MFMAs with one fragment
+            // read after each of the first FM + FN (step 0: this tile's second k step; step 1: the next tile's
+            // first, once it has landed) and half of tile kt + STAGES - 1's loads spread LSTRIDE MFMAs apart.
+            // Step 1 waits and meets the other waves after BARPOS MFMAs rather than before its first, so the
+            // barrier's skew hides under MFMAs already issued.
+            constexpr int NM = FM * FN, NL = LPS / 2;
+            constexpr int BARPOS = 2, LSTART = 2;
+            constexpr int LSTRIDE = NL > 1 ? (NM - 1 - LSTART) / (NL - 1) < 3 ? (NM - 1 - LSTART) / (NL - 1) : 3 : 1;
+            static_assert(LPS % 2 == 0 && LSTART >= BARPOS && LSTRIDE >= 1 && LSTART + LSTRIDE * (NL - 1) < NM,
+                          "every load is issued, none of step 1's before its wait");
+            static_assert(BARPOS + FM + FN - 1 < NM, "every fragment read is issued");
+            // at step 1's wait: tiles kt + 2 .. kt + STAGES - 2 and the first half of tile kt + STAGES - 1 may fly
+            constexpr int LATER = (STAGES - 3) * LPS + NL;
+            static_assert(LATER < 64, "vmcnt holds 6 bits");
+            auto read1 = [&](const char *ta_, int buf, int kk, int q) {  // q-th fragment in read()'s order
+                const char *tb_ = ta_ + TA::bytes;
+                if (q == 0) fa[buf][0] = frag(ta_, wm * WR, kk, std::integral_constant<bool, AT>{});
+                else if (q <= FN) fb[buf][q - 1] = frag(tb_, wn * WCOLS + 32 * (q - 1), kk, std::integral_constant<bool, BT>{});
+                else fa[buf][q - FN] = frag(ta_, wm * WR + 32 * (q - FN), kk, std::integral_constant<bool, AT>{});
+            };
+            for (int kt = 0; kt < ktiles; ++kt) {
+                const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+                const char *tn = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
+                const int lst = (kt + STAGES - 1) % STAGES, lkt = min(kt + STAGES - 1, ktiles - 1);
+#pragma unroll
+                for (int t = 0; t < NM; ++t) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    acc[t / FN][t % FN] = Mfma<F16>::run(fb[0][t % FN], fa[0][t / FN], acc[t / FN][t % FN]);
+                    if (t < FM + FN) read1(ta, 1, 16, t);
+                    if (t >= LSTART && (t - LSTART) % LSTRIDE == 0 && (t - LSTART) / LSTRIDE < NL)
+                        issue(lst, lkt, (t - LSTART) / LSTRIDE, (t - LSTART) / LSTRIDE + 1);
+                }
+#pragma unroll
+                for (int t = 0; t < NM; ++t) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (t == BARPOS) {
+                        // tile kt + 1 landed (this thread), LDS reads done; then every thread's (stage kt is free)
+                        __builtin_amdgcn_s_waitcnt((LATER & 15) | ((LATER >> 4) << 14) | 0x0070);
+                        asm volatile("s_barrier" ::: "memory");
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    acc[t / FN][t % FN] = Mfma<F16>::run(fb[1][t % FN], fa[1][t / FN], acc[t / FN][t % FN]);
+                    if (t >= BARPOS && t - BARPOS < FM + FN) read1(tn, 0, 0, t - BARPOS);
+                    if (t >= LSTART && (t - LSTART) % LSTRIDE == 0 && (t - LSTART) / LSTRIDE < NL)
+                        issue(lst, lkt, NL + (t - LSTART) / LSTRIDE, NL + (t - LSTART) / LSTRIDE + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else
         for (int kt = 0; kt < ktiles; ++kt) {
             const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
             const char *tn = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
