@@ -137,6 +137,10 @@ def main():
     from lumen_amd import workloads as W
 
     if args.config in OP_CONFIGS:
+        if args.config == "gemm" and args.gemm_library:
+            import torch  # the library comparison: torch's HIP runtime starts before this library's
+
+            torch.cuda.init()
         native.set_device(0)
         out = OP_CONFIGS[args.config](args)
         print(json.dumps(out), flush=True)
