@@ -153,14 +153,25 @@ __device__ __forceinline__ void load_tile_async(const uint16_t *src, int64_t rs,
     if (bytes < (int64_t(1) << 31) && (k0 + 64) * rs * 2 < (int64_t(1) << 31)) {
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, int(bytes), 0x00020000);
         const uint32_t so = uint32_t(k0 * rs * 2);
-#pragma unroll
-        for (int seg = wave; seg < SEGS; seg += NW) {
+        // the wave index as a scalar: the segment, its LDS destination and the trip count are then uniform
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        constexpr int PER = (SEGS + NW - 1) / NW;
+        auto seg_load = [&](int i, bool masked) {
+            const int seg = wu + NW * i;
+            if (SEGS % NW != 0 && seg >= SEGS) return;
             const int r = seg * RPS + lane / (D / 8);
             const int c = lane % (D / 8);
             const int sc = c ^ kv_swz<D>(r);
             const uint32_t vo = uint32_t((r * rs + (sc << 3)) * 2);
-            if (8 * sc < cols && k0 + r < rows)
+            if (!masked || (8 * sc < cols && k0 + r < rows))
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)(dst + seg * 512), 16, vo, so, 0, 0);
+        };
+        if (k0 + 64 <= rows && cols >= D) {  // a whole tile: no lane is masked
+#pragma unroll
+            for (int i = 0; i < PER; ++i) seg_load(i, false);
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) seg_load(i, true);
         }
         return;
     }
