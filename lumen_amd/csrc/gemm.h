@@ -435,7 +435,8 @@ __device__ __forceinline__ void stage_acc(const f32x16_t (&acc)[FM][FN], int hal
 // functor called as out(row, col, float4, pre) with the float32 sums of four consecutive columns (col a
 // multiple of 4, within m x n) and pre = out.load(row, col), its other operands read ahead. `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
 // KL, the k loop: 0 fragments of the next k step read under the current step's MFMAs; 1 (XPF) that read also
-// across k tiles; 2 (ping-pong) the two waves of each SIMD alternate between a memory phase and an MFMA phase.
+// across k tiles; 2 (ping-pong) the two waves of each SIMD alternate between a memory phase and an MFMA phase;
+// 3 (k tile 64, two stages, four waves) the cross-tile read placed by hand with the loads split in halves.
 template <bool F16, int BK, int WN, bool AT, bool BT, bool BUF, class Out, int TM = 256, int KL = 0>
 __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint16_t *__restrict__ a,
                                                  const uint16_t *__restrict__ b, const Out &out, char *smem) {
@@ -557,7 +558,64 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     constexpr bool XPF = KL == 1;
-    if constexpr (KL == 2) {
+    if constexpr (KL == 3) {
+        // k tile 64 (128-byte row segments: one L2 request a 128-byte line instead of two for k tile 32), two
+        // stages, one wave a SIMD, placed by hand one MFMA at a time. Each tile's loads go out in two halves: A
+        // of tile kt + 2 in tile kt's last k step, right after the barrier that frees its stage, B in tile
+        // kt + 1's first k step. Each k step reads the next one's fragments after its first FM + FN MFMAs; the
+        // last waits for all of tile kt + 1, meets the barrier after BARPOS MFMAs and reads tile kt + 1's first
+        // fragments under its own MFMAs. Past the last tile the loads repeat it into the free stage, so every
+        // tile runs the same straight-line body.
+        static_assert(STAGES == 2 && BK == 64 && WN == 2, "two stages of k 64 on four waves");
+        constexpr int NSTEP = BK / 16, NM = FM * FN, NL = LPS / 2;
+        constexpr int BARPOS = 2, L0 = 1, S0 = 2, L3 = 4, S3 = 1;
+        static_assert(NL == TA::segs / NW, "the halves are A's and B's loads");
+        static_assert(L0 + S0 * (NL - 1) < NM && L3 >= BARPOS && L3 + S3 * (NL - 1) < NM, "every load is issued");
+        static_assert(BARPOS + FM + FN - 1 < NM, "every fragment read is issued");
+        uint4 fa[2][FM], fb[2][FN];
+        auto read1 = [&](const char *ta_, int buf, int kk, int q) {  // q-th fragment: A 0, B 0 .. FN - 1, A 1 ..
+            const char *tb_ = ta_ + TA::bytes;
+            if (q == 0) fa[buf][0] = frag(ta_, wm * WR, kk, std::integral_constant<bool, AT>{});
+            else if (q <= FN) fb[buf][q - 1] = frag(tb_, wn * WCOLS + 32 * (q - 1), kk, std::integral_constant<bool, BT>{});
+            else fa[buf][q - FN] = frag(ta_, wm * WR + 32 * (q - FN), kk, std::integral_constant<bool, AT>{});
+        };
+        issue(0, 0, 0, LPS);
+        issue(1, min(1, ktiles - 1), 0, NL);
+        __builtin_amdgcn_s_waitcnt((NL & 15) | ((NL >> 4) << 14) | 0x0070);  // tile 0 landed (this thread)
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < FM + FN; ++q) read1(smem, 0, 0, q);
+        for (int kt = 0; kt < ktiles; ++kt) {
+            const char *ta = smem + (kt & 1) * STAGE_BYTES;
+            const char *tn = smem + ((kt + 1) & 1) * STAGE_BYTES;
+            const int k1 = min(kt + 1, ktiles - 1), k2 = min(kt + 2, ktiles - 1);
+#pragma unroll
+            for (int st = 0; st < NSTEP; ++st) {
+                const int cur = st & 1;
+#pragma unroll
+                for (int t = 0; t < NM; ++t) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (st == NSTEP - 1 && t == BARPOS) {
+                        __builtin_amdgcn_s_waitcnt(0x0070);      // tile kt + 1 landed (this thread), LDS reads done
+                        asm volatile("s_barrier" ::: "memory");  // ... every thread's; stage kt is free
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    acc[t / FN][t % FN] = Mfma<F16>::run(fb[cur][t % FN], fa[cur][t / FN], acc[t / FN][t % FN]);
+                    if (st < NSTEP - 1) {
+                        if (t < FM + FN) read1(ta, cur ^ 1, 16 * (st + 1), t);
+                    } else if (t >= BARPOS && t - BARPOS < FM + FN) {
+                        read1(tn, cur ^ 1, 0, t - BARPOS);
+                    }
+                    if (st == 0 && t >= L0 && (t - L0) % S0 == 0 && (t - L0) / S0 < NL)
+                        issue((kt + 1) & 1, k1, NL + (t - L0) / S0, NL + (t - L0) / S0 + 1);
+                    if (st == NSTEP - 1 && t >= L3 && (t - L3) % S3 == 0 && (t - L3) / S3 < NL)
+                        issue(kt & 1, k2, (t - L3) / S3, (t - L3) / S3 + 1);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0070);  // the repeated loads land before LDS is reused
+    } else if constexpr (KL == 2) {
         // Ping-pong: waves w and w + 4 share a SIMD (wm = 0 and 1). Each wave alternates a memory phase --
         // issue its loads of tile kt + STAGES - 1 into the stage tile kt - 1 left, read all of tile kt's MFMA
         // fragments into registers, wait for them and for its own loads of tile kt + 1 -- and an MFMA phase --

@@ -34,8 +34,8 @@ constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // 32, 4-wave (128 x 128 a wave) kernel with the cross-tile fragment prefetch.
 constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
               kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4, kStream8wX = kNumTiled + 5,
-              kStream8wP = kNumTiled + 6, kStream4wX = kNumTiled + 7;
-constexpr int kNumConfigs = kNumTiled + 8;
+              kStream8wP = kNumTiled + 6, kStream4wX = kNumTiled + 7, kStream4w64X = kNumTiled + 8;
+constexpr int kNumConfigs = kNumTiled + 9;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -162,17 +162,17 @@ int launch_stream128(hipStream_t st, GemmShape s, int64_t z, const void *a, cons
     return launch_stream128_kernel<F16, AT, BT, false>(st, s, z, a, b, out, dtype, splits);
 }
 
-// KL 1, the cross-tile fragment prefetch (buffer-load path only; the 64-bit-address path runs without it), or 2,
-// the ping-pong k loop
+// KL 1, the cross-tile fragment prefetch (buffer-load path only; the 64-bit-address path runs without it), 2,
+// the ping-pong k loop, or 3, the two-stage k-64 loop placed by hand
 template <bool F16, int BK, int WN, bool AT, bool BT, int KL = 0>
 int launch_stream(hipStream_t st, GemmShape s, int64_t z, const void *a, const void *b, void *out, int dtype,
                   int splits = 1) {
     s.tiles_m = int((s.m + 255) / 256);
     s.tiles_n = int((s.n + 255) / 256);
-    if constexpr (KL == 2) {
+    if constexpr (KL == 2 || KL == 3) {
         if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
-            return launch_stream_kernel<F16, BK, WN, AT, BT, true, 2>(st, s, z, a, b, out, dtype, splits);
-        return launch_stream_kernel<F16, BK, WN, AT, BT, false, 2>(st, s, z, a, b, out, dtype, splits);
+            return launch_stream_kernel<F16, BK, WN, AT, BT, true, KL>(st, s, z, a, b, out, dtype, splits);
+        return launch_stream_kernel<F16, BK, WN, AT, BT, false, KL>(st, s, z, a, b, out, dtype, splits);
     }
     if constexpr (KL == 1)
         if (stream_buffer_ok(s.m, s.n, s.k, AT, BT, s.a_m, s.a_k, s.b_k, s.b_n))
@@ -236,6 +236,7 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream8wX: return launch_stream<F16, 32, 4, AT, BT, 1>(st, s, z, a, b, out, dtype);
         case kStream8wP: return launch_stream<F16, 32, 4, AT, BT, 2>(st, s, z, a, b, out, dtype);
         case kStream4wX: return launch_stream<F16, 32, 2, AT, BT, 1>(st, s, z, a, b, out, dtype);
+        case kStream4w64X: return launch_stream<F16, 64, 2, AT, BT, 3>(st, s, z, a, b, out, dtype);
         case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case kStreamPersist: return launch_stream_persist<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
@@ -340,7 +341,8 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
-        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist) && d->k % 64) ||
+        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist || cfg == kStream4w64X) &&
+             d->k % 64) ||
             ((cfg == kStream8w32 || cfg == kStream8wX || cfg == kStream8wP || cfg == kStream4wX) && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");
         if (d->a_dtype == NHIP_F16) return launch_mfma<true>(st, cfg, s, z, a, b, out, d->d_dtype, at, bt);
