@@ -1254,10 +1254,11 @@ class GemmEpilogueKernel:
     (mn-contiguous operands), as nhip_gemm takes them."""
 
 
-    # The k loops a generated epilogue kernel can instantiate: (k tile, gemm_stream_tile's k loop KL). Variant 0
-    # is gemm_stream's config 7 body; variant 1 its config 11 body (k tile 32, four stages, cross-tile fragment
-    # prefetch, buffer loads only); variant 2 its config 12 body (k tile 32, four stages, ping-pong waves).
-    VARIANTS = ((64, 0), (32, 1), (32, 2))
+    # The k loops a generated epilogue kernel can instantiate: (k tile, gemm_stream_tile's k loop KL, waves a
+    # row of the 2 x WN wave grid). Variant 0 is gemm_stream's config 7 body; variant 1 its config 11 body (k tile
+    # 32, four stages, cross-tile fragment prefetch, buffer loads only); variant 2 its config 12 body (k tile 32,
+    # four stages, ping-pong waves); variant 3 its config 14 body (k tile 64, two stages, four waves).
+    VARIANTS = ((64, 0, 4), (32, 1, 4), (32, 2, 4), (64, 3, 2))
 
     def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None,
                  variant=0, aliased=frozenset()):
@@ -1273,14 +1274,14 @@ class GemmEpilogueKernel:
         self.name = "KNAME"
         d = desc
         self.grid = (-(-d.m // 256) * -(-d.n // 256), 1, 1)
-        self.block = (512, 1, 1)
+        self.block = (128 * self.VARIANTS[variant][2], 1, 1)
         self.lds = 0
         self.args = []
 
     def variant_ok(self, variant):
         """Whether k loop ``variant`` can run this dot (its k tile divides k; the cross-tile prefetch needs the
         buffer-load path)."""
-        bk, kl = self.VARIANTS[variant]
+        bk, kl, _ = self.VARIANTS[variant]
         return self.desc.k % bk == 0 and (kl != 1 or self.buffer_ok())
 
     def buffer_ok(self):
@@ -1371,7 +1372,7 @@ class GemmEpilogueKernel:
                 pre_uses.append(f"const {m.group(1)} {m.group(2)} = pre.{m.group(2)};")
             else:
                 rest.append(l)
-        bk, kl = self.VARIANTS[self.variant]
+        bk, kl, wn = self.VARIANTS[self.variant]
         if not self.variant_ok(self.variant):
             raise Unfusable(dv, f"GEMM epilogue k loop variant {self.variant} does not fit k = {d.k}")
         # chunks read ahead at a time: at most 64 VGPRs of 16-byte loads
@@ -1396,12 +1397,12 @@ class GemmEpilogueKernel:
             *["    " + l for l in pre_uses + rest + body + stores + ([ret] if ret else [])],
             "  }",
             "};",
-            f'extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) '
+            f'extern "C" __global__ __launch_bounds__({128 * wn}) __attribute__((amdgpu_waves_per_eu({wn // 2}, {wn // 2}))) '
             f'void KNAME({", ".join(params)}) {{',
-            f"  __shared__ __align__(1024) char smem[nhipk::gemm_stream_lds_bytes<{bk}, 4>()];",
+            f"  __shared__ __align__(1024) char smem[nhipk::gemm_stream_lds_bytes<{bk}, {wn}>()];",
             "  nhipk::GemmShape s;",
             f"  {shape}",
-            f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, {bk}, 4, {'true' if self.at else 'false'}, "
+            f"  nhipk::gemm_stream_tile<{'true' if self.f16 else 'false'}, {bk}, {wn}, {'true' if self.at else 'false'}, "
             f"{'true' if self.bt else 'false'}, {'true' if self.buffer_ok() else 'false'}, EpiKNAME, 256, "
             f"{kl}>(s, a, b, EpiKNAME{{{init}}}, smem);",
             "}",

@@ -214,9 +214,9 @@ def _epi_colsum_fn(x, w, h, b):
 
 @pytest.mark.parametrize("fn", [_epi_fn_keep, _epi_colsum_fn])
 def test_gemm_epilogue_k_loops_agree_and_autotune_keeps_values(hip, fn, monkeypatch):
-    """The generated epilogue GEMM's two k loops (k tile 64; k tile 32 with fragments read ahead across k
-    tiles) give the same bits, ragged m and n included; and a plan whose autotuner times both on its own
-    buffers before the first run still gives those bits. Column sums, added atomically into zeros in no fixed
+    """The generated epilogue GEMM's first and last k loops (k tile 64 on eight waves; k tile 64 on four waves,
+    two stages, placed by hand) give the same bits, ragged m and n included; and a plan whose autotuner times
+    every k loop on its own buffers before the first run still gives those bits. Column sums, added atomically into zeros in no fixed
     order, agree within float32 reassociation (1e-5 of the sum of magnitudes)."""
     from lumen_amd.compiler import codegen
     from lumen_amd.compiler.plan import Plan

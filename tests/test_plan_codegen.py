@@ -109,8 +109,8 @@ def test_elementwise_consumer_of_a_dot_runs_in_its_epilogue(fn, keep, monkeypatc
 
 def test_large_epilogue_dots_get_their_other_k_loop_for_the_autotuner(monkeypatch):
     """An epilogue GEMM large enough to tune is also generated (and compiled) with the other k loops (k tile 32
-    with cross-tile prefetch; k tile 32 with ping-pong waves), as separate kernels; small ones, or any with the
-    autotuner off, get none."""
+    with cross-tile prefetch; k tile 32 with ping-pong waves; k tile 64 on four waves), as separate kernels;
+    small ones, or any with the autotuner off, get none."""
     from lumen_amd.compiler import codegen
 
     monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
@@ -118,10 +118,12 @@ def test_large_epilogue_dots_get_their_other_k_loop_for_the_autotuner(monkeypatc
     with L.config.compiler.patch(horizontal_fusion=False):
         p = _plan(_epilogue_fn, *EPI_SHAPES, build=True)
     (si, alts), = p.epi_alts.items()
-    assert [a[0] for a in alts] == [1, 2]
+    assert [a[0] for a in alts] == [1, 2, 3]
     for i, (var, k, src) in enumerate(alts):
-        assert codegen.GemmEpilogueKernel.VARIANTS[var] == (32, var)
-        assert k.name != p.steps[si].name and k.name in src and ", 32, 4, " in src and f", {var}>(s, a, b" in src
+        bk, kl, wn = codegen.GemmEpilogueKernel.VARIANTS[var]
+        assert (bk, kl, wn) == ((32, var, 4) if var < 3 else (64, 3, 2))
+        assert k.name != p.steps[si].name and k.name in src and f", {bk}, {wn}, " in src and f", {kl}>(s, a, b" in src
+        assert k.block == (128 * wn, 1, 1) and f"__launch_bounds__({128 * wn})" in src
         assert p.alt_objects[(si, i)].endswith(".hsaco")
     with L.config.compiler.patch(horizontal_fusion=False, autotune=False):
         assert not _plan(_epilogue_fn, *EPI_SHAPES).epi_alts
