@@ -1257,8 +1257,9 @@ class GemmEpilogueKernel:
     # The k loops a generated epilogue kernel can instantiate: (k tile, gemm_stream_tile's k loop KL, waves a
     # row of the 2 x WN wave grid). Variant 0 is gemm_stream's config 7 body; variant 1 its config 11 body (k tile
     # 32, four stages, cross-tile fragment prefetch, buffer loads only); variant 2 its config 12 body (k tile 32,
-    # four stages, ping-pong waves); variant 3 its config 14 body (k tile 64, two stages, four waves).
-    VARIANTS = ((64, 0, 4), (32, 1, 4), (32, 2, 4), (64, 3, 2))
+    # four stages, ping-pong waves); variant 3 its config 14 body (k tile 64, two stages, four waves); variant 4
+    # its config 15 body (the same on eight waves).
+    VARIANTS = ((64, 0, 4), (32, 1, 4), (32, 2, 4), (64, 3, 2), (64, 3, 4))
 
     def __init__(self, graph, dot_step, loop_step, desc, at, bt, f16, store_dot, views, out_views, colsum=None,
                  variant=0, aliased=frozenset()):

@@ -560,15 +560,15 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
     constexpr bool XPF = KL == 1;
     if constexpr (KL == 3) {
         // k tile 64 (128-byte row segments: one L2 request a 128-byte line instead of two for k tile 32), two
-        // stages, one wave a SIMD, placed by hand one MFMA at a time. Each tile's loads go out in two halves: A
+        // stages, one or two waves a SIMD, placed by hand one MFMA at a time. Each tile's loads go out in two halves: A
         // of tile kt + 2 in tile kt's last k step, right after the barrier that frees its stage, B in tile
         // kt + 1's first k step. Each k step reads the next one's fragments after its first FM + FN MFMAs; the
         // last waits for all of tile kt + 1, meets the barrier after BARPOS MFMAs and reads tile kt + 1's first
         // fragments under its own MFMAs. Past the last tile the loads repeat it into the free stage, so every
         // tile runs the same straight-line body.
-        static_assert(STAGES == 2 && BK == 64 && WN == 2, "two stages of k 64 on four waves");
+        static_assert(STAGES == 2 && BK == 64 && (WN == 2 || WN == 4), "two stages of k 64 on four or eight waves");
         constexpr int NSTEP = BK / 16, NM = FM * FN, NL = LPS / 2;
-        constexpr int BARPOS = 2, L0 = 1, S0 = 2, L3 = 4, S3 = 1;
+        constexpr int BARPOS = 2, L0 = 1, S0 = 2, L3 = WN == 2 ? 4 : 3, S3 = 1;
         static_assert(NL == TA::segs / NW, "the halves are A's and B's loads");
         static_assert(L0 + S0 * (NL - 1) < NM && L3 >= BARPOS && L3 + S3 * (NL - 1) < NM, "every load is issued");
         static_assert(BARPOS + FM + FN - 1 < NM, "every fragment read is issued");

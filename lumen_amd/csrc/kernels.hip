@@ -34,8 +34,9 @@ constexpr int kNumTiled = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // 32, 4-wave (128 x 128 a wave) kernel with the cross-tile fragment prefetch.
 constexpr int kStream4w = kNumTiled, kStream8w = kNumTiled + 1, kStream8w32 = kNumTiled + 2,
               kStream128 = kNumTiled + 3, kStreamPersist = kNumTiled + 4, kStream8wX = kNumTiled + 5,
-              kStream8wP = kNumTiled + 6, kStream4wX = kNumTiled + 7, kStream4w64X = kNumTiled + 8;
-constexpr int kNumConfigs = kNumTiled + 9;
+              kStream8wP = kNumTiled + 6, kStream4wX = kNumTiled + 7, kStream4w64X = kNumTiled + 8,
+              kStream8w64X = kNumTiled + 9;
+constexpr int kNumConfigs = kNumTiled + 10;
 
 GemmShape shape_of(const nhip_gemm_desc *d) {
     GemmShape s;
@@ -237,6 +238,7 @@ int launch_mfma_layout(hipStream_t st, int cfg, GemmShape s, int64_t z, const vo
         case kStream8wP: return launch_stream<F16, 32, 4, AT, BT, 2>(st, s, z, a, b, out, dtype);
         case kStream4wX: return launch_stream<F16, 32, 2, AT, BT, 1>(st, s, z, a, b, out, dtype);
         case kStream4w64X: return launch_stream<F16, 64, 2, AT, BT, 3>(st, s, z, a, b, out, dtype);
+        case kStream8w64X: return launch_stream<F16, 64, 4, AT, BT, 3>(st, s, z, a, b, out, dtype);
         case kStream128: return launch_stream128<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case kStreamPersist: return launch_stream_persist<F16, AT, BT>(st, s, z, a, b, out, dtype);
         case 0: return launch_mfma_cfg<F16, 256, 256, 64, 2, 4, AT, BT>(st, s, z, a, b, out, dtype);
@@ -341,7 +343,8 @@ int gemm_on(hipStream_t st, const nhip_gemm_desc *d, const void *a, const void *
     if (d->k > 0 && mfma_ready(d, a, b, at, bt)) {  // k == 0 folds nothing: the exact kernel writes zeros
         int cfg = d->config < 0 ? default_config(d) : d->config;
         if (cfg >= kNumConfigs) return fail("nhip_gemm: no tile config " + std::to_string(cfg));
-        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist || cfg == kStream4w64X) &&
+        if (((cfg == kStream4w || cfg == kStream8w || cfg == kStream128 || cfg == kStreamPersist || cfg == kStream4w64X ||
+              cfg == kStream8w64X) &&
              d->k % 64) ||
             ((cfg == kStream8w32 || cfg == kStream8wX || cfg == kStream8wP || cfg == kStream4wX) && d->k % 32))
             return fail("nhip_gemm: the streamed configs need k to be a multiple of their k tile");

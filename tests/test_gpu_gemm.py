@@ -31,7 +31,7 @@ def _desc(m, n, k, a_m, a_k, b_k, b_n, dt=nv.NHIP_BF16, out=nv.NHIP_F32, cfg=-1,
     [(512, 384, 256, -1), (264, 136, 200, 2), (64, 64, 64, 4), (520, 520, 72, 0), (520, 264, 192, 6), (264, 776, 128, 7),
      (264, 136, 96, 8), (200, 392, 192, 9), (520, 776, 192, 10), (520, 776, 160, 11), (520, 776, 160, 12),
      (264, 520, 32, 12), (264, 264, 64, 12), (520, 776, 160, 13), (264, 520, 32, 13), (520, 776, 192, 14),
-     (264, 520, 64, 14), (264, 264, 128, 14)],
+     (264, 520, 64, 14), (264, 264, 128, 14), (520, 776, 192, 15), (264, 520, 64, 15)],
 )
 def test_gemm_layouts(hip, at, bt, m, n, k, cfg):
     """A as [m][k] or [k][m] in memory, B as [n][k] or [k][n]: float32 results within float32 rounding of
@@ -65,9 +65,10 @@ def test_gemm_batched_bf16_output(hip):
 @pytest.mark.parametrize("cfg,out", [(6, nv.NHIP_BF16), (7, nv.NHIP_F16), (7, nv.NHIP_F32), (8, nv.NHIP_BF16),
                                      (9, nv.NHIP_BF16), (9, nv.NHIP_F32), (10, nv.NHIP_BF16), (11, nv.NHIP_BF16),
                                      (11, nv.NHIP_F32), (12, nv.NHIP_BF16), (12, nv.NHIP_F32), (13, nv.NHIP_BF16),
-                                     (13, nv.NHIP_F32), (14, nv.NHIP_BF16), (14, nv.NHIP_F32)])
+                                     (13, nv.NHIP_F32), (14, nv.NHIP_BF16), (14, nv.NHIP_F32),
+                                     (15, nv.NHIP_BF16), (15, nv.NHIP_F32)])
 def test_gemm_streamed_16bit_outputs_and_ragged_edges(hip, cfg, out):
-    """The streamed kernels' LDS-staged row stores (256 x 256 tiles, configs 6-8, 11-14; 128 x 128, config 9):
+    """The streamed kernels' LDS-staged row stores (256 x 256 tiles, configs 6-8, 11-15; 128 x 128, config 9):
     16-bit and float32 outputs, m and n not multiples of the tile, two batches."""
     rng = np.random.default_rng(cfg + out)
     z, m, n, k = 2, 300, 264, 128

@@ -118,10 +118,10 @@ def test_large_epilogue_dots_get_their_other_k_loop_for_the_autotuner(monkeypatc
     with L.config.compiler.patch(horizontal_fusion=False):
         p = _plan(_epilogue_fn, *EPI_SHAPES, build=True)
     (si, alts), = p.epi_alts.items()
-    assert [a[0] for a in alts] == [1, 2, 3]
+    assert [a[0] for a in alts] == [1, 2, 3, 4]
     for i, (var, k, src) in enumerate(alts):
         bk, kl, wn = codegen.GemmEpilogueKernel.VARIANTS[var]
-        assert (bk, kl, wn) == ((32, var, 4) if var < 3 else (64, 3, 2))
+        assert (bk, kl, wn) == ((32, var, 4) if var < 3 else (64, 3, 2) if var == 3 else (64, 3, 4))
         assert k.name != p.steps[si].name and k.name in src and f", {bk}, {wn}, " in src and f", {kl}>(s, a, b" in src
         assert k.block == (128 * wn, 1, 1) and f"__launch_bounds__({128 * wn})" in src
         assert p.alt_objects[(si, i)].endswith(".hsaco")
