@@ -585,9 +585,12 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < FM + FN; ++q) read1(smem, 0, 0, q);
-        for (int kt = 0; kt < ktiles; ++kt) {
-            const char *ta = smem + (kt & 1) * STAGE_BYTES;
-            const char *tn = smem + ((kt + 1) & 1) * STAGE_BYTES;
+        // one k tile in stage P (a constant: the loop below runs tiles in pairs, so the stages' LDS offsets
+        // fold into the fragment reads' immediates)
+        auto tile = [&](int kt, auto parc) {
+            constexpr int P = decltype(parc)::value;
+            const char *ta = smem + P * STAGE_BYTES;
+            const char *tn = smem + (P ^ 1) * STAGE_BYTES;
             const int k1 = min(kt + 1, ktiles - 1), k2 = min(kt + 2, ktiles - 1);
 #pragma unroll
             for (int st = 0; st < NSTEP; ++st) {
@@ -607,13 +610,18 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                         read1(tn, cur ^ 1, 0, t - BARPOS);
                     }
                     if (st == 0 && t >= L0 && (t - L0) % S0 == 0 && (t - L0) / S0 < NL)
-                        issue((kt + 1) & 1, k1, NL + (t - L0) / S0, NL + (t - L0) / S0 + 1);
+                        issue(P ^ 1, k1, NL + (t - L0) / S0, NL + (t - L0) / S0 + 1);
                     if (st == NSTEP - 1 && t >= L3 && (t - L3) % S3 == 0 && (t - L3) / S3 < NL)
-                        issue(kt & 1, k2, (t - L3) / S3, (t - L3) / S3 + 1);
+                        issue(P, k2, (t - L3) / S3, (t - L3) / S3 + 1);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int kt = 0; kt + 1 < ktiles; kt += 2) {
+            tile(kt, std::integral_constant<int, 0>{});
+            tile(kt + 1, std::integral_constant<int, 1>{});
         }
+        if (ktiles & 1) tile(ktiles - 1, std::integral_constant<int, 0>{});
         __builtin_amdgcn_s_waitcnt(0x0070);  // the repeated loads land before LDS is reused
     } else if constexpr (KL == 2) {
         // Ping-pong: waves w and w + 4 share a SIMD (wm = 0 and 1). Each wave alternates a memory phase --
