@@ -431,6 +431,25 @@ __device__ __forceinline__ void stage_acc(const f32x16_t (&acc)[FM][FN], int hal
     }
 }
 
+// Runs tile(kt, P) for kt = 0 .. ktiles - 1 with P = kt % S as a constant (std::integral_constant), S tiles at
+// a time: a k loop whose LDS stage is a constant has the stage offsets in its LDS instructions' immediates
+// instead of recomputing addresses every tile.
+template <int S, int P = 0, class F>
+__device__ __forceinline__ void tiles_block(int kt, int n, F &tile) {
+    if constexpr (P < S) {
+        if (P < n) {
+            tile(kt + P, std::integral_constant<int, P>{});
+            tiles_block<S, P + 1>(kt, n, tile);
+        }
+    }
+}
+template <int S, class F>
+__device__ __forceinline__ void for_tiles(int ktiles, F &&tile) {
+    int kt = 0;
+    for (; kt + S <= ktiles; kt += S) tiles_block<S>(kt, S, tile);
+    tiles_block<S>(kt, ktiles - kt, tile);
+}
+
 // One workgroup's 256 x 256 output tile. `out` is AnyStore (a plain store of D), or a generated epilogue
 // functor called as out(row, col, float4, pre) with the float32 sums of four consecutive columns (col a
 // multiple of 4, within m x n) and pre = out.load(row, col), its other operands read ahead. `smem` holds gemm_stream_lds_bytes<BK, WN>() bytes.
@@ -646,11 +665,12 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         wait_tiles(min(STAGES - 2, ktiles - 1));
         __builtin_amdgcn_s_barrier();
         if (wm == 1) __builtin_amdgcn_s_barrier();
-        for (int kt = 0; kt < ktiles; ++kt) {
+        for_tiles<STAGES>(ktiles, [&](int kt, auto pc) {
+            constexpr int P = decltype(pc)::value;  // kt % STAGES
             __builtin_amdgcn_sched_barrier(0);
-            const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+            const char *ta = smem + P * STAGE_BYTES;
             const char *tb = ta + TA::bytes;
-            if (kt + STAGES - 1 < ktiles) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+            if (kt + STAGES - 1 < ktiles) issue((P + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
 #pragma unroll
             for (int i = 0; i < NSTEP; ++i) {
 #pragma unroll
@@ -672,7 +692,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
-        }
+        });
         if (wm == 0) __builtin_amdgcn_s_barrier();
     } else if constexpr (XPF) {
         // Fragments run ahead across k tiles: the last k step of tile kt waits for tile kt + 1's loads (issued
@@ -729,10 +749,12 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                 else if (q <= FN) fb[buf][q - 1] = frag(tb_, wn * WCOLS + 32 * (q - 1), kk, std::integral_constant<bool, BT>{});
                 else fa[buf][q - FN] = frag(ta_, wm * WR + 32 * (q - FN), kk, std::integral_constant<bool, AT>{});
             };
-            for (int kt = 0; kt < ktiles; ++kt) {
-                const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
-                const char *tn = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
-                const int lst = (kt + STAGES - 1) % STAGES, lkt = min(kt + STAGES - 1, ktiles - 1);
+            for_tiles<STAGES>(ktiles, [&](int kt, auto pc) {
+                constexpr int P = decltype(pc)::value;  // kt % STAGES
+                const char *ta = smem + P * STAGE_BYTES;
+                const char *tn = smem + ((P + 1) % STAGES) * STAGE_BYTES;
+                constexpr int lst = (P + STAGES - 1) % STAGES;
+                const int lkt = min(kt + STAGES - 1, ktiles - 1);
 #pragma unroll
                 for (int t = 0; t < NM; ++t) {
                     __builtin_amdgcn_sched_barrier(0);
@@ -756,11 +778,12 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                         issue(lst, lkt, NL + (t - LSTART) / LSTRIDE, NL + (t - LSTART) / LSTRIDE + 1);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-            }
-        } else
-        for (int kt = 0; kt < ktiles; ++kt) {
-            const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
-            const char *tn = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
+            });
+        } else {
+        for_tiles<STAGES>(ktiles, [&](int kt, auto pc) {
+            constexpr int P = decltype(pc)::value;  // kt % STAGES
+            const char *ta = smem + P * STAGE_BYTES;
+            const char *tn = smem + ((P + 1) % STAGES) * STAGE_BYTES;
             const bool more = kt + STAGES - 1 < ktiles;
             const bool next = kt + 1 < ktiles;
             auto step = [&](auto ic) {
@@ -778,7 +801,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                 }
                 if constexpr (i == 0) {
                     if (UNI || more)
-                        issue((kt + STAGES - 1) % STAGES, UNI ? min(kt + STAGES - 1, ktiles - 1) : kt + STAGES - 1, 0, LPS);
+                        issue((P + STAGES - 1) % STAGES, UNI ? min(kt + STAGES - 1, ktiles - 1) : kt + STAGES - 1, 0, LPS);
                 }
 #pragma unroll
                 for (int ii = 0; ii < FM; ++ii)
@@ -796,13 +819,15 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
                 step(std::integral_constant<int, 2>{});
                 step(std::integral_constant<int, 3>{});
             }
+        });
         }
         if constexpr (UNI) __builtin_amdgcn_s_waitcnt(0x0070);  // the repeated loads land before LDS is reused
     } else {
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
         if (st < ktiles) issue(st, st, 0, LPS);
-    for (int kt = 0; kt < ktiles; ++kt) {
+    for_tiles<STAGES>(ktiles, [&](int kt, auto pc) {
+        constexpr int P = decltype(pc)::value;  // kt % STAGES
         // wait for this thread's loads of tile kt: later tiles' loads may stay in flight
         const int later = min(STAGES - 2, ktiles - 1 - kt);
         if (STAGES <= 2 || later <= 0) __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);
@@ -810,7 +835,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
         else __builtin_amdgcn_s_waitcnt(((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | 0x0070 | 0x0f00);
         __syncthreads();  // every thread's loads of tile kt landed; the stage of tile kt - 1 is free
         const bool more = kt + STAGES - 1 < ktiles;
-        const char *ta = smem + (kt % STAGES) * STAGE_BYTES;
+        const char *ta = smem + P * STAGE_BYTES;
         const char *tb = ta + TA::bytes;
         uint4 fa[2][FM], fb[2][FN];
         auto read = [&](int buf, int kk) {  // in the order the MFMAs (i-major) first use them
@@ -831,9 +856,9 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             // (with one wave a SIMD, WN = 2, nothing else covers the loads' latency: all of them go out in the first
             // k step, a whole k tile ahead of their use)
             if constexpr (WN == 2 && TM == 256) {
-                if (kk == 0 && more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
+                if (kk == 0 && more) issue((P + STAGES - 1) % STAGES, kt + STAGES - 1, 0, LPS);
             } else {
-                if (more) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
+                if (more) issue((P + STAGES - 1) % STAGES, kt + STAGES - 1, (kk / 16) * LPS * 16 / BK, (kk / 16 + 1) * LPS * 16 / BK);
             }
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -848,7 +873,7 @@ __device__ __forceinline__ void gemm_stream_tile(const GemmShape &s, const uint1
             step(std::integral_constant<int, 32>{});
             step(std::integral_constant<int, 48>{});
         }
-    }
+    });
     }
 
     // acc[i][j][e]: row m0 + wm*WR + 32 i + l32, column n0 + wn*WCOLS + 32 j + 8 (e / 4) + 4 h + e % 4.
