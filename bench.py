@@ -115,6 +115,8 @@ def main():
     ap.add_argument("--gemm-shape", default="8192,8192,8192", help="gemm: m,n,k")
     ap.add_argument("--gemm-config", type=int, default=-1, help="gemm: the tile config (-1 default)")
     ap.add_argument("--gemm-out", default="f32", choices=["f32", "bf16"], help="gemm: the output dtype")
+    ap.add_argument("--gemm-layout", default="kk", choices=["kk", "km", "mk", "mm"],
+                    help="gemm: A then B contiguous along k or along m / n (kk: A [m, k], B [n, k])")
     ap.add_argument("--gemm-library", action="store_true",
                     help="gemm: also time the vendor library (torch.mm) on the same shape, alternating with ours")
     ap.add_argument("--top", type=int, default=0, help="print the N slowest plan steps to stderr")
@@ -527,7 +529,8 @@ def _attn_cpu(b, s, n, d, sl=256):
 
 def _config_gemm(args):
     """One dot through the C ABI (nhip_gemm) at ``--gemm-shape m,n,k`` (A [m, k] and B [n, k] k-contiguous bf16,
-    D [m, n] float32 or with ``--gemm-out bf16``) and tile config ``--gemm-config`` (-1: the default pick): the
+    or along m / n with ``--gemm-layout``; D [m, n] float32 or with ``--gemm-out bf16``) and tile config
+    ``--gemm-config`` (-1: the default pick): the
     GEMM kernels measured alone, for comparing k loops and for counter runs. Not a BASELINE configuration."""
     import ctypes as C
 
@@ -549,7 +552,10 @@ def _config_gemm(args):
     g.m, g.n, g.k, g.nbatch = m, n, k, 0
     g.a_dtype = g.b_dtype = nv.NHIP_BF16
     g.d_dtype = out
-    g.a_m, g.a_k, g.b_k, g.b_n, g.d_m, g.d_n = k, 1, 1, k, n, 1
+    at, bt = args.gemm_layout[0] == "m", args.gemm_layout[1] == "m"  # A [k, m], B [k, n] in memory
+    g.a_m, g.a_k = (1, m) if at else (k, 1)
+    g.b_k, g.b_n = (n, 1) if bt else (1, k)
+    g.d_m, g.d_n = n, 1
     g.config, g.splits = args.gemm_config, 0
 
     def call():
@@ -572,16 +578,18 @@ def _config_gemm(args):
         # same bf16 operands (B as [n, k], used transposed) and output dtype, calls alternated with ours
         import torch
 
-        ta = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).reshape(m, k).to("cuda")
-        tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).reshape(n, k).to("cuda")
+        ta = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).reshape((k, m) if at else (m, k)).to("cuda")
+        tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).reshape((k, n) if bt else (n, k)).to("cuda")
+        ta = ta.t() if at else ta  # [m, k] views
+        tb = tb if bt else tb.t()  # [k, n] views
         od = torch.float32 if out == nv.NHIP_F32 else torch.bfloat16
         to = torch.empty(m, n, dtype=od, device="cuda")
 
         def lib():
             if od == torch.float32:
-                torch.mm(ta, tb.t(), out_dtype=torch.float32)  # aten::mm.dtype: bf16 operands, float32 output
+                torch.mm(ta, tb, out_dtype=torch.float32)  # aten::mm.dtype: bf16 operands, float32 output
             else:
-                torch.mm(ta, tb.t(), out=to)
+                torch.mm(ta, tb, out=to)
 
         lib_ms, our_ms = [], []
         for _ in range(3):
@@ -602,7 +610,8 @@ def _config_gemm(args):
             "per_launch": {"flops": 2 * m * n * k, "bytes": (m + n) * k * 2 + m * n * (2 if out == nv.NHIP_BF16 else 4),
                            "ms": round(ms, 4)}}
     return _op_line(args, "gemm TFLOP/s", ms, tf, "TFLOP/s",
-                    {"workload": f"gemm [{m}, {k}] x [{n}, {k}]^T -> {args.gemm_out}, config {args.gemm_config}"},
+                    {"workload": f"gemm [{m}, {k}] x [{n}, {k}]^T -> {args.gemm_out}, config {args.gemm_config}, "
+                                 f"layout {args.gemm_layout}"},
                     roof, None, "bf16", extra)
 
 
