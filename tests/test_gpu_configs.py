@@ -256,6 +256,38 @@ def test_gemm_epilogue_k_loops_agree_and_autotune_keeps_values(hip, fn, monkeypa
             assert np.array_equal(a, b_) and np.array_equal(a, c)
 
 
+@pytest.mark.parametrize("variant", [1, 2, 3, 4])
+def test_each_gemm_epilogue_k_loop_gives_the_first_ones_bits(hip, variant, monkeypatch):
+    """Every k loop a generated epilogue GEMM can be built with (k tile 32 cross-tile prefetch and ping-pong,
+    k tile 64 two-stage on four and eight waves), forced as the only one, gives the bits of the default
+    (k tile 64 on eight waves): ragged m and n, an odd number of k tiles of 64 (k = 320)."""
+    from lumen_amd.compiler import codegen
+    from lumen_amd.compiler.plan import Plan
+
+    monkeypatch.setattr(Plan, "EPI_MIN_TILES", 1)
+    m, n, k = 1000, 776, 320
+    rng = np.random.default_rng(29)
+    x = _bf16(rng.standard_normal((m, k)) * 0.25)
+    w = _bf16(rng.standard_normal((k, n)) * 0.25)
+    h = rng.standard_normal((m, n)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    args = [L.tensor(D.bf16_to_f32(x), "bfloat16"), L.tensor(D.bf16_to_f32(w), "bfloat16"), L.from_numpy(h),
+            L.from_numpy(b)]
+
+    def run():
+        with L.config.compiler.patch(horizontal_fusion=False, autotune=False):
+            f = L.compile(_epi_fn_keep, device="hip")
+            out = [np.asarray(L.to_numpy(t), np.float32) for t in f(*args)]
+            assert any(s["name"].startswith("gemm_epi_") for s in f.plan.describe())
+            return out
+
+    first = run()
+    variants = codegen.GemmEpilogueKernel.VARIANTS
+    monkeypatch.setattr(codegen.GemmEpilogueKernel, "VARIANTS", (variants[variant],) + variants[1:])
+    for a, b_ in zip(first, run()):
+        assert np.array_equal(a, b_)
+
+
 @pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,))])
 def test_leading_axis_sums_match_oracle(hip, shape, axes):
     """float32 sums over leading axes (the vectorized reduce kernel: four columns a thread, 64-row chunks
