@@ -137,6 +137,24 @@ DEV float fdiv_row(float a, float b, float r, int ok) {
   if (!ok) return a / b;
   return fdiv_q(a, b, r);
 }
+// a / b for a row-uniform divisor as a times its refined reciprocal r (within 2 ulp: r within 1 ulp of 1 / b,
+// one more rounding in the product); divisors near the ends of the exponent range, zero, infinities and NaN
+// take the IEEE division by the same scalar branch
+DEV float fdiv_rowm(float a, float b, float r, int ok) {
+  if (!ok) return a / b;
+  return a * r;
+}
+// 1 + tanh(u) in float32 as 2 / (1 + 2^(-2 u log2 e)) = 2 sigmoid(2u): no cancellation as tanh(u) nears -1,
+// one exp2 and one reciprocal where tanh_f32 evaluates a polynomial and an exp2/reciprocal form and selects.
+// The exponent's rounding (relative 2^-24 of |2u log2 e|) bounds the error: under 1e-6 relative for |u| < 8,
+// 2e-5 at the underflow end; u = +-inf gives 2 and 0, NaN propagates.
+DEV float onep_tanh_f32(float u) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u)); }
+// the same with u = c x folded into one product (the tanh argument of GELU's tanh form): k = -2 c log2 e
+DEV float onep_tanh_k(float x, float k) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(k * x)); }
+// exp(d) of a row-shifted value d = x - (a row's statistic), softmax's exponent: 2^(d log2 e) on the hardware
+// exp2. The product's rounding bounds the error to 2^-24 |d log2 e| ln 2 relative: under 5.2e-6 for every d
+// whose exponential is a normal float (d > -87.3); -inf gives 0, NaN propagates
+DEV float exp_shifted_f32(float d) { return __builtin_amdgcn_exp2f(d * 1.4426950408889634f); }
 // NaN-propagating float32 maximum and minimum (-0 below +0): gfx950's v_maximum3_f32 / v_minimum3_f32, one
 // instruction for two operands or a chain of three
 DEV float fmax_n(float a, float b) { return __builtin_elementwise_maximum(a, b); }
@@ -272,6 +290,14 @@ class Emitter:
     # float32 division as a refined reciprocal and one quotient correction (fdiv_f32, within 1 ulp) instead of
     # the correctly rounded division sequence; the reciprocal of a row statistic is then computed once a row
     FAST_DIV = True
+    # a quotient by a row statistic (layer norm's deviation, softmax's sum) as one multiply by the row's refined
+    # reciprocal (within 2 ulp) instead of the corrected quotient (within 1 ulp, four more instructions)
+    ROW_RECIP_MUL = True
+    # 1 + tanh(u) whose tanh nothing else reads (GELU's tanh form) evaluated as 2 sigmoid(2u) (onep_tanh_f32)
+    ONEP_TANH = True
+    # exp of a row-shifted value (softmax) as one exp2 of the scaled argument (within 5.2e-6 relative)
+    # instead of exp_f32's split product (within 4 ulp)
+    SHIFTED_EXP = True
 
     def __init__(self, graph: Graph, nodes, inputs: dict, rows=None):
         self.graph = graph
@@ -288,6 +314,7 @@ class Emitter:
         self.uniform: set = set()     # C names of per-row values (the same on every lane of a row's wave)
         self.recips: dict = {}        # uniform divisor name -> (reciprocal name, range-flag name)
         self.rounded: dict = {}       # name of a bf16-rounded float -> the name it was rounded from
+        self._users = None            # the graph's readers of each value, built on first need
 
     def tmp(self, prefix="t"):
         self.count += 1
@@ -315,7 +342,7 @@ class Emitter:
                 self.emit(f"const int {ok} = __builtin_amdgcn_readfirstlane(fdiv_ok({b}));")
                 self.recips[b] = (r, ok)
             r, ok = self.recips[b]
-            return f"fdiv_row({a}, {b}, {r}, {ok})"
+            return f"{'fdiv_rowm' if Emitter.ROW_RECIP_MUL else 'fdiv_row'}({a}, {b}, {r}, {ok})"
         return f"fdiv_f32({a}, {b})"
 
     # ---- indices
@@ -419,6 +446,44 @@ class Emitter:
             return f"(({expr}) != 0)"
         return f"(({COMP_T[dtype]})({STORE_T[dtype]})({expr}))"
 
+    def _const(self, var):
+        """The fill value of ``var`` when it is a scalar fill, possibly broadcast or reshaped, else None."""
+        n = self.prod.get(var)
+        while n is not None and n.prim in ("broadcast_in_dim", "reshape"):
+            n = self.prod.get(n.inputs[0])
+        return n.params["fill_value"] if n is not None and n.prim == "full" else None
+
+    def _onep_tanh_arg(self, n):
+        """For ``n`` = 1 + tanh(u) (either order) where the kernel computes the tanh and every reader of it in
+        the graph is such a sum: u, else None."""
+        if self._users is None:
+            self._users = self.graph.users()
+        for k in (0, 1):
+            t = self.prod.get(n.inputs[k])
+            if t is None or t.prim != "tanh" or self._const(n.inputs[1 - k]) != 1.0:
+                continue
+            if t.inputs[0] in self.given or self.graph.types[t.inputs[0]].dtype != "float32":
+                continue
+            readers = self._users.get(t.output, [])
+            if t.output in self.graph.outputs or not all(
+                    r.prim == "add" and any(r.inputs[j] == t.output and self._const(r.inputs[1 - j]) == 1.0
+                                            for j in (0, 1)) for r in readers):
+                continue
+            return t.inputs[0]
+        return None
+
+    def _row_shifted(self, var):
+        """Whether ``var`` is x - s with s a per-row value of this row kernel (a softmax's shifted logits)."""
+        m = self.prod.get(var)
+        if self.rows is None or m is None or m.prim != "sub":
+            return False
+        s = self.prod.get(m.inputs[1])
+        while s is not None and s.prim in ("broadcast_in_dim", "reshape"):
+            if s.inputs[0] in self.row_scalars:
+                return True
+            s = self.prod.get(s.inputs[0])
+        return m.inputs[1] in self.row_scalars
+
     def _compute(self, var, idx, ty):
         if var in self.given:
             return self.given[var](idx)
@@ -436,6 +501,24 @@ class Emitter:
         def same(k=0):
             return self.value(n.inputs[k], idx)
 
+        if p == "add" and dt == "float32" and Emitter.ONEP_TANH:
+            u = self._onep_tanh_arg(n)
+            if u is not None:
+                m = self.prod.get(u)
+                c = None
+                if m is not None and m.prim == "mul":
+                    for j in (0, 1):
+                        c = self._const(m.inputs[j])
+                        if isinstance(c, float) and c == c and abs(c) != float("inf"):
+                            x = m.inputs[1 - j]
+                            break
+                        c = None
+                if c is not None:
+                    k = float(-2.0 * c * 1.4426950408889634)
+                    self.emit(f"const float {out} = onep_tanh_k({self.value(x, idx)}, {k.hex()}f);")
+                else:
+                    self.emit(f"const float {out} = onep_tanh_f32({self.value(u, idx)});")
+                return out
         if p in ("add", "sub", "mul", "div", "max", "eq", "lt"):
             a, b = same(0), same(1)
             src = ins[0].dtype
@@ -522,6 +605,8 @@ class Emitter:
             one = "1.0f" if f32 else "1.0"
             if p == "tanh" and f32:
                 expr = f"tanh_f32({a})"
+            elif p == "exp" and f32 and Emitter.SHIFTED_EXP and self._row_shifted(n.inputs[0]):
+                expr = f"exp_shifted_f32({a})"
             elif p == "exp" and f32:
                 expr = f"exp_f32({a})"
             elif p == "logistic":
