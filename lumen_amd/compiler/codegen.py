@@ -151,6 +151,14 @@ DEV float fdiv_rowm(float a, float b, float r, int ok) {
 DEV float onep_tanh_f32(float u) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u)); }
 // the same with u = c x folded into one product (the tanh argument of GELU's tanh form): k = -2 c log2 e
 DEV float onep_tanh_k(float x, float k) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(k * x)); }
+// GELU's tanh form 0.5 x (1 + tanh(c1 (x + c2 x^3))) as x sigmoid(2 c1 x (1 + c2 x^2)) = x / (1 + 2^(x (k + k c2 x^2)))
+// with k = -2 c1 log2 e: three products, one exp2 and one reciprocal. Within 2e-6 relative of the exact value for
+// |x| < 8 (the exponent's rounding, relative 2^-24 of its magnitude, and the two hardware approximations); +inf
+// gives inf, -inf NaN and large negative x -0, as the traced form does in float32
+DEV float gelu_tanh_f32(float x, float k, float kc2) {
+  const float p = fmaf(x * x, kc2, k);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * p));
+}
 // exp(d) of a row-shifted value d = x - (a row's statistic), softmax's exponent: 2^(d log2 e) on the hardware
 // exp2. The product's rounding bounds the error to 2^-24 |d log2 e| ln 2 relative: under 5.2e-6 for every d
 // whose exponential is a normal float (d > -87.3); -inf gives 0, NaN propagates
@@ -472,6 +480,52 @@ class Emitter:
             return t.inputs[0]
         return None
 
+    def _mul_const(self, var):
+        """(c, y) when ``var`` is the product of a finite float scalar fill c and y (either order), else None."""
+        m = self.prod.get(var)
+        if m is None or m.prim != "mul":
+            return None
+        for j in (0, 1):
+            c = self._const(m.inputs[j])
+            if isinstance(c, float) and c == c and abs(c) != float("inf"):
+                return c, m.inputs[1 - j]
+        return None
+
+    def _times(self, var, x):
+        """The operand multiplied by ``x`` when ``var`` is a product with x (either order), else None."""
+        m = self.prod.get(var)
+        if m is None or m.prim != "mul" or x not in m.inputs:
+            return None
+        return m.inputs[1] if m.inputs[0] == x else m.inputs[0]
+
+    def _gelu_tanh(self, n):
+        """(x, c1, c2) when ``n`` is the traced tanh GELU (0.5 x) (1 + tanh(c1 (x + ((c2 x) x) x))) in float32
+        and its tanh qualifies for onep_tanh (nothing else reads it), else None."""
+        for j in (0, 1):
+            half = self._mul_const(n.inputs[j])
+            if half is None or half[0] != 0.5:
+                continue
+            x = half[1]
+            b = self.prod.get(n.inputs[1 - j])
+            if b is None or b.prim != "add" or self.graph.types[x].dtype != "float32":
+                continue
+            u = self._onep_tanh_arg(b)
+            cu = self._mul_const(u) if u is not None else None
+            if cu is None:
+                continue
+            c1, s = cu
+            sn = self.prod.get(s)
+            if sn is None or sn.prim != "add" or x not in sn.inputs:
+                continue
+            cube = sn.inputs[1] if sn.inputs[0] == x else sn.inputs[0]
+            sq = self._times(cube, x)
+            lin = self._times(sq, x) if sq is not None else None
+            c2 = self._mul_const(lin) if lin is not None else None
+            if c2 is None or c2[1] != x:
+                continue
+            return x, c1, c2[0]
+        return None
+
     def _row_shifted(self, var):
         """Whether ``var`` is x - s with s a per-row value of this row kernel (a softmax's shifted logits)."""
         m = self.prod.get(var)
@@ -501,21 +555,21 @@ class Emitter:
         def same(k=0):
             return self.value(n.inputs[k], idx)
 
+        if p == "mul" and dt == "float32" and Emitter.ONEP_TANH:
+            g = self._gelu_tanh(n)
+            if g is not None:
+                x, c1, c2 = g
+                k = -2.0 * c1 * 1.4426950408889634
+                self.emit(f"const float {out} = gelu_tanh_f32({self.value(x, idx)}, {_f32_hex(k)}, "
+                          f"{_f32_hex(k * c2)});")
+                return out
         if p == "add" and dt == "float32" and Emitter.ONEP_TANH:
             u = self._onep_tanh_arg(n)
             if u is not None:
-                m = self.prod.get(u)
-                c = None
-                if m is not None and m.prim == "mul":
-                    for j in (0, 1):
-                        c = self._const(m.inputs[j])
-                        if isinstance(c, float) and c == c and abs(c) != float("inf"):
-                            x = m.inputs[1 - j]
-                            break
-                        c = None
-                if c is not None:
-                    k = float(-2.0 * c * 1.4426950408889634)
-                    self.emit(f"const float {out} = onep_tanh_k({self.value(x, idx)}, {k.hex()}f);")
+                cu = self._mul_const(u)
+                if cu is not None:
+                    k = -2.0 * cu[0] * 1.4426950408889634
+                    self.emit(f"const float {out} = onep_tanh_k({self.value(cu[1], idx)}, {_f32_hex(k)});")
                 else:
                     self.emit(f"const float {out} = onep_tanh_f32({self.value(u, idx)});")
                 return out
@@ -797,6 +851,13 @@ class Emitter:
         from lumen_amd.compiler.fusion import row_broadcast
 
         return self.rows is not None and row_broadcast(src, out, dims, self.rows)
+
+
+def _f32_hex(v):
+    """``v`` rounded to float32, as an exact C hex-float literal."""
+    import numpy as np
+
+    return f"{float(np.float32(v)).hex()}f"
 
 
 def _red_identity(prim, dt):
@@ -1130,9 +1191,9 @@ class LoopKernel:
         else:
             src += [
                 "  const int tid = threadIdx.x; const int lane = tid & 63; const int wave = tid >> 6;",
-                "  const int64_t r = blockIdx.x;",
                 "  __shared__ double red_lds[16];",
                 "  __shared__ int64_t red_ldsi[16];",
+                "  const int64_t r = blockIdx.x;",
             ]
         src += ["  (void)lane; (void)wave;"]
         # vector loads need the c indices declared before them: emit prologue after index decls

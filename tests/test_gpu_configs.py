@@ -441,3 +441,58 @@ def test_float32_division_is_within_1_ulp(hip):
     tail_g, tail_w = got[n:], want[n:]
     same = (tail_g.view(np.uint32) == tail_w.view(np.uint32)) | (np.isnan(tail_g) & np.isnan(tail_w))
     assert same.all(), (tail_g, tail_w)
+
+
+def test_gelu_tanh_form_matches_float64_and_oracle(hip):
+    """The traced tanh GELU, evaluated in its sigmoid form x / (1 + 2^(x (k + k c2 x^2))): within 1e-5 relative of
+    float64 GELU (tanh form) on [-10, 10] and within rtol 1e-4 (atol 1e-4 of the largest value) of the oracle,
+    which evaluates the traced float32 graph (its 1 + tanh(u) loses relative accuracy as tanh(u) nears -1, so
+    the oracle comparison is scaled by the largest value, as the float32 checks elsewhere). +inf gives inf,
+    -inf NaN (0.5 x (1 + tanh u) is -inf * 0 in float32 too), NaN NaN."""
+    x = np.concatenate([np.linspace(-10.0, 10.0, 200001, dtype=np.float32),
+                        np.float32([0.0, -0.0, 1e-30, -1e-30, 1e-3, -1e-3, 30.0, -30.0, np.inf, -np.inf, np.nan])])
+    f = L.compile(lambda x: F.gelu(x), device="hip")
+    got = np.asarray(L.to_numpy(f(L.from_numpy(x))), np.float64)
+    xd = x.astype(np.float64)
+    with np.errstate(all="ignore"):  # 0.5 x (1 + tanh u) = x sigmoid(2u), without the cancellation
+        want = xd / (1.0 + np.exp(-2.0 * 0.7978845608 * (xd + 0.044715 * xd ** 3)))
+    n = 200001 + 8
+    # the exponent's roundings (relative 2^-24 each, three of them) grow with its magnitude: 1e-5 relative down
+    # to x = -8 (exponent -71 in base 2); below that the results are under 1e-18 and leave the float range
+    # near x = -9.4 (-0), as the traced float32 form's do
+    ok = xd[:n] >= -8.0
+    rel = np.abs(got[:n] - want[:n]) / np.maximum(np.abs(want[:n]), 1e-300)
+    assert rel[ok & (want[:n] != 0)].max() <= 1e-5, (rel[ok].max(), x[:n][ok][rel[ok].argmax()])
+    assert np.abs(got[:n][~ok]).max() <= 1e-18
+    assert got[n] == np.inf and np.isnan(got[n + 1]) and np.isnan(got[n + 2])
+    g = L.make_graph(lambda x: F.gelu(x))(L.empty([n], "float32", "meta"))
+    (ref,) = oracle.run(g, [x[:n]])
+    np.testing.assert_allclose(got[:n], ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+
+
+def test_float32_softmax_and_layer_norm_match_float64(hip):
+    """A float32 row softmax (its shifted exponent as one exp2) and layer norm (its quotient as a multiply by
+    the row's reciprocal) against float64 within 1e-5 relative (largest value of the row), and against the
+    oracle within rtol 1e-4; rows with -inf entries give zeros there, a row of equal values a uniform row."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((64, 2048)) * 4.0).astype(np.float32)
+    x[3, ::7] = -np.inf
+    x[5] = 1.5
+    f = L.compile(lambda x: (F.softmax(x, -1), F.layer_norm(x[1:], 2048)), device="hip")
+    sm, ln = (np.asarray(L.to_numpy(t), np.float64) for t in f(L.from_numpy(x)))
+    xd = x.astype(np.float64)
+    e = np.exp(xd - xd.max(-1, keepdims=True))
+    want_sm = e / e.sum(-1, keepdims=True)
+    assert (np.abs(sm - want_sm) / want_sm.max(-1, keepdims=True)).max() <= 1e-5
+    assert np.all(sm[3, ::7] == 0.0) and np.allclose(sm[5], 1.0 / 2048, rtol=1e-6)
+    y = xd[1:]
+    y = np.where(np.isinf(y), 0.0, y)  # the row with -inf entries normalizes to NaN: left out below
+    mu = y.mean(-1, keepdims=True)
+    want_ln = (y - mu) / np.sqrt(((y - mu) ** 2).mean(-1, keepdims=True) + 1e-5)
+    keep = [r for r in range(63) if r != 2]
+    err = np.abs(ln[keep] - want_ln[keep]) / np.maximum(np.abs(want_ln[keep]).max(-1, keepdims=True), 1e-30)
+    assert err.max() <= 1e-5, err.max()
+    g = L.make_graph(lambda x: (F.softmax(x, -1), F.layer_norm(x[1:], 2048)))(L.empty([64, 2048], "float32", "meta"))
+    ref_sm, ref_ln = oracle.run(g, [x])
+    np.testing.assert_allclose(sm, ref_sm, rtol=1e-4, atol=1e-4 * np.abs(ref_sm).max())
+    np.testing.assert_allclose(ln[keep], ref_ln[keep], rtol=1e-4, atol=1e-4 * np.abs(ref_ln[keep]).max())

@@ -405,3 +405,43 @@ def test_flash_backward_scratch_is_what_the_library_reports(mode, shape):
     assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode) == want
     if d == 32 and mode == 0:  # a value head dim above the query's pads the accumulator to the larger one
         assert A.backward_workspace_bytes(b, n, sq, sk, d, n, mode, 96) == want + b * n * sq * 64 * 4
+
+
+def _chain2(x, a, b):
+    t = F.gelu((x * a + b).float())
+    return F.softmax(F.layer_norm(t, x.shape[-1]), -1).bfloat16()
+
+
+def test_gelu_softmax_and_row_divisions_take_their_short_forms():
+    """The config-2 chain's row kernel evaluates the traced tanh GELU in its sigmoid form (gelu_tanh_f32, no
+    tanh_f32), softmax's exponent of the row-shifted value as one exp2 (exp_shifted_f32) and both row
+    divisions as multiplies by the row's reciprocal (fdiv_rowm); exp and division elsewhere keep their
+    within-4-ulp and within-1-ulp forms."""
+    p = _plan(_chain2, ((64, 512), "bfloat16"), ((512,), "bfloat16"), ((512,), "bfloat16"))
+    (src,) = p.sources.values()
+    body = src[src.index('extern "C"'):]
+    n = body.count("gelu_tanh_f32(")  # one an element a thread
+    assert n >= 8 and "tanh_f32(" not in body.replace("gelu_tanh_f32(", "")
+    assert body.count("exp_shifted_f32(") == n and "exp_f32(" not in body.replace("exp_shifted_f32(", "")
+    assert body.count("fdiv_rowm(") == 2 * n and "fdiv_f32(" not in body and "fdiv_row(" not in body
+    q = _plan(lambda x, y: F.exp(x) / y, ((64, 512), "float32"), ((64, 512), "float32"))
+    (src,) = q.sources.values()
+    body = src[src.index('extern "C"'):]
+    assert "exp_f32(" in body and "fdiv_f32(" in body and "exp_shifted_f32(" not in body
+
+
+def test_one_plus_tanh_keeps_tanh_when_tanh_is_read_elsewhere():
+    """1 + tanh(u) becomes 2 sigmoid(2u) only when nothing else reads the tanh (GELU's backward reads it, so
+    the training step keeps tanh_f32 there)."""
+    p = _plan(lambda u: (1.0 + F.tanh(u)) * 3.0, ((64, 256), "float32"))
+    (src,) = p.sources.values()
+    body = src[src.index('extern "C"'):]
+    assert "onep_tanh_f32(" in body and "tanh_f32(" not in body.replace("onep_tanh", "")
+    p = _plan(lambda u: F.tanh(u * 0.5) + 1.0, ((64, 256), "float32"))
+    (src,) = p.sources.values()
+    body = src[src.index('extern "C"'):]
+    assert "onep_tanh_k(" in body and "tanh_f32(" not in body.replace("onep_tanh", "")
+    p = _plan(lambda u: (1.0 + F.tanh(u)) * F.tanh(u), ((64, 256), "float32"))
+    (src,) = p.sources.values()
+    body = src[src.index('extern "C"'):]
+    assert "tanh_f32(" in body and "onep_tanh" not in body
