@@ -149,6 +149,10 @@ DEV float fdiv_rowm(float a, float b, float r, int ok) {
 // The exponent's rounding (relative 2^-24 of |2u log2 e|) bounds the error: under 1e-6 relative for |u| < 8,
 // 2e-5 at the underflow end; u = +-inf gives 2 and 0, NaN propagates.
 DEV float onep_tanh_f32(float u) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u)); }
+// tanh(u) as 1 - 2 / (1 + 2^(2u log2 e)): one exp2 and one reciprocal, absolute error under 3e-7 everywhere but
+// not relative near 0, so it serves readers that use tanh(u) in 1 +- tanh(u) and tanh(u)^2 (GELU's derivative),
+// whose values carry that absolute error in float32 anyway; +-inf give +-1, NaN propagates
+DEV float tanh_abs_f32(float u) { return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.8853900817779268f * u)), 1.0f); }
 // the same with u = c x folded into one product (the tanh argument of GELU's tanh form): k = -2 c log2 e
 DEV float onep_tanh_k(float x, float k) { return 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(k * x)); }
 // GELU's tanh form 0.5 x (1 + tanh(c1 (x + c2 x^3))) as x sigmoid(2 c1 x (1 + c2 x^2)) = x / (1 + 2^(x (k + k c2 x^2)))
@@ -322,7 +326,10 @@ class Emitter:
         self.uniform: set = set()     # C names of per-row values (the same on every lane of a row's wave)
         self.recips: dict = {}        # uniform divisor name -> (reciprocal name, range-flag name)
         self.rounded: dict = {}       # name of a bf16-rounded float -> the name it was rounded from
-        self._users = None            # the graph's readers of each value, built on first need
+        self._users = None            # readers of each value, built on first need
+        # the values the kernel stores (None: unknown, so every reader in the graph counts): a value another
+        # step reads is one of them, or that step computes it again from stored operands
+        self.outputs = None
 
     def tmp(self, prefix="t"):
         self.count += 1
@@ -464,21 +471,48 @@ class Emitter:
     def _onep_tanh_arg(self, n):
         """For ``n`` = 1 + tanh(u) (either order) where the kernel computes the tanh and every reader of it in
         the graph is such a sum: u, else None."""
-        if self._users is None:
-            self._users = self.graph.users()
         for k in (0, 1):
             t = self.prod.get(n.inputs[k])
             if t is None or t.prim != "tanh" or self._const(n.inputs[1 - k]) != 1.0:
                 continue
             if t.inputs[0] in self.given or self.graph.types[t.inputs[0]].dtype != "float32":
                 continue
-            readers = self._users.get(t.output, [])
-            if t.output in self.graph.outputs or not all(
+            readers = self._readers(t.output)
+            stored = self.graph.outputs if self.outputs is None else self.outputs
+            if t.output in stored or not all(
                     r.prim == "add" and any(r.inputs[j] == t.output and self._const(r.inputs[1 - j]) == 1.0
                                             for j in (0, 1)) for r in readers):
                 continue
             return t.inputs[0]
         return None
+
+    def _readers(self, var):
+        if self._users is None:
+            if self.outputs is None:
+                self._users = self.graph.users()
+            else:  # readers inside the kernel
+                self._users = {}
+                for m in self.prod.values():
+                    for v in m.inputs:
+                        self._users.setdefault(v, []).append(m)
+        return self._users.get(var, [])
+
+    def _tanh_abs_ok(self, t):
+        """Whether every reader of tanh node ``t`` takes 1 + t, 1 - t or t * t (so an absolute error bound
+        serves), and the kernel does not store it."""
+        stored = self.graph.outputs if self.outputs is None else self.outputs
+        if t.output in stored:
+            return False
+        v = t.output
+        for r in self._readers(v):
+            if r.prim == "mul" and r.inputs == (v, v):
+                continue
+            if r.prim == "add" and any(r.inputs[j] == v and self._const(r.inputs[1 - j]) == 1.0 for j in (0, 1)):
+                continue
+            if r.prim == "sub" and r.inputs[1] == v and self._const(r.inputs[0]) == 1.0:
+                continue
+            return False
+        return bool(self._readers(v))
 
     def _mul_const(self, var):
         """(c, y) when ``var`` is the product of a finite float scalar fill c and y (either order), else None."""
@@ -657,7 +691,9 @@ class Emitter:
             }.get(p)
             s = "f" if f32 else ""
             one = "1.0f" if f32 else "1.0"
-            if p == "tanh" and f32:
+            if p == "tanh" and f32 and Emitter.ONEP_TANH and dt == "float32" and self._tanh_abs_ok(n):
+                expr = f"tanh_abs_f32({a})"
+            elif p == "tanh" and f32:
                 expr = f"tanh_f32({a})"
             elif p == "exp" and f32 and Emitter.SHIFTED_EXP and self._row_shifted(n.inputs[0]):
                 expr = f"exp_shifted_f32({a})"
@@ -962,7 +998,9 @@ class LoopKernel:
 
     def _emitter(self, rows=None):
         ins = {v: (k, self.views[v]) for k, v in enumerate(self.step.inputs)}
-        return Emitter(self.graph, self.step.nodes, ins, rows)
+        em = Emitter(self.graph, self.step.nodes, ins, rows)
+        em.outputs = set(self.step.outputs)
+        return em
 
     # ---- elementwise
     def _loop(self):
@@ -1452,6 +1490,7 @@ class GemmEpilogueKernel:
         lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views, self.aliased)
         lk.far = self.far
         em = Emitter(g, loop.nodes, {v: (k, self.views[v]) for k, v in enumerate(lin)})
+        em.outputs = set(loop.outputs)
         em.vec = 4
         accs = [f"acc.{c}" for c in "xyzw"]
         dnames = []

@@ -496,3 +496,26 @@ def test_float32_softmax_and_layer_norm_match_float64(hip):
     ref_sm, ref_ln = oracle.run(g, [x])
     np.testing.assert_allclose(sm, ref_sm, rtol=1e-4, atol=1e-4 * np.abs(ref_sm).max())
     np.testing.assert_allclose(ln[keep], ref_ln[keep], rtol=1e-4, atol=1e-4 * np.abs(ref_ln[keep]).max())
+
+
+def test_gelu_gradient_matches_float64_and_oracle(hip):
+    """The derivative of the traced tanh GELU (its tanh read in 1 + t and t * t, evaluated as
+    1 - 2 / (1 + 2^(2u log2 e))) against float64 within 1e-4 absolute on [-10, 10] (the derivative is at most
+    1.13 in magnitude) and against the oracle within rtol 1e-4 (atol 1e-4 of the largest value)."""
+    x = np.linspace(-10.0, 10.0, 100001, dtype=np.float32)
+    g = np.cos(x).astype(np.float32)
+
+    def f(x, g):
+        _, pull = L.vjp(lambda x: F.gelu(x), x)
+        return pull(g)[0]
+
+    fc = L.compile(f, device="hip")
+    got = np.asarray(L.to_numpy(fc(L.from_numpy(x), L.from_numpy(g))), np.float64)
+    xd = x.astype(np.float64)
+    u = 0.7978845608 * (xd + 0.044715 * xd ** 3)
+    t = np.tanh(u)
+    want = g * (0.5 * (1.0 + t) + 0.5 * xd * (1.0 - t * t) * 0.7978845608 * (1.0 + 3.0 * 0.044715 * xd * xd))
+    assert np.abs(got - want).max() <= 1e-4, np.abs(got - want).max()
+    gr = L.make_graph(f)(*[L.empty([x.size], "float32", "meta")] * 2)
+    (ref,) = oracle.run(gr, [x, g])
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())

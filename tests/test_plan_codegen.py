@@ -445,3 +445,17 @@ def test_one_plus_tanh_keeps_tanh_when_tanh_is_read_elsewhere():
     (src,) = p.sources.values()
     body = src[src.index('extern "C"'):]
     assert "tanh_f32(" in body and "onep_tanh" not in body
+
+
+def test_training_step_gelu_takes_the_sigmoid_forms():
+    """In the training step, the forward GELU (whose tanh the backward recomputes from the stored
+    pre-activation) runs in its sigmoid form, and the backward's tanh, read only in 1 + t and t * t, as
+    tanh_abs_f32; no kernel keeps the polynomial tanh_f32."""
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=False)
+    bodies = [src[src.index("struct Epi") if "struct Epi" in src else src.index('extern "C"'):]
+              for src in p.sources.values()]
+    assert sum("gelu_tanh_f32(" in b for b in bodies) >= 2  # one a layer
+    assert sum("tanh_abs_f32(" in b for b in bodies) >= 2
+    assert not any(" tanh_f32(" in b for b in bodies)
