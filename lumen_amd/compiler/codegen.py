@@ -1258,9 +1258,14 @@ class LoopKernel:
         atomic = red.prim == "reduce_sum" and out_dt == "float32" and Q >= 64
         chunk = max(1, min(Q, 64)) if atomic else Q
         nchunks = -(-Q // chunk)
-        if atomic and tuple(axes) == tuple(range(len(axes))) and O % 4 == 0 and O >= 1024:
-            chunk = max(1, min(Q, self.LEAD_CHUNK))
-            return self._reduce_leading(red, Q, O, chunk, -(-Q // chunk))
+        if atomic and tuple(axes) == tuple(range(len(axes))) and O % 4 == 0 and O >= 256:
+            # narrow sums ([8192, 512] -> [512]) take 64 columns x 16 row lanes a workgroup and longer chunks: as
+            # many workgroups as 256 columns x 4 row lanes would give, a quarter of the atomic adds (the adds to
+            # the few output columns, not the loads, bound these)
+            cl = 64 if O >= 1024 else 16
+            chunk = self.LEAD_CHUNK * (64 // cl)
+            chunk = max(1, min(Q, chunk))
+            return self._reduce_leading(red, Q, O, chunk, -(-Q // chunk), cl)
         em = self._emitter()
         om = em.multi(("flat", "o"), oshape)
         qm = em.multi(("flat", "q"), rshape)
@@ -1294,12 +1299,13 @@ class LoopKernel:
         return "\n".join(src)
 
 
-    def _reduce_leading(self, red, Q, O, chunk, nchunks):
+    def _reduce_leading(self, red, Q, O, chunk, nchunks, cl=64):
         """float32 sum over the leading axes of a [Q, O] row-major value (a bias or norm-weight gradient): a
-        workgroup covers 256 columns of ``chunk`` rows, each thread 4 consecutive columns (16-byte loads) of
-        every fourth row; the four row lanes combine through LDS and the workgroup adds its 256 sums atomically
-        into the zero-filled output (one atomic a column per chunk: the adds, not the loads, bound this kernel
-        when chunks are short)."""
+        workgroup covers 4 ``cl`` columns of ``chunk`` rows, each thread 4 consecutive columns (16-byte loads) of
+        every (256 / ``cl``)-th row; the row lanes combine through LDS and the workgroup adds its column sums
+        atomically into the zero-filled output (one atomic a column per chunk: the adds, not the loads, bound
+        this kernel when chunks are short)."""
+        rl = 256 // cl
         g = self.graph
         em = self._emitter()
         em.vec = 4
@@ -1309,22 +1315,22 @@ class LoopKernel:
         body = self._vec_prologue(em, 4) + em.lines
         self.atomic = True
         threads = 256
-        self.grid, self.block, self.lds = (-(-O // 256), nchunks, 1), (threads, 1, 1), 0
+        self.grid, self.block, self.lds = (-(-O // (4 * cl)), nchunks, 1), (threads, 1, 1), 0
         view = self.out_views[red.output]
         oshape = g.types[red.output].shape
-        adds = [f"atomicAdd(&out0[{self._out_addr(view, oshape, f'(o + {l})')}], part[0][tx][{l}] + part[1][tx][{l}]"
-                f" + part[2][tx][{l}] + part[3][tx][{l}]);" for l in range(4)]
+        adds = [f"atomicAdd(&out0[{self._out_addr(view, oshape, f'(o + {l})')}], "
+                + " + ".join(f"part[{r}][tx][{l}]" for r in range(rl)) + ");" for l in range(4)]
         src = [
             f'extern "C" __global__ __launch_bounds__({threads}) void {self.name}({self._params()}) {{',
-            "  __shared__ float part[4][64][4];",
-            "  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;",
-            f"  const int64_t o = ((int64_t)blockIdx.x * 64 + tx) * 4;",
+            f"  __shared__ float part[{rl}][{cl}][4];",
+            f"  const int tx = threadIdx.x % {cl}, ty = threadIdx.x / {cl};",
+            f"  const int64_t o = ((int64_t)blockIdx.x * {cl} + tx) * 4;",
             f"  const int64_t q0 = (int64_t)blockIdx.y * {chunk}LL;",
             f"  const int64_t q1 = min(q0 + {chunk}LL, {Q}LL);",
             "  float acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;",
             f"  if (o < {O}LL) {{",
             f"#pragma unroll {self.LEAD_UNROLL}",
-            "  for (int64_t q = q0 + ty; q < q1; q += 4) {",
+            f"  for (int64_t q = q0 + ty; q < q1; q += {rl}) {{",
             f"    const int64_t qb = q * {O}LL + o;",
         ]
         src += ["    " + l for l in body]

@@ -288,11 +288,13 @@ def test_each_gemm_epilogue_k_loop_gives_the_first_ones_bits(hip, variant, monke
         assert np.array_equal(a, b_)
 
 
-@pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,))])
+@pytest.mark.parametrize("shape,axes", [((1000, 2048), (0,)), ((3, 70, 1024), (0, 1)), ((130, 4100), (0,)),
+                                        ((8192, 512), (0,)), ((1100, 260), (0,)), ((5, 600, 768), (0, 1))])
 def test_leading_axis_sums_match_oracle(hip, shape, axes):
-    """float32 sums over leading axes (the vectorized reduce kernel: four columns a thread, 64-row chunks
-    added atomically; 4100 columns is not a multiple of 4 x 256 threads) against the oracle's sequential sum
-    (float32 reassociation: rtol 1e-4 of the sum of magnitudes)."""
+    """float32 sums over leading axes (the vectorized reduce kernel: four columns a thread, row chunks added
+    atomically; 4100 columns is not a multiple of 4 x 256 threads; under 1024 columns a workgroup takes 64
+    columns of 16 row lanes, 260 of them ragged) against the oracle's sequential sum (float32 reassociation:
+    rtol 1e-4 of the sum of magnitudes)."""
     rng = np.random.default_rng(9)
     x = rng.standard_normal(shape).astype(np.float32)
 
