@@ -112,6 +112,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--attn-shape", default="8,2048,16,128", help="config 3: B,S,N,D of the attention")
     ap.add_argument("--attn-config", type=int, default=-1, help="config 3: the forward tile config (-1 default)")
+    ap.add_argument("--attn-mode", type=int, default=1, choices=[0, 1, 2],
+                    help="config 3: the backward's dQ mode (nhip_attn_desc.deterministic; 1 default)")
     ap.add_argument("--gemm-shape", default="8192,8192,8192", help="gemm: m,n,k")
     ap.add_argument("--gemm-config", type=int, default=-1, help="gemm: the tile config (-1 default)")
     ap.add_argument("--gemm-out", default="f32", choices=["f32", "bf16"], help="gemm: the output dtype")
@@ -453,7 +455,9 @@ def _config3(args):
     desc = nv.AttnDesc()
     desc.batch, desc.heads, desc.kv_heads, desc.sq, desc.sk, desc.head_dim = b, n, n, s, s, d
     desc.dtype, desc.causal, desc.scale, desc.config = 1, 1, 1.0 / math.sqrt(d), args.attn_config
-    desc.deterministic = 1  # dQ by its own kernel (the plans' default; faster here than atomic adds)
+    # dQ from the dS tiles the dK/dV kernel stores (1: the plans' default), by a kernel recomputing S and dP (2)
+    # or added atomically (0)
+    desc.deterministic = args.attn_mode
     desc.q_b, desc.q_s, desc.q_n = s * n * d, n * d, d
     for nm in ("k", "v", "o", "do", "dq", "dk", "dv"):
         setattr(desc, f"{nm}_b", s * n * d)
