@@ -366,6 +366,16 @@ class Emitter:
         kind = idx[0]
         if kind == "multi":
             return list(idx[1])
+        if kind == "rc" and self.rows is not None and shape:
+            # a row kernel's (row, column) index over a value whose trailing dims span the row: the leading
+            # indices from the row alone (the same for the whole row, computed once) and the trailing ones from
+            # the column, instead of decomposing r * C + c with 64-bit divisions for every element
+            R, C = self.rows
+            for k in range(len(shape), -1, -1):
+                if math.prod(shape[k:]) == C and math.prod(shape[:k]) == R:
+                    return self._split(idx[1], shape[:k]) + self._split(idx[2], shape[k:])
+                if math.prod(shape[k:]) > C:
+                    break
         f = self.flat(idx, shape)
         if not shape:
             return []
@@ -378,6 +388,24 @@ class Emitter:
                 out.append(f"(({f}) / {st[0]}LL)")
             else:
                 out.append(f"((({f}) / {st[d]}LL) % {n}LL)")
+        return out
+
+    @staticmethod
+    def _split(e, shape):
+        """The row-major multi-index of flat index expression ``e`` over ``shape``."""
+        if not shape:
+            return []
+        st = _contig(shape)
+        out = []
+        for d, n in enumerate(shape):
+            if n == 1:
+                out.append("0")
+            elif len(shape) == 1:
+                out.append(f"({e})")
+            elif d == 0:
+                out.append(f"(({e}) / {st[0]}LL)")
+            else:
+                out.append(f"((({e}) / {st[d]}LL) % {n}LL)")
         return out
 
     def flat(self, idx, shape):

@@ -459,3 +459,21 @@ def test_training_step_gelu_takes_the_sigmoid_forms():
     assert sum("gelu_tanh_f32(" in b for b in bodies) >= 2  # one a layer
     assert sum("tanh_abs_f32(" in b for b in bodies) >= 2
     assert not any(" tanh_f32(" in b for b in bodies)
+
+
+def test_row_kernel_indices_split_into_row_and_column():
+    """A row kernel reading a value at (row, column) through a gather or a broadcast over leading dims indexes it
+    by the row (once a row) and the column, not by decomposing r * C + c with 64-bit divisions for every element
+    (the training step's embedding row: the token id read once a row, the table row and the position row
+    indexed by the column)."""
+    import re
+
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=False)
+    gathers = [src for si, src in p.sources.items() if p.steps[si].kind == "row" and "gather" in p.steps[si].label()]
+    assert gathers
+    for src in gathers:
+        body = src[src.index('extern "C"'):]
+        for ix in re.findall(r"\bin\d+\[([^\]]*)\]", body):
+            assert not ("r * " in ix and "/" in ix), ix
