@@ -85,6 +85,28 @@ def test_integer_scatter_add_is_exact(hip):
     _check(lambda a, i, u: prims.scatter_add(a, i, u, 0), xf, idf, uf)
 
 
+def test_float_scatter_add_of_rows(hip):
+    """float32 scatter_add of whole rows along axis 0 (an embedding gradient's form: [B, S] ids, [B, S, D]
+    updates into [V, D]) with repeated ids and ids clamped from below and above: bit for bit with small-integer
+    updates (every partial sum exact), and within float32 reassociation (rtol 1e-5 of the summed magnitudes)
+    with normal ones."""
+    rng = np.random.default_rng(4)
+    x = rng.integers(-4, 5, (300, 512)).astype(np.float32)
+    ids = rng.integers(-5, 305, (7, 90)).astype(np.int64)
+    ids[0, :40] = 17  # one row hit 40 times
+    upd = rng.integers(-8, 9, (7, 90, 512)).astype(np.float32)
+    got = _check(lambda a, i, u: prims.scatter_add(a, i, u, 0), x, ids, upd, kinds={"scatter_add", "copy", "fill"})
+    uf = rng.standard_normal((7, 90, 512)).astype(np.float32)
+    fn = lambda a, i, u: prims.scatter_add(a, i, u, 0)  # noqa: E731
+    f = L.compile(fn, device="hip")
+    out = np.asarray(L.to_numpy(f(L.from_numpy(x), L.from_numpy(ids), L.from_numpy(uf))), np.float64)
+    (want,) = oracle.run(L.make_graph(fn)(*[L.from_numpy(a) for a in (x, ids, uf)]), [x, ids, uf])
+    mag = np.abs(x).astype(np.float64)
+    np.add.at(mag, np.clip(ids, 0, 299).ravel(), np.abs(uf).reshape(-1, 512))
+    assert np.all(np.abs(out - want) <= 1e-5 * mag + 1e-6)
+    del got
+
+
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 def test_argmax_argmin_ties_and_nan(hip, dtype):
     """The first index of the maximum / minimum: ties resolve to the smallest position, a row holding NaN
