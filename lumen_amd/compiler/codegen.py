@@ -44,9 +44,12 @@ DEV float lb_bf16(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
 // float32 -> bfloat16 round to nearest even, NaN -> (bits >> 16) | 0x40: gfx950's v_cvt_pk_bf16_f32, equal to
 // that integer rounding on all 2^32 float32 inputs (checked on MI355X)
 DEV uint16_t sb_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
-DEV float r_bf16(float f) { return lb_bf16(sb_bf16(f)); }
 typedef float lk_f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 lk_bf16x2 __attribute__((ext_vector_type(2)));
+// float32 rounded to bfloat16 and widened back: the pair {0, f} converted in one v_cvt_pk_bf16_f32 puts bf16(f)
+// in the high half over a zero low half, which is that value as a float32 (the same bits as
+// lb_bf16(sb_bf16(f)), NaN included), without the shift
+DEV float r_bf16(float f) { return __builtin_bit_cast(float, __builtin_convertvector((lk_f32x2){0.0f, f}, lk_bf16x2)); }
 // two float32 -> bfloat16 (a in the low half) in one v_cvt_pk_bf16_f32
 DEV uint32_t sb2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((lk_f32x2){a, b}, lk_bf16x2));

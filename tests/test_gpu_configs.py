@@ -351,7 +351,8 @@ def test_bf16_stores_round_to_nearest_even_bit_for_bit(hip):
     """float32 -> bfloat16 in generated kernels (the hardware conversion) against the reference's rounding
     restated on the host (round to nearest even; NaN -> its top 16 bits with the quiet bit): every tie and
     half-ulp neighbour of a sweep of exponents, NaN payloads of both signs, infinities, subnormals, the
-    largest finite values, and 2^24 random bit patterns, bit for bit."""
+    largest finite values, and 2^24 random bit patterns, bit for bit; stored as bfloat16 and rounded inside a
+    kernel then widened back to float32."""
     rng = np.random.default_rng(12)
     hi = (np.arange(0, 1 << 16, 7, dtype=np.uint32) << 16)
     lows = np.uint32([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x4000, 0xC000])
@@ -364,6 +365,12 @@ def test_bf16_stores_round_to_nearest_even_bit_for_bit(hip):
     f = L.compile(lambda x: x.bfloat16(), device="hip")
     got = np.asarray(f(L.from_numpy(x)).raw()).view(np.uint16).ravel()
     assert np.array_equal(got, D.bf16_bits(x))
+    # the rounding inside a kernel, widened back to float32 (r_bf16: one conversion of the pair {0, x}, whose
+    # high half over a zero low half is the rounded value)
+    f = L.compile(lambda x: x.bfloat16().float(), device="hip")
+    got = np.asarray(f(L.from_numpy(x)).raw()).view(np.uint32).ravel()
+    assert all("r_bf16(" in src for src in f.plan.sources.values())
+    assert np.array_equal(got, D.bf16_bits(x).astype(np.uint32) << 16)
 
 
 def test_float32_exp_is_within_4_ulp(hip):
