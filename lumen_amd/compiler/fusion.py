@@ -329,10 +329,10 @@ def _inputs_of(nodes):
 def _rematerialize(graph, steps, prod):
     """Recomputes values instead of storing them (``passes/fusion/mod.rs`` duplicates cheap producers the
     same way). A loop or row kernel that reads a value computed elementwise from values already in memory
-    computes it itself, when the new operands it reads hold at most the replaced value's bytes (or at most
-    1 MiB): the training graph's backward kernels then recompute an activation's
-    intermediates (GELU's tanh argument and friends) from its input instead of reading them back, and the
-    forward kernels stop writing them."""
+    computes it itself from the nearest stored ones, when the new operands it reads hold at most the replaced
+    value's bytes (or at most 1 MiB): the training graph's backward kernels then recompute an activation's
+    intermediates (GELU's tanh argument and friends) from its input instead of reading them back, read a norm's
+    per-row statistic instead of its broadcast over the row, and the forward kernels stop writing them."""
     in_memory = set(graph.inputs)
     for st in steps:
         in_memory.update(st.outputs)
@@ -353,7 +353,10 @@ def _rematerialize(graph, steps, prod):
                     if v in expr:
                         continue
                     m = prod.get(v)
-                    if m is None or m.prim not in REMAT:
+                    # a value some step stores already is read, not recomputed: a row statistic broadcast over
+                    # the row ([R, 1] -> [R, C]) is read as the [R, 1] vector its kernel stores, a float32 copy
+                    # of a stored bf16 value as that value, whatever computed them
+                    if m is None or m.prim not in REMAT or (v != u and v in in_memory):
                         if v not in in_memory:
                             ok = False
                         leaves.add(v)

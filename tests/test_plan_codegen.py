@@ -477,3 +477,27 @@ def test_row_kernel_indices_split_into_row_and_column():
         body = src[src.index('extern "C"'):]
         for ix in re.findall(r"\bin\d+\[([^\]]*)\]", body):
             assert not ("r * " in ix and "/" in ix), ix
+
+
+def test_norm_statistics_are_read_not_stored_broadcast():
+    """The training step's forward norm rows store the per-row statistic ([rows, 1]) and bf16 values only: no
+    step writes a float32 [rows, width] broadcast of a row statistic, nor a float32 copy of a stored bf16 value
+    that only loop and row kernels read (they recompute those from what is stored)."""
+    model, opt = W.build(W.TINY)
+    ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
+    p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=False)
+    g, prod = p.graph, p.graph.producers()
+    for st in p.steps:
+        if st.kind not in ("loop", "row"):
+            continue
+        for v in st.outputs:
+            n = prod.get(v)
+            if n is None or g.types[v].dtype != "float32" or len(g.types[v].shape) < 2:
+                continue
+            src = g.types[n.inputs[0]] if n.inputs else None
+            assert not (n.prim == "broadcast_in_dim" and src is not None and src.numel() * 8 <= g.types[v].numel()), \
+                (st.label(), v)
+            readers = [s.kind for s in p.steps if v in s.inputs]
+            if readers and all(k in ("loop", "row") for k in readers):  # kernels that can recompute it
+                assert not (n.prim == "cast" and src is not None and src.dtype == "bfloat16" and n.inputs[0] in
+                            {o for s in p.steps for o in s.outputs}), (st.label(), v)
