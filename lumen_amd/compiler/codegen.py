@@ -500,8 +500,9 @@ class Emitter:
         return n.params["fill_value"] if n is not None and n.prim == "full" else None
 
     def _onep_tanh_arg(self, n):
-        """For ``n`` = 1 + tanh(u) (either order) where the kernel computes the tanh and every reader of it in
-        the graph is such a sum: u, else None."""
+        """For ``n`` = 1 + tanh(u) (either order) where the kernel computes the tanh, does not store it, and
+        every reader of it (in the kernel when its stored values are known, else in the graph) is such a sum: u,
+        else None."""
         for k in (0, 1):
             t = self.prod.get(n.inputs[k])
             if t is None or t.prim != "tanh" or self._const(n.inputs[1 - k]) != 1.0:
