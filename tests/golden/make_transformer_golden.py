@@ -1,6 +1,7 @@
 """Writes the transformer golden fixtures (``transformer_<case>.npz``) with the CPU oracle: the loss, and for
 every parameter a fixed sample of its gradient and of its SGD-updated weight, plus each gradient's norm and
-largest magnitude. Run from the repository root: ``python -m tests.golden.make_transformer_golden [case ...]``.
+largest magnitude and the sum and norm of its every row and column. Run from the repository root:
+``python -m tests.golden.make_transformer_golden [case ...]``.
 
 The oracle evaluates the same traced graph the GPU test compiles (``trace`` of ``step_with_grads``).
 """
@@ -48,6 +49,7 @@ def make(case):
     outs = oracle.run(traced.graph, oracle_inputs(traced, ids, targets, weights, names, TC.LR))
     print(f"{case}: oracle {time.time() - t:.1f} s", flush=True)
     pnames = [n for n, _ in model.named_parameters()]
+    shapes = {n: tuple(p.shape) for n, p in model.named_parameters()}
     data = {"loss": np.asarray(outs[0], np.float32)}
     gdt = [traced.graph.types[v].dtype for v in traced.graph.outputs]
     for j, name in enumerate(pnames):
@@ -57,6 +59,12 @@ def make(case):
         data[f"grad/{name}"] = g[idx].astype(np.float32)
         data[f"grad_norm/{name}"] = np.array(np.linalg.norm(g))
         data[f"grad_max/{name}"] = np.array(np.abs(g).max())
+        # every row's and every column's sum and norm (the gradient as [leading dims, last dim]): an error
+        # confined to a few rows or columns, which the sampled entries may miss, moves them
+        g2 = g.reshape(TC.as_rows(shapes[name]))
+        for axis, part in ((1, "row"), (0, "col")):
+            data[f"{part}sum/{name}"] = g2.sum(axis=axis).astype(np.float32)
+            data[f"{part}norm/{name}"] = np.sqrt((g2 * g2).sum(axis=axis)).astype(np.float32)
     written = {names[id(traced.weights[k])]: 1 + len(pnames) + j for j, k in enumerate(traced.written)}
     for name in pnames:
         w = np.asarray(outs[written[name]]).ravel()  # bf16 bits

@@ -3,8 +3,9 @@ oracle, and the GPU test, which runs the same program compiled for hip).
 
 Each case is the benchmark decoder (``lumen_amd.workloads``) at a named size: ``config4_b1`` is config 4's
 model at its real shapes (vocab 32000, d 512, 8 heads, FFN 2048, seq 512, 2 layers) with batch 1 of the 16;
-``config5_layer`` is one config-5 layer (d 2048, 16 heads of 128, FFN 8192, vocab 32000) at batch 1 with the
-sequence shortened from 4096 to ``CONFIG5_SEQ`` so the single-threaded-per-row oracle finishes in minutes.
+``config5_layer`` is one config-5 layer (d 2048, 16 heads of 128, FFN 8192, vocab 32000) at batch 1 and
+sequence ``CONFIG5_SEQ`` (config 5's own 4096; the oracle, threaded over rows, finishes it in about 7
+minutes).
 The program is one SGD training step that also returns every gradient, so one run yields the loss, each
 gradient and each updated weight.
 """
@@ -43,6 +44,14 @@ def setup(cfg):
     W.load(model, weights)
     ids, targets = W.batch(cfg)
     return model, opt, weights, ids, targets
+
+
+def as_rows(shape):
+    """A parameter's shape as [rows, columns]: its leading dims flattened, its last dim the columns (a vector is
+    one row)."""
+    shape = tuple(shape)
+    cols = shape[-1] if shape else 1
+    return (int(np.prod(shape[:-1], dtype=np.int64)) if len(shape) > 1 else 1, cols)
 
 
 def sample_indices(name, numel, k=SAMPLES):
