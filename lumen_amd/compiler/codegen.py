@@ -166,6 +166,20 @@ DEV float gelu_tanh_f32(float x, float k, float kc2) {
   const float p = fmaf(x * x, kc2, k);
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * p));
 }
+// dy times the derivative of that GELU, d/dx 0.5 x (1 + tanh u) with u = c1 (x + c2 x^3):
+// 0.5 (1 + tanh u) + 0.5 x (1 - tanh^2 u) c1 (1 + 3 c2 x^2) = s (1 + 2 c1 x (1 - s) (1 + 3 c2 x^2)), where
+// s = sigmoid(2u) = 1 / (1 + e) and 1 - s = e s, e = exp(-2u) = 2^(x (k + k c2 x^2)): no cancellation where tanh u
+// nears +-1 (the traced 1 - tanh^2 loses its digits there). a = 2 c1, b = 3 c2. Within 3e-6 relative of the exact
+// value for |x| < 8 (the exponent's rounding and the hardware exp2 and reciprocal). e overflowing (x below about
+// -10) makes s 0 and e s NaN, which the minimum with 1 (its value's bound) replaces, so the result is 0 as the
+// traced form gives; x = +-inf or NaN give NaN, as the traced form does
+DEV float gelu_tanh_grad_f32(float x, float dy, float k, float kc2, float a, float b) {
+  const float x2 = x * x;
+  const float e = __builtin_amdgcn_exp2f(x * fmaf(x2, kc2, k));
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  const float es = fminf(e * s, 1.0f);
+  return (dy * s) * fmaf((a * x) * es, fmaf(x2, b, 1.0f), 1.0f);
+}
 // exp(d) of a row-shifted value d = x - (a row's statistic), softmax's exponent: 2^(d log2 e) on the hardware
 // exp2. The product's rounding bounds the error to 2^-24 |d log2 e| ln 2 relative: under 5.2e-6 for every d
 // whose exponential is a normal float (d > -87.3); -inf gives 0, NaN propagates
@@ -310,6 +324,8 @@ class Emitter:
     ROW_RECIP_MUL = True
     # 1 + tanh(u) whose tanh nothing else reads (GELU's tanh form) evaluated as 2 sigmoid(2u) (onep_tanh_f32)
     ONEP_TANH = True
+    # the traced derivative of the tanh GELU times its cotangent as one closed form (gelu_tanh_grad_f32)
+    GELU_GRAD = True
     # exp of a row-shifted value (softmax) as one exp2 of the scaled argument (within 5.2e-6 relative)
     # instead of exp_f32's split product (within 4 ulp)
     SHIFTED_EXP = True
@@ -333,6 +349,7 @@ class Emitter:
         # the values the kernel stores (None: unknown, so every reader in the graph counts): a value another
         # step reads is one of them, or that step computes it again from stored operands
         self.outputs = None
+        self._gelu_grads: dict = {}   # var -> _gelu_tanh_grad's answer
 
     def tmp(self, prefix="t"):
         self.count += 1
@@ -592,6 +609,86 @@ class Emitter:
             return x, c1, c2[0]
         return None
 
+    # float32 operations a GELU derivative's expression is made of
+    _GRAD_OPS = ("add", "sub", "mul", "neg", "tanh")
+    # points (x, dy) at which a candidate expression is compared with the derivative in float64
+    _GRAD_POINTS = ((-3.1, 0.7), (-1.3, -1.9), (-0.45, 1.1), (0.2, -0.35), (0.8, 2.3), (2.6, -1.2))
+
+    def _gelu_tanh_grad(self, n):
+        """(x, dy, c1, c2) when ``n`` is, as a float32 expression of two values x and dy and scalar constants,
+        dy times the derivative of the tanh GELU 0.5 x (1 + tanh(c1 (x + c2 x^3))), else None. The expression
+        (add, sub, mul, neg and one tanh) is evaluated in float64: the tanh's argument at x = 1 and 2 gives c1
+        and c2, and the argument and the whole expression are then compared with their closed forms at fixed
+        points, so any arrangement of the terms matches (autograd's is a sum of eight products)."""
+        if n.output in self._gelu_grads:
+            return self._gelu_grads[n.output]
+        self._gelu_grads[n.output] = None
+        shape = self.graph.types[n.output].shape
+        nodes, leaves, consts, tanhs = {}, set(), {}, []
+        stack = [n.output]
+        while stack:
+            v = stack.pop()
+            if v in nodes or v in leaves or v in consts:
+                continue
+            c = self._const(v)
+            if c is not None:
+                if not isinstance(c, float):
+                    return None
+                consts[v] = c
+                continue
+            m = self.prod.get(v)
+            if v in self.given or v in self.inputs or m is None or m.prim not in self._GRAD_OPS:
+                if self.graph.types[v].shape != shape or self.graph.types[v].dtype != "float32":
+                    return None
+                leaves.add(v)
+                continue
+            if self.graph.types[v].dtype != "float32" or len(nodes) >= 48:
+                return None
+            nodes[v] = m
+            if m.prim == "tanh":
+                tanhs.append(m)
+            stack.extend(m.inputs)
+        if len(tanhs) != 1 or len(leaves) != 2:
+            return None
+        arg = tanhs[0].inputs[0]
+
+        def ev(v, env):
+            if v in env:
+                return env[v]
+            if v in consts:
+                return consts[v]
+            m = nodes[v]
+            a = [ev(w, env) for w in m.inputs]
+            r = {"add": lambda: a[0] + a[1], "sub": lambda: a[0] - a[1], "mul": lambda: a[0] * a[1],
+                 "neg": lambda: -a[0], "tanh": lambda: math.tanh(a[0])}[m.prim]()
+            env[v] = r
+            return r
+
+        def close(a, b):
+            return abs(a - b) <= 1e-12 * max(1.0, abs(b))
+
+        for x, dy in (tuple(leaves), tuple(leaves)[::-1]):
+            try:
+                a1, a2 = ev(arg, {x: 1.0, dy: 0.37}), ev(arg, {x: 2.0, dy: 0.37})
+                c1c2 = (a2 - 2.0 * a1) / 6.0  # a(x) = c1 x + c1 c2 x^3
+                c1 = a1 - c1c2
+                if not (c1 != 0.0 and math.isfinite(c1) and math.isfinite(c1c2)):
+                    continue
+                c2 = c1c2 / c1
+                if not all(close(ev(arg, {x: xv, dy: dv}), c1 * (xv + c2 * xv ** 3)) for xv, dv in self._GRAD_POINTS):
+                    continue
+                ok = True
+                for xv, dv in self._GRAD_POINTS:
+                    t = math.tanh(c1 * (xv + c2 * xv ** 3))
+                    want = dv * (0.5 * (1 + t) + 0.5 * xv * (1 - t * t) * c1 * (1 + 3 * c2 * xv * xv))
+                    ok = ok and close(ev(n.output, {x: xv, dy: dv}), want)
+            except (OverflowError, ZeroDivisionError):
+                continue
+            if ok:
+                self._gelu_grads[n.output] = (x, dy, c1, c2)
+                return x, dy, c1, c2
+        return None
+
     def _row_shifted(self, var):
         """Whether ``var`` is x - s with s a per-row value of this row kernel (a softmax's shifted logits)."""
         m = self.prod.get(var)
@@ -628,6 +725,14 @@ class Emitter:
                 k = -2.0 * c1 * 1.4426950408889634
                 self.emit(f"const float {out} = gelu_tanh_f32({self.value(x, idx)}, {_f32_hex(k)}, "
                           f"{_f32_hex(k * c2)});")
+                return out
+        if p in ("add", "sub", "mul") and dt == "float32" and Emitter.GELU_GRAD:
+            g = self._gelu_tanh_grad(n)
+            if g is not None:
+                x, dy, c1, c2 = g
+                k = -2.0 * c1 * 1.4426950408889634
+                self.emit(f"const float {out} = gelu_tanh_grad_f32({self.value(x, idx)}, {self.value(dy, idx)}, "
+                          f"{_f32_hex(k)}, {_f32_hex(k * c2)}, {_f32_hex(2.0 * c1)}, {_f32_hex(3.0 * c2)});")
                 return out
         if p == "add" and dt == "float32" and Emitter.ONEP_TANH:
             u = self._onep_tanh_arg(n)

@@ -528,3 +528,34 @@ def test_gelu_gradient_matches_float64_and_oracle(hip):
     gr = L.make_graph(f)(*[L.empty([x.size], "float32", "meta")] * 2)
     (ref,) = oracle.run(gr, [x, g])
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+
+
+def test_gelu_gradient_closed_form_matches_float64():
+    """The GELU vjp's closed form (gelu_tanh_grad_f32: dy s (1 + 2 c1 x e s (1 + 3 c2 x^2)), s = 1 / (1 + e))
+    against float64 on 2^20 points of [-8, 8] within 4e-6 of the value plus 4e-7 of |dy| (the absolute part
+    for the derivative's zero near x = -0.75, where the sum cancels), and at the ends as the traced form
+    gives: dy itself for large positive x, zero for large negative x (e = 2^(..) overflows there), NaN for
+    +-inf and NaN."""
+    n = 1 << 20
+    x = np.concatenate([np.linspace(-8.0, 8.0, n, dtype=np.float32),
+                        np.array([20.0, 90.0, -20.0, -90.0, np.inf, -np.inf, np.nan], np.float32)])
+    g = (1.0 + 0.5 * np.sin(np.arange(x.size) * 0.37)).astype(np.float32) * np.where(np.arange(x.size) % 2, 1, -1)
+    g = g.astype(np.float32)
+
+    def f(x, g):
+        _, pull = L.vjp(lambda x: F.gelu(x), x)
+        return pull(g)[0]
+
+    fc = L.compile(f, device="hip")
+    got = np.asarray(L.to_numpy(fc(L.from_numpy(x), L.from_numpy(g))), np.float64)
+    assert any("gelu_tanh_grad_f32(" in src for src in fc.plan.sources.values())
+    xd, gd = x[:n].astype(np.float64), g.astype(np.float64)
+    u = 0.7978845608028654 * (xd + 0.044715 * xd ** 3)
+    t = np.tanh(u)
+    want = gd[:n] * (0.5 * (1.0 + t) + 0.5 * xd * (1.0 - t * t) * 0.7978845608028654 * (1.0 + 3.0 * 0.044715 * xd * xd))
+    bound = 4e-6 * np.abs(want) + 4e-7 * np.abs(gd[:n])
+    err = np.abs(got[:n] - want)
+    assert np.all(err <= bound), (float((err / bound).max()), float(xd[np.argmax(err / bound)]))
+    np.testing.assert_array_equal(got[n:n + 2], gd[n:n + 2])
+    assert np.all(got[n + 2:n + 4] == 0.0), got[n + 2:n + 4]
+    assert np.all(np.isnan(got[n + 4:])), got[n + 4:]

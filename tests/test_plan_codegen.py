@@ -449,16 +449,52 @@ def test_one_plus_tanh_keeps_tanh_when_tanh_is_read_elsewhere():
 
 def test_training_step_gelu_takes_the_sigmoid_forms():
     """In the training step, the forward GELU (whose tanh the backward recomputes from the stored
-    pre-activation) runs in its sigmoid form, and the backward's tanh, read only in 1 + t and t * t, as
-    tanh_abs_f32; no kernel keeps the polynomial tanh_f32."""
+    pre-activation) runs in its sigmoid form, and the backward's traced derivative times its cotangent as one
+    closed form (gelu_tanh_grad_f32); no kernel keeps a tanh."""
     model, opt = W.build(W.TINY)
     ids = L.empty([W.TINY.batch, W.TINY.seq], "int64", "meta")
     p = Plan(trace(W.train_step, (model, opt, ids, ids)).graph, build_kernels=False)
     bodies = [src[src.index("struct Epi") if "struct Epi" in src else src.index('extern "C"'):]
               for src in p.sources.values()]
     assert sum("gelu_tanh_f32(" in b for b in bodies) >= 2  # one a layer
-    assert sum("tanh_abs_f32(" in b for b in bodies) >= 2
-    assert not any(" tanh_f32(" in b for b in bodies)
+    assert sum("gelu_tanh_grad_f32(" in b for b in bodies) >= 2
+    assert not any("tanh_f32(" in b.replace("gelu_tanh_f32(", "").replace("gelu_tanh_grad_f32(", "")
+                   for b in bodies)
+
+
+def _gelu_grad_forms(fn):
+    p = _plan(fn, ((64, 256), "float32"), ((64, 256), "float32"))
+    (src,) = p.sources.values()
+    return src[src.index('extern "C"'):]
+
+
+def test_gelu_gradient_short_form_needs_the_whole_derivative():
+    """The closed form replaces an expression only when it is dy times GELU's derivative as a function of
+    (x, dy): the traced vjp and a hand-written arrangement of the same terms take it (a term added outside the
+    derivative stays outside it); the same terms with one coefficient changed, or with a term added among
+    them, keep their traced arithmetic and its tanh."""
+    c1, c2 = 0.7978845608028654, 0.044715
+
+    def vjp(x, g):
+        _, pull = L.vjp(lambda x: F.gelu(x), x)
+        return pull(g)[0]
+
+    def by_hand(scale=1.0, inner=0.0, outer=0.0):
+        def f(x, g):
+            t = F.tanh((x + x * x * x * c2) * c1)
+            a = g * (t + 1.0) * 0.5
+            if inner:
+                a = a + x * g * inner
+            d = a + (x * g) * (1.0 - t * t) * (1.0 + x * x * (3.0 * c2)) * (0.5 * c1 * scale)
+            return d + x * outer if outer else d
+        return f
+
+    for fn in (vjp, by_hand(), by_hand(outer=1e-3)):
+        body = _gelu_grad_forms(fn)
+        assert "gelu_tanh_grad_f32(" in body and "tanh" not in body.replace("gelu_tanh_grad_f32(", "")
+    for fn in (by_hand(scale=1.001), by_hand(inner=1e-3)):
+        body = _gelu_grad_forms(fn)
+        assert "gelu_tanh_grad_f32(" not in body and "tanh" in body
 
 
 def test_row_kernel_indices_split_into_row_and_column():
