@@ -343,6 +343,9 @@ class Emitter:
         self.vec = 1
         self.given: dict = {}         # var -> fn(idx) -> C name: values the caller computes (a GEMM's sums)
         self.uniform: set = set()     # C names of per-row values (the same on every lane of a row's wave)
+        # whether a row's values are the same on every lane of a wave (a row kernel's; not a GEMM epilogue's,
+        # whose lanes hold different rows)
+        self.rows_uniform = True
         self.recips: dict = {}        # uniform divisor name -> (reciprocal name, range-flag name)
         self.rounded: dict = {}       # name of a bf16-rounded float -> the name it was rounded from
         self._users = None            # readers of each value, built on first need
@@ -448,7 +451,7 @@ class Emitter:
             return self.memo[key]
         name = self._compute(var, idx, ty)
         self.memo[key] = name
-        if idx[0] == "r" and self.rows is not None:
+        if idx[0] == "r" and self.rows is not None and self.rows_uniform:
             self.uniform.add(name)
         return name
 
@@ -1629,7 +1632,7 @@ class GemmEpilogueKernel:
             raise Unfusable(dv, "GEMM epilogue over a row length that is not a multiple of 4")
         ddt = g.types[dv].dtype
         lin = [v for v in loop.inputs if v != dv]
-        # the loop's body, evaluated 4 columns at a time at flat index base + lane of the [m, n] result
+        # the loop's body, evaluated 4 columns at a time at row r, columns c + lane of the [m, n] result
         lk = LoopKernel(g, loop, "KNAME", {v: self.views[v] for v in lin}, self.out_views, self.aliased)
         lk.far = self.far
         em = Emitter(g, loop.nodes, {v: (k, self.views[v]) for k, v in enumerate(lin)})
@@ -1643,16 +1646,19 @@ class GemmEpilogueKernel:
             dnames.append(nm)
 
         def given(idx):
-            if idx[0] == "flat" and len(idx) == 4 and idx[2] == "base":
-                return dnames[idx[3]]
+            if idx[0] == "rc" and len(idx) == 5 and idx[1] == "r" and idx[3] == "c":
+                return dnames[idx[4]]
             raise Unfusable(dv, "the fused loop reads the dot's result at another index")
 
         em.given[dv] = given
+        # elements are indexed by (row r, column c + lane): an operand broadcast along the row (a per-row
+        # statistic) is read at r, not at (r n + c + lane) / n
+        em.rows, em.rows_uniform = (d.m, d.n), False
         stored = [v for v in loop.outputs if not (self.colsum and v == self.colsum[0])]
         per_lane = []
         summed = []
         for lane in range(4):
-            idx = ("flat", f"(base + {lane})", "base", lane)
+            idx = ("rc", "r", f"(c + {lane})", "c", lane)
             per_lane.append([em.value(v, idx) for v in stored])
             if self.colsum:
                 summed.append(em.value(self.colsum[0], idx))
