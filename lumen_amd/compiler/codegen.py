@@ -313,6 +313,16 @@ class View:
         return self.strides == _contig(self.shape) or math.prod(self.shape) <= 1
 
 
+def _block_offset(src, out, start):
+    """The flat offset of a slice [start, start + out) of a row-major ``src`` when the slice is one contiguous
+    block of it (leading dims of size 1, then one partial dim, then full dims), else None."""
+    for d0 in range(len(out) + 1):
+        if all(out[d] == 1 for d in range(d0)) and all(out[d] == src[d] for d in range(d0 + 1, len(out))):
+            st = _contig(src)
+            return sum(s * t for s, t in zip(start, st))
+    return None
+
+
 class Emitter:
     """Evaluates graph values of one kernel at index expressions, writing C statements."""
 
@@ -953,8 +963,15 @@ class Emitter:
                 sm[d] = m[i]
             return self.value(n.inputs[0], ("multi", tuple(sm)))
         if p == "slice":
-            m = self.multi(idx, ty.shape)
             st = n.params["start_indices"]
+            off = _block_offset(ins[0].shape, ty.shape, st)
+            if off is not None and idx[0] == "flat":
+                # one contiguous block of the operand: its flat index is the slice's plus the block's offset
+                if len(idx) == 4 and off % max(1, self.vec) == 0:
+                    nb = f"({idx[2]} + {off}LL)"
+                    return self.value(n.inputs[0], ("flat", f"({nb} + {idx[3]})", nb, idx[3]))
+                return self.value(n.inputs[0], ("flat", f"({idx[1]} + {off}LL)"))
+            m = self.multi(idx, ty.shape)
             return self.value(n.inputs[0], ("multi", tuple(f"({e} + {s}LL)" if s else e for e, s in zip(m, st))))
         if p == "swap_pairs":
             m = self.multi(idx, ty.shape)

@@ -1,7 +1,7 @@
 """Integer and indexing primitives on the GPU, bit for bit against the CPU oracle (the reference
 interpreter's semantics, ``lumen/reference/mod.rs:415-462,738-856``): gathers and take_along_axis with
 indices clamped into the axis, integer scatter_add, argmax/argmin with ties and NaN
-(``functional/functions.py:613-638``), iota/compare masks, dynamic slices with traced starts, integer
+(``functional/functions.py:613-638``), iota/compare masks, static slices (contiguous blocks and windows), dynamic slices with traced starts, integer
 reductions with two's-complement wrap, saturating float-to-int casts and integer bit operations."""
 
 import numpy as np
@@ -42,6 +42,24 @@ def _check(fn, *arrays, kinds=None):
 
 def _bf16(a):
     return D.bf16_bits(np.asarray(a, np.float32))
+
+
+def test_static_slices_in_loops(hip):
+    """Static slices read inside loop kernels, bit for bit: contiguous blocks of their operand (rows of a
+    packed [6144, 2048] bf16 weight gradient, whose flat index is the slice's plus an aligned offset and takes
+    vector loads; a block of a float32 [3, 7, 10] at an offset of 90 elements, off the vector width; one row of
+    an odd-width [5, 33]) and a window that is not one block ([5, 8] rows 1-3, columns 2-5)."""
+    rng = np.random.default_rng(3)
+    g = _bf16(rng.standard_normal((6144, 2048)))
+    w = _bf16(rng.standard_normal((2048, 2048)))
+    got = _check(lambda g, w: w - prims.slice(g, [4096, 0], [6144, 2048]) * 0.25, g, w, kinds=["loop"])
+    assert got[0].shape == (2048, 2048)
+    x = rng.standard_normal((3, 7, 10)).astype(np.float32)
+    _check(lambda x: prims.slice(x, [1, 2, 0], [2, 5, 10]) * 3.0 + 1.0, x)
+    y = rng.standard_normal((5, 33)).astype(np.float32)
+    _check(lambda y: prims.slice(y, [2, 0], [3, 33]) * 2.0 - 1.0, y)
+    z = rng.standard_normal((5, 8)).astype(np.float32)
+    _check(lambda z: prims.slice(z, [1, 2], [4, 6]) - 0.5, z)
 
 
 def test_embedding_gather_clamps_ids(hip):
