@@ -34,6 +34,7 @@ class Compiled:
         self._plans = {}
         self._latest = None
         self._graphs = {}  # id(plan) -> captured graphs by the addresses they read in place (empty: warm)
+        self._scalars = collections.OrderedDict()  # (device, float64 bits) -> device float64 holding it
 
     def _target(self, args):
         if self._device is not None:
@@ -84,6 +85,24 @@ class Compiled:
     # copy would cost as much as a memory-bound plan itself.
     DIRECT_BYTES = 1 << 20
     GRAPHS_PER_PLAN = 8
+    # runtime scalars kept on the device between calls (a learning rate is the same every step)
+    SCALARS_KEPT = 64
+
+    def _device_scalar(self, target, value):
+        """A device float64 holding ``value``, uploaded once per (device, value) and kept: the upload is a
+        synchronous host-to-device copy, which would otherwise make every call wait for the previous call's
+        kernels before it could queue its own. Evicted entries may still be read by queued kernels; their
+        memory is only reused by work queued after them on the device's one stream."""
+        key = (target, np.float64(value).tobytes())
+        t = self._scalars.get(key)
+        if t is None:
+            t = Tensor("float64", (), "cpu", host=np.array(value, np.float64)).to(device=target)
+            self._scalars[key] = t
+            while len(self._scalars) > self.SCALARS_KEPT:
+                self._scalars.popitem(last=False)
+        else:
+            self._scalars.move_to_end(key)
+        return t
     # Plans of fewer native steps run uncaptured: launching a graph costs the host ~40 us, launching a step
     # ~3 us, so a short plan (a fused elementwise chain is one kernel) loses time to the graph.
     GRAPH_MIN_STEPS = 16
@@ -159,7 +178,7 @@ class Compiled:
                     keep.append(t)
                     ptrs.append(t.data_ptr())
                 elif kind == "scalar":
-                    t = Tensor("float64", (), "cpu", host=np.array(scalars[k], np.float64)).to(device=target)
+                    t = self._device_scalar(target, scalars[k])
                     keep.append(t)
                     ptrs.append(t.data_ptr())
                 else:

@@ -193,6 +193,33 @@ def test_hip_graph_replays_match_uncaptured_runs(hip, monkeypatch):
     assert np.array_equal(losses[True][4], losses[False][4])
 
 
+def test_runtime_scalars_are_uploaded_once_per_value(hip, monkeypatch):
+    """A runtime scalar is uploaded once per value and kept on the device (the upload synchronizes, so a
+    per-call upload would stall every call on the previous one): calls alternating two values keep two
+    device copies, captured and replayed, each call equal bit for bit to the same call run uncaptured."""
+    import lumen_amd.functional as F
+    from lumen_amd.graph.compiled import Compiled
+
+    monkeypatch.setattr(Compiled, "GRAPH_MIN_STEPS", 1)
+
+    def fn(x, s):
+        return F.relu(x.float() * s - 0.25)
+
+    rng = np.random.default_rng(11)
+    x = L.tensor(D.bf16_to_f32(D.bf16_bits(rng.standard_normal((256, 512)))), "bfloat16")
+    values = [0.5, 1.5, 0.5, 1.5, 0.5, 1.5]
+    with L.config.compiler.patch(hip_graphs=True):
+        f = L.compile(fn, device="hip")
+        got = [np.asarray(L.to_numpy(f(x, v)), np.float32) for v in values]
+        assert len(f._scalars) == 2 and len(f._graphs[id(f.plan)]) == 1
+    with L.config.compiler.patch(hip_graphs=False):
+        u = L.compile(fn, device="hip")
+        want = [np.asarray(L.to_numpy(u(x, v)), np.float32) for v in values]
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(g_, w_)
+    assert not np.array_equal(got[0], got[1])
+
+
 @pytest.mark.parametrize("cfg_name", ["TINY", "CONFIG4"])
 def test_weights_updated_in_place_match_copied_updates(hip, cfg_name):
     """Every weight the training step assigns is computed over its old value (no workspace copy, no copy
